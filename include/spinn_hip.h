@@ -1,0 +1,154 @@
+/*
+ * spinn_hip.h - C ABI of the HIP (gfx950) compute layer.
+ *
+ * Plain C: plain pointers, sizes and small descriptor structs, no HIP or torch
+ * types (a hipStream_t is passed as void*, NULL = the null stream). Every
+ * pointer argument of a compute entry point is a DEVICE address. Entry points
+ * return 0 on success or a negative SPINN_HIP_E* code; they never allocate
+ * device memory: scratch comes in through `workspace`, sized by the matching
+ * *_workspace_size() query, and pre-laid-out weights through `packed_w`.
+ *
+ * Which reference interface each entry point replaces is noted on it.
+ */
+#ifndef SPINN_AMD_HIP_H
+#define SPINN_AMD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPINN_HIP_OK 0
+#define SPINN_HIP_EINVAL (-1)      /* bad arity / shape / argument (reference ops return -1) */
+#define SPINN_HIP_EUNSUPPORTED (-2) /* valid request this layer does not implement */
+#define SPINN_HIP_EWORKSPACE (-3)   /* workspace missing or too small */
+#define SPINN_HIP_ERUNTIME (-100)   /* HIP runtime error: code = -100 - hipError_t */
+
+/* Convolution algorithms. AUTO picks per shape (see spinn_hip_conv_select_algo). */
+enum {
+    SPINN_CONV_ALGO_AUTO = 0,
+    SPINN_CONV_ALGO_IMPLICIT_GEMM = 1, /* im2col fused into the tile load; 1x1 s1 p0 reads X directly */
+    SPINN_CONV_ALGO_WINOGRAD = 2,      /* F(2x2,3x3), 3x3 s1 group 1 only; needs packed_w */
+    SPINN_CONV_ALGO_DIRECT = 3         /* grouped / depthwise direct convolution */
+};
+
+/*
+ * Conv2d + fused epilogue, NCHW fp32.
+ *   y[n,oc,oh,ow] = post( sum_{c,kh,kw} w[oc,c,kh,kw] * x[n, g*C/g + c, oh*sh-ph+kh, ow*sw-pw+kw] )
+ *   post(v): v += bias[oc] (if bias); if act in {ADD, ADD_RELU}: v += residual[n,oc,oh,ow];
+ *            if act in {RELU, ADD_RELU}: v = max(v,0); else if act == SILU: v = v/(1+exp(-v)).
+ * Only the begin pads are used and dilations are ignored, as in
+ * SPINN/run_time/ops/conv/conv2d.c:124-142; the epilogue order is
+ * SPINN/run_time/ops/mm/gemm_kernel.c:316-338 with the codes of SPINN/graph_opt.h:31-36.
+ */
+typedef struct {
+    int32_t n, c, h, w;     /* input */
+    int32_t oc, oh, ow;     /* output */
+    int32_t kh, kw;         /* kernel */
+    int32_t sh, sw;         /* strides */
+    int32_t ph, pw;         /* begin pads */
+    int32_t group;          /* C and OC divisible by group */
+    int32_t act;            /* SPINN_ACT_* */
+    int32_t algo;           /* SPINN_CONV_ALGO_* */
+    int32_t reserved;
+} SpinnHipConvDesc;
+
+/* Replaces the arithmetic of op_conv2d (SPINN/run_time/ops/conv/conv2d.c:92-232):
+ * im2col (:14-79) + sgemm_nn_packed_a / sgemm_nn (SPINN/run_time/ops/mm/gemm_kernel.c:304-339,497-590),
+ * the Winograd path (SPINN/run_time/ops/conv/winograd.c:96-210) and the grouped loop (:178-227).
+ * bias may be NULL; residual must be non-NULL iff act is ADD or ADD_RELU. */
+int spinn_hip_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed_w,
+                   const float *bias, const float *residual, float *y, void *workspace,
+                   size_t workspace_bytes, void *stream);
+
+/* Algorithm AUTO would run for this shape (never returns AUTO). */
+int spinn_hip_conv_select_algo(const SpinnHipConvDesc *d);
+/* Device scratch bytes spinn_hip_conv needs for this descriptor (0 = none). */
+size_t spinn_hip_conv_workspace_size(const SpinnHipConvDesc *d);
+/* Bytes of pre-laid-out weights the selected algorithm needs (0 = reads w directly).
+ * Replaces sgemm_pack_a_offline / winograd_pack_weight
+ * (SPINN/run_time/ops/mm/gemm_kernel.c:346-369, SPINN/run_time/ops/conv/winograd.c:82-94). */
+size_t spinn_hip_conv_packed_size(const SpinnHipConvDesc *d);
+/* Fill `packed` (spinn_hip_conv_packed_size bytes) from w [OC, C/g, KH, KW]. */
+int spinn_hip_conv_pack_weights(const SpinnHipConvDesc *d, const float *w, float *packed, void *stream);
+
+/*
+ * Gemm / MatMul, fp32 row-major.
+ *   y[b] = alpha * op(A[b]) * op(B[b]) + beta * C    (op = transpose when trans_*)
+ * A[b] is M x K (K x M when trans_a), B[b] is K x N (N x K when trans_b).
+ * c_mode: 0 = no C, 1 = C is a vector [N] broadcast over rows, 2 = C is [M, N].
+ * batch > 1 steps A, B and Y by stride_a / stride_b / stride_y elements
+ * (stride_b = 0 broadcasts one B over the batch). C is never batched.
+ * alpha scales only the product (the reference also scales the C prefill when
+ * M > 1, SPINN/run_time/ops/mm/gemm_kernel.c:298-301; parity is held to the
+ * operator's definition, which the reference configs hit with alpha = 1).
+ */
+typedef struct {
+    int32_t m, n, k;
+    int32_t trans_a, trans_b;
+    int32_t c_mode;
+    float alpha, beta;
+    int32_t batch;
+    int32_t reserved;
+    int64_t stride_a, stride_b, stride_y;
+} SpinnHipGemmDesc;
+
+/* Replaces op_gemm (SPINN/run_time/ops/mm/gemm.c:7-78) and op_matmul
+ * (SPINN/run_time/ops/mm/matmul.c:6-62) over sgemm_tiled (gemm_kernel.c:206-302). */
+int spinn_hip_gemm(const SpinnHipGemmDesc *d, const float *a, const float *b, const float *c, float *y,
+                   void *workspace, size_t workspace_bytes, void *stream);
+size_t spinn_hip_gemm_workspace_size(const SpinnHipGemmDesc *d);
+
+/* ---- glue operators around the conv/GEMM path ---- */
+
+typedef struct {
+    int32_t n, c, h, w;
+    int32_t oh, ow;
+    int32_t kh, kw, sh, sw, ph, pw;
+} SpinnHipPoolDesc;
+
+/* MaxPool2d; a window with no valid tap yields -1e30 (SPINN/run_time/ops/pool/maxpool.c:5-49). */
+int spinn_hip_maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, void *stream);
+
+/* Mean over the middle axis of an [outer, dim, inner] view
+ * (SPINN/run_time/ops/reduce/reduce_mean.c:62-75; GlobalAveragePool is outer=N*C, dim=H*W, inner=1,
+ * SPINN/run_time/ops/pool/global_avg_pool.c:4-28). */
+int spinn_hip_reduce_mean(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y,
+                          void *stream);
+
+/* Device-to-device copy for Reshape / Flatten / Identity
+ * (SPINN/run_time/ops/shape/reshape.c:6-14, SPINN/run_time/ops/tensor/flatten.c:3-8). */
+int spinn_hip_copy(void *dst, const void *src, size_t bytes, void *stream);
+
+/* ---- device, memory, stream, event and graph plumbing for the host runtime ---- */
+
+int spinn_hip_init(int device);
+int spinn_hip_device_count(int *count);
+int spinn_hip_malloc(void **ptr, size_t bytes);
+int spinn_hip_free(void *ptr);
+int spinn_hip_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+int spinn_hip_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+/* Fill `bytes` (multiple of 4) with a 32-bit pattern using a kernel (graph-safe, no memset node). */
+int spinn_hip_fill_u32(void *dst, uint32_t value, size_t bytes, void *stream);
+int spinn_hip_stream_create(void **stream);
+int spinn_hip_stream_destroy(void *stream);
+int spinn_hip_stream_sync(void *stream);
+int spinn_hip_event_create(void **event);
+int spinn_hip_event_destroy(void *event);
+int spinn_hip_event_record(void *event, void *stream);
+int spinn_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+int spinn_hip_graph_capture_begin(void *stream);
+int spinn_hip_graph_capture_end(void *stream, void **graph_exec);
+int spinn_hip_graph_launch(void *graph_exec, void *stream);
+int spinn_hip_graph_destroy(void *graph_exec);
+const char *spinn_hip_error_string(int code);
+
+/* Library version / build identification string. */
+const char *spinn_hip_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPINN_AMD_HIP_H */

@@ -1,0 +1,194 @@
+"""ORACLE (test infrastructure only): ctypes access to the CPU restatement
+(liboracle.so, built from spinn_cpu.c + cpu_runtime.c) and, where it was
+built, to the reference's own CPU runtime (_ref/libspinn_ref.so).
+
+Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use
+this module, and only as the checker / the timed CPU baseline.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+REF_LIB = HERE / "_ref" / "libspinn_ref.so"
+REF_SRC = Path("/root/reference/SPINN")
+
+_FP = C.POINTER(C.c_float)
+_DP = C.POINTER(C.c_double)
+
+
+class OracleConv(C.Structure):
+    _fields_ = [(n, C.c_int) for n in (
+        "n", "c", "h", "w", "oc", "oh", "ow", "kh", "kw", "sh", "sw", "ph", "pw", "group", "act")]
+
+
+def build(ref: bool = True) -> None:
+    """Compile liboracle.so and, when the reference sources are present, _ref/libspinn_ref.so."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    if ref and REF_SRC.exists():
+        subprocess.run(["make", "-s", "-C", str(HERE), "-j8", "ref"], check=True)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build(ref=False)
+        L = C.CDLL(str(LIB))
+        L.oracle_conv2d.argtypes = [C.POINTER(OracleConv), _FP, _FP, _FP, _FP, _FP]
+        L.oracle_conv2d_f64.argtypes = [C.POINTER(OracleConv), _FP, _FP, _FP, _FP, _DP]
+        L.oracle_winograd.argtypes = [C.POINTER(OracleConv), _FP, _FP, _FP, _FP, _FP]
+        L.oracle_gemm.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float, _FP, _FP, _FP,
+                                  C.c_int, _FP]
+        L.oracle_gemm_f64.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_double, _FP, _FP,
+                                      _FP, C.c_int, _DP]
+        L.oracle_matmul.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, _FP, _FP, _FP]
+        L.oracle_maxpool.argtypes = [C.c_int] * 12 + [_FP, _FP]
+        L.oracle_reduce_mean.argtypes = [C.c_long, C.c_long, C.c_long, _FP, _FP]
+        L.oracle_set_as_shipped.argtypes = [C.c_int]
+        L.oracle_set_num_threads.argtypes = [C.c_int]
+        L.oracle_model_load.restype = C.c_void_p
+        L.oracle_model_load.argtypes = [C.c_char_p]
+        L.oracle_model_run.argtypes = [C.c_void_p, _FP, _FP]
+        L.oracle_model_free.argtypes = [C.c_void_p]
+        L.oracle_model_tensor.restype = C.c_long
+        L.oracle_model_tensor.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]
+        L.oracle_model_set_winograd.argtypes = [C.c_void_p, C.c_int]
+        L.oracle_model_num_nodes.argtypes = [C.c_void_p]
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_FP)
+
+
+def conv_desc(n, c, h, w, oc, kh, kw, sh=1, sw=1, ph=0, pw=0, group=1, act=0, oh=None, ow=None) -> OracleConv:
+    if oh is None:
+        oh = (h + 2 * ph - kh) // sh + 1
+    if ow is None:
+        ow = (w + 2 * pw - kw) // sw + 1
+    return OracleConv(n, c, h, w, oc, oh, ow, kh, kw, sh, sw, ph, pw, group, act)
+
+
+def conv2d(d: OracleConv, x, w, bias=None, res=None, as_shipped=False) -> np.ndarray:
+    """Restated SPINN conv (float32, im2col + packed 6x16 GEMM + epilogue)."""
+    y = np.zeros((d.n, d.oc, d.oh, d.ow), np.float32)
+    L = lib()
+    L.oracle_set_as_shipped(1 if as_shipped else 0)
+    try:
+        rc = L.oracle_conv2d(C.byref(d), _f(x), _f(w), _f(bias), _f(res), _f(y))
+    finally:
+        L.oracle_set_as_shipped(0)
+    assert rc == 0
+    return y
+
+
+def conv2d_f64(d: OracleConv, x, w, bias=None, res=None) -> np.ndarray:
+    """Closed-form direct convolution accumulated in float64, with the epilogue."""
+    y = np.zeros((d.n, d.oc, d.oh, d.ow), np.float64)
+    rc = lib().oracle_conv2d_f64(C.byref(d), _f(x), _f(w), _f(bias), _f(res), y.ctypes.data_as(_DP))
+    assert rc == 0
+    return y
+
+
+def winograd(d: OracleConv, x, w, bias=None, res=None) -> np.ndarray:
+    y = np.zeros((d.n, d.oc, d.oh, d.ow), np.float32)
+    rc = lib().oracle_winograd(C.byref(d), _f(x), _f(w), _f(bias), _f(res), _f(y))
+    assert rc == 0
+    return y
+
+
+def gemm(a, b, c=None, alpha=1.0, beta=1.0, trans_a=0, trans_b=0) -> np.ndarray:
+    m = a.shape[1] if trans_a else a.shape[0]
+    k = a.shape[0] if trans_a else a.shape[1]
+    n = b.shape[0] if trans_b else b.shape[1]
+    y = np.zeros((m, n), np.float32)
+    rc = lib().oracle_gemm(m, n, k, trans_a, trans_b, alpha, beta, _f(a), _f(b), _f(c), 0 if c is None else c.size,
+                           _f(y))
+    assert rc == 0
+    return y
+
+
+def gemm_f64(a, b, c=None, alpha=1.0, beta=1.0, trans_a=0, trans_b=0) -> np.ndarray:
+    m = a.shape[1] if trans_a else a.shape[0]
+    k = a.shape[0] if trans_a else a.shape[1]
+    n = b.shape[0] if trans_b else b.shape[1]
+    y = np.zeros((m, n), np.float64)
+    rc = lib().oracle_gemm_f64(m, n, k, trans_a, trans_b, alpha, beta, _f(a), _f(b), _f(c),
+                               0 if c is None else c.size, y.ctypes.data_as(_DP))
+    assert rc == 0
+    return y
+
+
+def matmul(a, b) -> np.ndarray:
+    batch = int(np.prod(a.shape[:-2])) if a.ndim > 2 else 1
+    m, k = a.shape[-2:]
+    n = b.shape[-1]
+    y = np.zeros(a.shape[:-2] + (m, n), np.float32)
+    rc = lib().oracle_matmul(batch, m, n, k, _f(a), _f(b), _f(y))
+    assert rc == 0
+    return y
+
+
+def maxpool(x, oh, ow, kh, kw, sh, sw, ph, pw) -> np.ndarray:
+    n, c, h, w = x.shape
+    y = np.zeros((n, c, oh, ow), np.float32)
+    lib().oracle_maxpool(n, c, h, w, oh, ow, kh, kw, sh, sw, ph, pw, _f(x), _f(y))
+    return y
+
+
+def reduce_mean(x, outer, dim, inner) -> np.ndarray:
+    y = np.zeros(outer * inner, np.float32)
+    lib().oracle_reduce_mean(outer, dim, inner, _f(np.ascontiguousarray(x, np.float32)), _f(y))
+    return y
+
+
+def set_threads(n: int) -> None:
+    lib().oracle_set_num_threads(int(n))
+
+
+class Model:
+    """An ENNF model run on the CPU by the restated operators."""
+
+    def __init__(self, path, winograd: bool = False):
+        self._m = lib().oracle_model_load(str(path).encode())
+        if not self._m:
+            raise RuntimeError(f"oracle could not load {path}")
+        lib().oracle_model_set_winograd(self._m, 1 if winograd else 0)
+
+    def run(self, x: np.ndarray, out_shape) -> np.ndarray:
+        y = np.zeros(out_shape, np.float32)
+        rc = lib().oracle_model_run(self._m, _f(np.ascontiguousarray(x, np.float32)), _f(y))
+        if rc != 0:
+            raise RuntimeError(f"oracle model run failed: {rc}")
+        return y
+
+    def tensor(self, tid: int, shape, dtype=np.float32) -> np.ndarray:
+        a = np.zeros(shape, dtype)
+        got = lib().oracle_model_tensor(self._m, tid, a.ctypes.data, a.nbytes)
+        if got < 0:
+            raise KeyError(tid)
+        return a
+
+    def close(self):
+        if self._m:
+            lib().oracle_model_free(self._m)
+            self._m = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,279 @@
+// api.hip - the extern "C" entry points of include/spinn_hip.h: argument
+// validation, algorithm selection, and the device/stream/graph plumbing the
+// host runtime uses. All compute goes to the kernels in the other units.
+#include "spinn_hip_internal.h"
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
+namespace spinn {
+
+int device_cu_count() {
+    static int cached[64];
+    static std::once_flag once[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::call_once(once[dev], [dev]() {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+        cached[dev] = v;
+    });
+    return cached[dev];
+}
+
+static int env_winograd() {
+    // SPINN_WINOGRAD=1 sends eligible 3x3 stride-1 convs to Winograd under AUTO,
+    // 0 keeps them on the implicit GEMM; unset = per-shape choice.
+    static int v = [] {
+        const char *e = std::getenv("SPINN_WINOGRAD");
+        if (!e || !*e) return -1;
+        return e[0] == '0' ? 0 : 1;
+    }();
+    return v;
+}
+
+static bool winograd_pays(const SpinnHipConvDesc *d) {
+    // Winograd cuts GEMM flops 2.25x but moves V (4x the input) and M (4x the
+    // output) through memory; it wins once the GEMM is deep enough.
+    return d->c >= 256 && d->oc >= 256;
+}
+
+static int select_algo(const SpinnHipConvDesc *d) {
+    if (d->algo != SPINN_CONV_ALGO_AUTO) return d->algo;
+    const int Cg = d->c / d->group;
+    const int OCg = d->oc / d->group;
+    if (d->group > 1 && (Cg < 8 || OCg < 8)) return SPINN_CONV_ALGO_DIRECT;
+    if (winograd_eligible(d)) {
+        const int w = env_winograd();
+        if (w == 1 || (w < 0 && winograd_pays(d))) return SPINN_CONV_ALGO_WINOGRAD;
+    }
+    return SPINN_CONV_ALGO_IMPLICIT_GEMM;
+}
+
+static bool conv_desc_ok(const SpinnHipConvDesc *d) {
+    if (!d) return false;
+    if (d->n <= 0 || d->c <= 0 || d->h <= 0 || d->w <= 0 || d->oc <= 0 || d->oh <= 0 || d->ow <= 0) return false;
+    if (d->kh <= 0 || d->kw <= 0 || d->sh <= 0 || d->sw <= 0 || d->ph < 0 || d->pw < 0) return false;
+    if (d->group <= 0 || d->c % d->group != 0 || d->oc % d->group != 0) return false;
+    if (d->act < 0 || d->act > 5) return false;
+    // 32-bit tile indexing: pixels per launch and elements per image plane
+    const int64_t ntot = (int64_t)d->n * d->oh * d->ow;
+    if (ntot > (int64_t)INT32_MAX || (int64_t)d->c * d->kh * d->kw > (int64_t)INT32_MAX) return false;
+    return true;
+}
+
+} // namespace spinn
+
+using namespace spinn;
+
+extern "C" {
+
+int spinn_hip_conv_select_algo(const SpinnHipConvDesc *d) {
+    if (!conv_desc_ok(d)) return SPINN_HIP_EINVAL;
+    return select_algo(d);
+}
+
+size_t spinn_hip_conv_workspace_size(const SpinnHipConvDesc *d) {
+    if (!conv_desc_ok(d)) return 0;
+    switch (select_algo(d)) {
+    case SPINN_CONV_ALGO_IMPLICIT_GEMM: return igemm_workspace_bytes(d);
+    case SPINN_CONV_ALGO_WINOGRAD: return winograd_eligible(d) ? winograd_workspace_bytes(d) : 0;
+    default: return 0;
+    }
+}
+
+size_t spinn_hip_conv_packed_size(const SpinnHipConvDesc *d) {
+    if (!conv_desc_ok(d)) return 0;
+    switch (select_algo(d)) {
+    case SPINN_CONV_ALGO_IMPLICIT_GEMM: return (size_t)igemm_packed_floats(d) * sizeof(float);
+    case SPINN_CONV_ALGO_WINOGRAD: return winograd_eligible(d) ? (size_t)winograd_packed_floats(d) * sizeof(float) : 0;
+    default: return 0;
+    }
+}
+
+int spinn_hip_conv_pack_weights(const SpinnHipConvDesc *d, const float *w, float *packed, void *stream) {
+    if (!conv_desc_ok(d) || !w || !packed) return SPINN_HIP_EINVAL;
+    hipStream_t st = (hipStream_t)stream;
+    switch (select_algo(d)) {
+    case SPINN_CONV_ALGO_IMPLICIT_GEMM: return igemm_pack(d, w, packed, st);
+    case SPINN_CONV_ALGO_WINOGRAD:
+        if (!winograd_eligible(d)) return SPINN_HIP_EUNSUPPORTED;
+        return winograd_pack(d, w, packed, st);
+    default: return SPINN_HIP_OK; // reads w directly
+    }
+}
+
+int spinn_hip_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed_w,
+                   const float *bias, const float *residual, float *y, void *workspace, size_t workspace_bytes,
+                   void *stream) {
+    if (!conv_desc_ok(d) || !x || !y) return SPINN_HIP_EINVAL;
+    const bool has_res = d->act == SPINN_ACT_ADD || d->act == SPINN_ACT_ADD_RELU;
+    if (has_res != (residual != nullptr)) return SPINN_HIP_EINVAL;
+    hipStream_t st = (hipStream_t)stream;
+    switch (select_algo(d)) {
+    case SPINN_CONV_ALGO_IMPLICIT_GEMM:
+        if (!packed_w) return SPINN_HIP_EINVAL;
+        return igemm_conv(d, x, packed_w, bias, residual, y, workspace, workspace_bytes, st);
+    case SPINN_CONV_ALGO_WINOGRAD:
+        if (!winograd_eligible(d)) return SPINN_HIP_EUNSUPPORTED;
+        if (!packed_w) return SPINN_HIP_EINVAL;
+        return winograd_conv(d, x, packed_w, bias, residual, y, workspace, workspace_bytes, st);
+    case SPINN_CONV_ALGO_DIRECT:
+        if (!w) return SPINN_HIP_EINVAL;
+        return direct_conv(d, x, w, bias, residual, y, st);
+    default: return SPINN_HIP_EINVAL;
+    }
+}
+
+static bool gemm_desc_ok(const SpinnHipGemmDesc *d) {
+    if (!d) return false;
+    if (d->m <= 0 || d->n <= 0 || d->k <= 0) return false;
+    if (d->c_mode < 0 || d->c_mode > 2) return false;
+    if (d->batch < 0) return false;
+    if (d->batch > 1 && (d->stride_a < 0 || d->stride_b < 0 || d->stride_y <= 0)) return false;
+    return true;
+}
+
+size_t spinn_hip_gemm_workspace_size(const SpinnHipGemmDesc *d) {
+    if (!gemm_desc_ok(d)) return 0;
+    return gemm_workspace_bytes(d);
+}
+
+int spinn_hip_gemm(const SpinnHipGemmDesc *d, const float *a, const float *b, const float *c, float *y,
+                   void *workspace, size_t workspace_bytes, void *stream) {
+    if (!gemm_desc_ok(d) || !a || !b || !y) return SPINN_HIP_EINVAL;
+    if (d->c_mode != 0 && !c) return SPINN_HIP_EINVAL;
+    return gemm_run(d, a, b, c, y, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int spinn_hip_maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, void *stream) {
+    if (!d || !x || !y || d->n <= 0 || d->c <= 0 || d->h <= 0 || d->w <= 0 || d->oh <= 0 || d->ow <= 0 ||
+        d->kh <= 0 || d->kw <= 0 || d->sh <= 0 || d->sw <= 0)
+        return SPINN_HIP_EINVAL;
+    return maxpool2d(d, x, y, (hipStream_t)stream);
+}
+
+int spinn_hip_reduce_mean(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, void *stream) {
+    if (!x || !y || outer <= 0 || dim <= 0 || inner <= 0) return SPINN_HIP_EINVAL;
+    return reduce_mean(outer, dim, inner, x, y, (hipStream_t)stream);
+}
+
+int spinn_hip_copy(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0 || dst == src) return SPINN_HIP_OK;
+    if (!dst || !src) return SPINN_HIP_EINVAL;
+    return hip_code(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+}
+
+int spinn_hip_init(int device) { return hip_code(hipSetDevice(device)); }
+
+int spinn_hip_device_count(int *count) {
+    if (!count) return SPINN_HIP_EINVAL;
+    return hip_code(hipGetDeviceCount(count));
+}
+
+int spinn_hip_malloc(void **ptr, size_t bytes) {
+    if (!ptr) return SPINN_HIP_EINVAL;
+    *ptr = nullptr;
+    if (bytes == 0) return SPINN_HIP_OK;
+    return hip_code(hipMalloc(ptr, bytes));
+}
+
+int spinn_hip_free(void *ptr) { return ptr ? hip_code(hipFree(ptr)) : SPINN_HIP_OK; }
+
+int spinn_hip_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return SPINN_HIP_OK;
+    if (!dst || !src) return SPINN_HIP_EINVAL;
+    return hip_code(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+}
+
+int spinn_hip_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream) {
+    if (bytes == 0) return SPINN_HIP_OK;
+    if (!dst || !src) return SPINN_HIP_EINVAL;
+    return hip_code(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+}
+
+int spinn_hip_fill_u32(void *dst, uint32_t value, size_t bytes, void *stream) {
+    if (bytes % 4 != 0) return SPINN_HIP_EINVAL;
+    if (bytes == 0) return SPINN_HIP_OK;
+    if (!dst) return SPINN_HIP_EINVAL;
+    return fill_u32(dst, value, bytes, (hipStream_t)stream);
+}
+
+int spinn_hip_stream_create(void **stream) {
+    if (!stream) return SPINN_HIP_EINVAL;
+    hipStream_t s = nullptr;
+    int rc = hip_code(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = rc ? nullptr : (void *)s;
+    return rc;
+}
+
+int spinn_hip_stream_destroy(void *stream) {
+    return stream ? hip_code(hipStreamDestroy((hipStream_t)stream)) : SPINN_HIP_OK;
+}
+
+int spinn_hip_stream_sync(void *stream) { return hip_code(hipStreamSynchronize((hipStream_t)stream)); }
+
+int spinn_hip_event_create(void **event) {
+    if (!event) return SPINN_HIP_EINVAL;
+    hipEvent_t e = nullptr;
+    int rc = hip_code(hipEventCreate(&e));
+    *event = rc ? nullptr : (void *)e;
+    return rc;
+}
+
+int spinn_hip_event_destroy(void *event) {
+    return event ? hip_code(hipEventDestroy((hipEvent_t)event)) : SPINN_HIP_OK;
+}
+
+int spinn_hip_event_record(void *event, void *stream) {
+    if (!event) return SPINN_HIP_EINVAL;
+    return hip_code(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+}
+
+int spinn_hip_event_elapsed_ms(void *start, void *stop, float *ms) {
+    if (!start || !stop || !ms) return SPINN_HIP_EINVAL;
+    int rc = hip_code(hipEventSynchronize((hipEvent_t)stop));
+    if (rc) return rc;
+    return hip_code(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+}
+
+int spinn_hip_graph_capture_begin(void *stream) {
+    if (!stream) return SPINN_HIP_EINVAL; // the null stream cannot be captured
+    return hip_code(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+}
+
+int spinn_hip_graph_capture_end(void *stream, void **graph_exec) {
+    if (!stream || !graph_exec) return SPINN_HIP_EINVAL;
+    *graph_exec = nullptr;
+    hipGraph_t g = nullptr;
+    int rc = hip_code(hipStreamEndCapture((hipStream_t)stream, &g));
+    if (rc) return rc;
+    hipGraphExec_t ex = nullptr;
+    rc = hip_code(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0));
+    (void)hipGraphDestroy(g);
+    if (rc) return rc;
+    *graph_exec = (void *)ex;
+    return SPINN_HIP_OK;
+}
+
+int spinn_hip_graph_launch(void *graph_exec, void *stream) {
+    if (!graph_exec) return SPINN_HIP_EINVAL;
+    return hip_code(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream));
+}
+
+int spinn_hip_graph_destroy(void *graph_exec) {
+    return graph_exec ? hip_code(hipGraphExecDestroy((hipGraphExec_t)graph_exec)) : SPINN_HIP_OK;
+}
+
+const char *spinn_hip_error_string(int code) {
+    if (code == SPINN_HIP_OK) return "ok";
+    if (code == SPINN_HIP_EINVAL) return "invalid argument";
+    if (code == SPINN_HIP_EUNSUPPORTED) return "unsupported configuration";
+    if (code == SPINN_HIP_EWORKSPACE) return "workspace missing or too small";
+    if (code <= SPINN_HIP_ERUNTIME) return hipGetErrorString((hipError_t)(SPINN_HIP_ERUNTIME - code));
+    return "unknown error";
+}
+
+const char *spinn_hip_version(void) { return "spinn_amd 0.1 gfx950 fp32-mfma"; }
+
+} // extern "C"

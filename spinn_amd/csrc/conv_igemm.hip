@@ -1,0 +1,291 @@
+// conv_gemm.hip - implicit-GEMM convolution and Gemm/MatMul on fp32 MFMA.
+//
+// Convolution as GEMM, SPINN orientation (SPINN/run_time/ops/conv/conv2d.c:184-225):
+//   M = OC/g (output channels), N = batch*OH*OW (output pixels, batch folded
+//   into N instead of the reference's per-image loop), K = C/g*KH*KW (taps).
+// The A operand is the weight matrix re-laid out once as W^T [K][OCg padded to 4]
+// (the plan-time counterpart of sgemm_pack_a_offline, gemm_kernel.c:346-369);
+// the B operand is never materialised: each K slice of im2col is gathered from
+// NCHW input straight into LDS (no column buffer, unlike conv2d.c:172-193).
+// The bias / residual / ReLU / SiLU epilogue (gemm_kernel.c:316-338) is applied
+// to the accumulators before the only store of the output.
+//
+// When the tile grid is too small to fill 256 CUs, K is split over blockIdx.z:
+// each split writes raw partial sums to the workspace and a reduction kernel
+// sums them in a fixed order and applies the epilogue (deterministic).
+#include "mfma_core.h"
+#include "spinn_hip_internal.h"
+#include <type_traits>
+
+namespace spinn {
+
+struct ConvKArgs {
+    const float *wpk;  // packed W^T: [group][K][ldw]
+    int64_t wpk_group_stride;
+    int ldw;
+    int M, K;          // per group
+    ConvGeom geom;
+    float *y;
+    const float *bias;
+    const float *res;
+    int act;
+    int OC, OHW;
+    float *ws;         // split-K partials [split][OC][ntot]
+    int k_chunk;       // K per split (multiple of kBK)
+};
+
+template <int BM, int BN, int BK, class BLoader, bool SPLIT>
+__global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
+    using WT = WaveTiling<BM, BN>;
+    constexpr int SA = LdsPad<BM>::stride;
+    constexpr int SB = LdsPad<BN>::stride;
+    __shared__ __attribute__((aligned(16))) float As[2][BK * SA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * SB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = (wave >> 1) * WT::WM;
+    const int wn0 = (wave & 1) * WT::WN;
+    const int n0 = blockIdx.x * BN;
+    const int m0 = blockIdx.y * BM;
+    const int z = blockIdx.z;
+    const int group = SPLIT ? 0 : z;
+    const int k_begin = SPLIT ? z * a.k_chunk : 0;
+    const int k_end = SPLIT ? min(a.K, k_begin + a.k_chunk) : a.K;
+
+    KMajorLoader<BM, BK, true> al;
+    al.src = a.wpk + group * a.wpk_group_stride + m0;
+    al.ld = a.ldw;
+    al.t_valid = a.ldw - m0;
+    al.k_end = k_end;
+    BLoader bl;
+    bl.init(a.geom, n0, group, tid, k_end);
+
+    f32x16 acc[WT::TM][WT::TN];
+#pragma unroll
+    for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < WT::TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nslices = (k_end - k_begin + BK - 1) / BK;
+    if (nslices > 0) {
+        al.fetch(k_begin, tid);
+        bl.fetch(k_begin, tid);
+        al.commit(As[0], tid);
+        bl.commit(Bs[0], tid);
+        __syncthreads();
+        for (int s = 0; s < nslices; ++s) {
+            const int cur = s & 1;
+            const bool more = s + 1 < nslices;
+            if (more) {
+                al.fetch(k_begin + (s + 1) * BK, tid);
+                bl.fetch(k_begin + (s + 1) * BK, tid);
+            }
+            mma_slice<BM, BN, BK>(As[cur], Bs[cur], acc, wm0, wn0, lane);
+            if (more) {
+                al.commit(As[cur ^ 1], tid);
+                bl.commit(Bs[cur ^ 1], tid);
+            }
+            __syncthreads();
+        }
+    }
+
+    // Epilogue: lane owns column jcol = n0 + wn0 + j*32 + lane%32 and rows
+    // m0 + wm0 + i*32 + 8*(r/4) + 4*(lane/32) + r%4.
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+    const int ntot = a.geom.ntot;
+#pragma unroll
+    for (int j = 0; j < WT::TN; ++j) {
+        const int jcol = n0 + wn0 + j * 32 + l32;
+        if (jcol >= ntot) continue;
+        if constexpr (SPLIT) {
+            float *wsz = a.ws + (int64_t)z * a.OC * ntot + jcol;
+#pragma unroll
+            for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < a.M) wsz[(int64_t)m * ntot] = acc[i][j][r];
+                }
+        } else {
+            const int img = jcol / a.OHW;
+            const int p = jcol - img * a.OHW;
+            const int64_t ybase = (int64_t)img * a.OC * a.OHW + p;
+#pragma unroll
+            for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < a.M) {
+                        const int oc = group * a.M + m;
+                        const int64_t idx = ybase + (int64_t)oc * a.OHW;
+                        float v = acc[i][j][r];
+                        if (a.bias) v += a.bias[oc];
+                        if (a.res) v += a.res[idx];
+                        a.y[idx] = apply_act(v, a.act);
+                    }
+                }
+        }
+    }
+}
+
+// Sum split-K partials in split order and apply the conv epilogue.
+__global__ __launch_bounds__(256) void conv_splitk_reduce_kernel(const float *__restrict__ ws, int nsplit,
+                                                                 int OC, int ntot, int OHW,
+                                                                 const float *__restrict__ bias,
+                                                                 const float *__restrict__ res, int act,
+                                                                 float *__restrict__ y) {
+    const int64_t total = (int64_t)OC * ntot;
+    const int64_t plane = total;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int oc = (int)(e / ntot);
+        const int jcol = (int)(e - (int64_t)oc * ntot);
+        float v = 0.f;
+        for (int s = 0; s < nsplit; ++s) v += ws[s * plane + e];
+        const int img = jcol / OHW;
+        const int p = jcol - img * OHW;
+        const int64_t idx = ((int64_t)img * OC + oc) * OHW + p;
+        if (bias) v += bias[oc];
+        if (res) v += res[idx];
+        y[idx] = apply_act(v, act);
+    }
+}
+
+// W [group][OCg][Cg][KH][KW] -> W^T [group][K][ldw], K in tap-major (kh,kw,c)
+// order when tap_order, else (c,kh,kw); columns OCg..ldw-1 are zero.
+__global__ void conv_pack_wt_kernel(const float *__restrict__ w, float *__restrict__ out, int groups, int OCg,
+                                    int Cg, int KHW, int ldw, int tap_order) {
+    const int K = Cg * KHW;
+    const int64_t total = (int64_t)groups * K * ldw;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int m = (int)(e % ldw);
+        const int64_t gk = e / ldw;
+        const int k = (int)(gk % K);
+        const int g = (int)(gk / K);
+        float v = 0.f;
+        if (m < OCg) {
+            int c, tap;
+            if (tap_order) {
+                tap = k / Cg;
+                c = k - tap * Cg;
+            } else {
+                c = k / KHW;
+                tap = k - c * KHW;
+            }
+            v = w[(((int64_t)g * OCg + m) * Cg + c) * KHW + tap];
+        }
+        out[e] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: tile selection and launch.
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int BM, int BN, class BL>
+int launch_conv_tile(const ConvKArgs &a, int groups, int split, hipStream_t st) {
+    dim3 grid((a.geom.ntot + BN - 1) / BN, (a.M + BM - 1) / BM, split > 1 ? split : groups);
+    if (split > 1)
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, kBK, BL, true>), grid, dim3(kThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, kBK, BL, false>), grid, dim3(kThreads), 0, st, a);
+    return check_launch();
+}
+
+template <template <int> class BLT>
+int launch_conv_bl(const ConvKArgs &a, const TileChoice &tc, int groups, hipStream_t st) {
+    if (tc.bm == 128 && tc.bn == 128) return launch_conv_tile<128, 128, BLT<128>>(a, groups, tc.split, st);
+    if (tc.bm == 128 && tc.bn == 64) return launch_conv_tile<128, 64, BLT<64>>(a, groups, tc.split, st);
+    if (tc.bm == 64 && tc.bn == 128) return launch_conv_tile<64, 128, BLT<128>>(a, groups, tc.split, st);
+    return launch_conv_tile<64, 64, BLT<64>>(a, groups, tc.split, st);
+}
+
+template <int BN> using TapBL = Im2colTapLoader<BN, kBK>;
+template <int BN> using Gen33BL = Im2colLoader<BN, kBK, 3, 3>;
+template <int BN> using Gen77BL = Im2colLoader<BN, kBK, 7, 7>;
+template <int BN> using Gen11BL = Im2colLoader<BN, kBK, 1, 1>;
+template <int BN> using GenBL = Im2colLoader<BN, kBK, 0, 0>;
+
+bool conv_tap_order(const SpinnHipConvDesc *d) { return ((d->c / d->group) % kBK) == 0; }
+
+} // namespace
+
+int64_t igemm_packed_floats(const SpinnHipConvDesc *d) {
+    const int OCg = d->oc / d->group;
+    const int ldw = (OCg + 3) / 4 * 4;
+    const int64_t K = (int64_t)(d->c / d->group) * d->kh * d->kw;
+    return (int64_t)d->group * K * ldw;
+}
+
+int igemm_pack(const SpinnHipConvDesc *d, const float *w, float *packed, hipStream_t st) {
+    const int OCg = d->oc / d->group;
+    const int ldw = (OCg + 3) / 4 * 4;
+    const int64_t total = igemm_packed_floats(d);
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65535);
+    hipLaunchKernelGGL(conv_pack_wt_kernel, dim3(blocks), dim3(256), 0, st, w, packed, d->group, OCg,
+                       d->c / d->group, d->kh * d->kw, ldw, conv_tap_order(d) ? 1 : 0);
+    return check_launch();
+}
+
+static TileChoice igemm_tiles(const SpinnHipConvDesc *d) {
+    const int OCg = d->oc / d->group;
+    const int K = (d->c / d->group) * d->kh * d->kw;
+    const int ntot = d->n * d->oh * d->ow;
+    return choose_tiles(OCg, ntot, K, d->group, d->group == 1);
+}
+
+size_t igemm_workspace_bytes(const SpinnHipConvDesc *d) {
+    TileChoice tc = igemm_tiles(d);
+    if (tc.split <= 1) return 0;
+    return (size_t)tc.split * d->oc * ((size_t)d->n * d->oh * d->ow) * sizeof(float);
+}
+
+int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+               const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st) {
+    ConvKArgs a{};
+    const int OCg = d->oc / d->group;
+    a.ldw = (OCg + 3) / 4 * 4;
+    a.M = OCg;
+    a.K = (d->c / d->group) * d->kh * d->kw;
+    a.wpk = packed;
+    a.wpk_group_stride = (int64_t)a.K * a.ldw;
+    a.geom = ConvGeom{x, d->c, d->h, d->w, d->c / d->group, d->oh, d->ow, d->kh, d->kw,
+                      d->sh, d->sw, d->ph, d->pw, d->n * d->oh * d->ow};
+    a.y = y;
+    a.bias = bias;
+    a.res = res;
+    a.act = d->act;
+    a.OC = d->oc;
+    a.OHW = d->oh * d->ow;
+    TileChoice tc = igemm_tiles(d);
+    if (tc.split > 1) {
+        const size_t need = (size_t)tc.split * d->oc * (size_t)a.geom.ntot * sizeof(float);
+        if (!ws || ws_bytes < need) return SPINN_HIP_EWORKSPACE;
+        a.ws = (float *)ws;
+        a.k_chunk = tc.k_chunk;
+    }
+    int rc;
+    if (conv_tap_order(d)) rc = launch_conv_bl<TapBL>(a, tc, d->group, st);
+    else if (d->kh == 3 && d->kw == 3) rc = launch_conv_bl<Gen33BL>(a, tc, d->group, st);
+    else if (d->kh == 7 && d->kw == 7) rc = launch_conv_bl<Gen77BL>(a, tc, d->group, st);
+    else if (d->kh == 1 && d->kw == 1) rc = launch_conv_bl<Gen11BL>(a, tc, d->group, st);
+    else rc = launch_conv_bl<GenBL>(a, tc, d->group, st);
+    if (rc) return rc;
+    if (tc.split > 1) {
+        const int64_t total = (int64_t)d->oc * a.geom.ntot;
+        const int blocks = (int)std::min<int64_t>((total + 255) / 256, 8192);
+        hipLaunchKernelGGL(conv_splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, (const float *)ws,
+                           tc.split, d->oc, a.geom.ntot, a.OHW, bias, res, d->act, y);
+        rc = check_launch();
+    }
+    return rc;
+}
+
+} // namespace spinn

@@ -1,0 +1,258 @@
+// gemm.hip - Gemm / MatMul on the fp32 MFMA tile engine.
+//
+// y[b] = alpha * op(A[b]) op(B[b]) + beta * C, row-major, any transpose
+// combination: each operand is staged k-major in LDS by the loader matching
+// its memory order (16-byte loads when rows are aligned), so a transposed B
+// (the usual Gemm weight layout, transB=1) is read in place instead of being
+// transposed into a temporary on every call (SPINN/run_time/ops/mm/gemm.c:50-59).
+// Small grids split K over blockIdx.z with a deterministic reduction.
+#include "mfma_core.h"
+#include "spinn_hip_internal.h"
+#include <type_traits>
+
+namespace spinn {
+
+// ---------------------------------------------------------------------------
+// Gemm
+// ---------------------------------------------------------------------------
+struct GemmKArgs {
+    const float *a, *b, *c;
+    int64_t lda, ldb;
+    int64_t stride_a, stride_b, stride_y;
+    int M, N, K;
+    int c_mode;
+    float alpha, beta;
+    float *y;
+    float *ws;
+    int k_chunk;
+};
+
+template <int BM, int BN, int BK, class ALoader, class BLoader, bool SPLIT>
+__global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmKArgs a) {
+    using WT = WaveTiling<BM, BN>;
+    constexpr int SA = LdsPad<BM>::stride;
+    constexpr int SB = LdsPad<BN>::stride;
+    __shared__ __attribute__((aligned(16))) float As[2][BK * SA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * SB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = (wave >> 1) * WT::WM;
+    const int wn0 = (wave & 1) * WT::WN;
+    const int n0 = blockIdx.x * BN;
+    const int m0 = blockIdx.y * BM;
+    const int z = blockIdx.z;
+    const int batch = SPLIT ? 0 : z;
+    const int k_begin = SPLIT ? z * a.k_chunk : 0;
+    const int k_end = SPLIT ? min(a.K, k_begin + a.k_chunk) : a.K;
+
+    ALoader al;
+    BLoader bl;
+    // A tile rows are m: KMajor source a[k*lda + m], RowK source a[m*lda + k].
+    if constexpr (ALoader::kIsKMajor) {
+        al.src = a.a + batch * a.stride_a + m0;
+    } else {
+        al.src = a.a + batch * a.stride_a + (int64_t)m0 * a.lda;
+    }
+    al.ld = a.lda;
+    al.t_valid = a.M - m0;
+    al.k_end = k_end;
+    if constexpr (BLoader::kIsKMajor) {
+        bl.src = a.b + batch * a.stride_b + n0;
+    } else {
+        bl.src = a.b + batch * a.stride_b + (int64_t)n0 * a.ldb;
+    }
+    bl.ld = a.ldb;
+    bl.t_valid = a.N - n0;
+    bl.k_end = k_end;
+
+    f32x16 acc[WT::TM][WT::TN];
+#pragma unroll
+    for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < WT::TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    const int nslices = (k_end - k_begin + BK - 1) / BK;
+    if (nslices > 0) {
+        al.fetch(k_begin, tid);
+        bl.fetch(k_begin, tid);
+        al.commit(As[0], tid);
+        bl.commit(Bs[0], tid);
+        __syncthreads();
+        for (int s = 0; s < nslices; ++s) {
+            const int cur = s & 1;
+            const bool more = s + 1 < nslices;
+            if (more) {
+                al.fetch(k_begin + (s + 1) * BK, tid);
+                bl.fetch(k_begin + (s + 1) * BK, tid);
+            }
+            mma_slice<BM, BN, BK>(As[cur], Bs[cur], acc, wm0, wn0, lane);
+            if (more) {
+                al.commit(As[cur ^ 1], tid);
+                bl.commit(Bs[cur ^ 1], tid);
+            }
+            __syncthreads();
+        }
+    }
+
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+#pragma unroll
+    for (int j = 0; j < WT::TN; ++j) {
+        const int n = n0 + wn0 + j * 32 + l32;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m >= a.M) continue;
+                if constexpr (SPLIT) {
+                    a.ws[((int64_t)z * a.M + m) * a.N + n] = acc[i][j][r];
+                } else {
+                    float v = a.alpha * acc[i][j][r];
+                    if (a.c_mode == 1) v += a.beta * a.c[n];
+                    else if (a.c_mode == 2) v += a.beta * a.c[(int64_t)m * a.N + n];
+                    a.y[batch * a.stride_y + (int64_t)m * a.N + n] = v;
+                }
+            }
+    }
+}
+
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *__restrict__ ws, int nsplit, int M,
+                                                                 int N, float alpha, float beta, int c_mode,
+                                                                 const float *__restrict__ c,
+                                                                 float *__restrict__ y) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        float v = 0.f;
+        for (int s = 0; s < nsplit; ++s) v += ws[s * total + e];
+        v *= alpha;
+        if (c_mode == 1) v += beta * c[e % N];
+        else if (c_mode == 2) v += beta * c[e];
+        y[e] = v;
+    }
+}
+
+// Tag the loaders with their source orientation for gemm_kernel.
+template <int BT, int BK, bool VEC>
+struct KMajorG : KMajorLoader<BT, BK, VEC> {
+    static constexpr bool kIsKMajor = true;
+};
+template <int BT, int BK, bool VEC>
+struct RowKG : RowKLoader<BT, BK, VEC> {
+    static constexpr bool kIsKMajor = false;
+};
+
+// ---- Gemm ----
+namespace {
+
+template <int BM, int BN, class AL, class BL>
+int launch_gemm_tile(const GemmKArgs &a, int batch, int split, hipStream_t st) {
+    dim3 grid((a.N + BN - 1) / BN, (a.M + BM - 1) / BM, split > 1 ? split : batch);
+    if (split > 1)
+        hipLaunchKernelGGL((gemm_kernel<BM, BN, kBK, AL, BL, true>), grid, dim3(kThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_kernel<BM, BN, kBK, AL, BL, false>), grid, dim3(kThreads), 0, st, a);
+    return check_launch();
+}
+
+template <int BM, int BN, bool TA, bool TB, bool VA, bool VB>
+int launch_gemm_cfg(const GemmKArgs &a, int batch, int split, hipStream_t st) {
+    // A: trans_a -> source [K][M] (k-major); else [M][K] (rows, K contiguous).
+    // B: trans_b -> source [N][K] (rows, K contiguous); else [K][N] (k-major).
+    using AL = typename std::conditional<TA, KMajorG<BM, kBK, VA>, RowKG<BM, kBK, VA>>::type;
+    using BL = typename std::conditional<TB, RowKG<BN, kBK, VB>, KMajorG<BN, kBK, VB>>::type;
+    return launch_gemm_tile<BM, BN, AL, BL>(a, batch, split, st);
+}
+
+template <int BM, int BN, bool TA, bool TB, bool VA>
+int gemm_pick_vb(const GemmKArgs &a, bool vb, int batch, int split, hipStream_t st) {
+    return vb ? launch_gemm_cfg<BM, BN, TA, TB, VA, true>(a, batch, split, st)
+              : launch_gemm_cfg<BM, BN, TA, TB, VA, false>(a, batch, split, st);
+}
+
+template <int BM, int BN, bool TA, bool TB>
+int gemm_pick_va(const GemmKArgs &a, bool va, bool vb, int batch, int split, hipStream_t st) {
+    return va ? gemm_pick_vb<BM, BN, TA, TB, true>(a, vb, batch, split, st)
+              : gemm_pick_vb<BM, BN, TA, TB, false>(a, vb, batch, split, st);
+}
+
+template <int BM, int BN, bool TA>
+int gemm_pick_tb(const GemmKArgs &a, bool tb, bool va, bool vb, int batch, int split, hipStream_t st) {
+    return tb ? gemm_pick_va<BM, BN, TA, true>(a, va, vb, batch, split, st)
+              : gemm_pick_va<BM, BN, TA, false>(a, va, vb, batch, split, st);
+}
+
+template <int BM, int BN>
+int launch_gemm_loaders(const GemmKArgs &a, bool ta, bool tb, bool va, bool vb, int batch, int split,
+                        hipStream_t st) {
+    return ta ? gemm_pick_tb<BM, BN, true>(a, tb, va, vb, batch, split, st)
+              : gemm_pick_tb<BM, BN, false>(a, tb, va, vb, batch, split, st);
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+TileChoice gemm_tiles(const SpinnHipGemmDesc *d) {
+    return choose_tiles(d->m, d->n, d->k, d->batch > 0 ? d->batch : 1, d->batch <= 1);
+}
+
+} // namespace
+
+size_t gemm_workspace_bytes(const SpinnHipGemmDesc *d) {
+    TileChoice tc = gemm_tiles(d);
+    if (tc.split <= 1) return 0;
+    return (size_t)tc.split * d->m * (size_t)d->n * sizeof(float);
+}
+
+int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const float *C, float *Y, void *ws,
+             size_t ws_bytes, hipStream_t st) {
+    GemmKArgs a{};
+    a.a = A;
+    a.b = B;
+    a.c = C;
+    a.M = d->m;
+    a.N = d->n;
+    a.K = d->k;
+    a.lda = d->trans_a ? d->m : d->k;
+    a.ldb = d->trans_b ? d->k : d->n;
+    const int batch = d->batch > 0 ? d->batch : 1;
+    a.stride_a = d->stride_a;
+    a.stride_b = d->stride_b;
+    a.stride_y = d->stride_y;
+    a.c_mode = C ? d->c_mode : 0;
+    a.alpha = d->alpha;
+    a.beta = d->beta;
+    a.y = Y;
+    // Vector loads need 16-byte aligned rows in every batch entry.
+    const bool va = aligned16(A) && (a.lda % 4 == 0) && (batch == 1 || d->stride_a % 4 == 0);
+    const bool vb = aligned16(B) && (a.ldb % 4 == 0) && (batch == 1 || d->stride_b % 4 == 0);
+    TileChoice tc = gemm_tiles(d);
+    if (tc.split > 1) {
+        const size_t need = (size_t)tc.split * d->m * (size_t)d->n * sizeof(float);
+        if (!ws || ws_bytes < need) return SPINN_HIP_EWORKSPACE;
+        a.ws = (float *)ws;
+        a.k_chunk = tc.k_chunk;
+    }
+    const bool ta = d->trans_a != 0, tb = d->trans_b != 0;
+    int rc;
+    if (tc.bm == 128 && tc.bn == 128) rc = launch_gemm_loaders<128, 128>(a, ta, tb, va, vb, batch, tc.split, st);
+    else if (tc.bm == 128 && tc.bn == 64) rc = launch_gemm_loaders<128, 64>(a, ta, tb, va, vb, batch, tc.split, st);
+    else if (tc.bm == 64 && tc.bn == 128) rc = launch_gemm_loaders<64, 128>(a, ta, tb, va, vb, batch, tc.split, st);
+    else rc = launch_gemm_loaders<64, 64>(a, ta, tb, va, vb, batch, tc.split, st);
+    if (rc) return rc;
+    if (tc.split > 1) {
+        const int64_t total = (int64_t)d->m * d->n;
+        const int blocks = (int)std::min<int64_t>((total + 255) / 256, 8192);
+        hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, (const float *)ws, tc.split,
+                           d->m, d->n, d->alpha, d->beta, a.c_mode, C, Y);
+        rc = check_launch();
+    }
+    return rc;
+}
+
+} // namespace spinn

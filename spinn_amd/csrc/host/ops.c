@@ -1,0 +1,424 @@
+/*
+ * ops.c - operator registry and the device operator kernels behind it.
+ *
+ * The registry and dispatcher keep the reference's contract
+ * (SPINN/run_time/spinn_ops.c:17-228): a lazily filled table of 512
+ * SpinnOpKernel slots indexed by ENNF op id; an id >= 512 returns -1; an
+ * unregistered op prints a notice and returns 0 (skipped).
+ *
+ * Each kernel reads its operands exactly as the reference operator does
+ * (arity, dims, params, fused-act sniffing), then hands device pointers to the
+ * HIP C ABI (spinn_hip_*). Nothing here touches tensor data on the host.
+ */
+#include "spinn_host.h"
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+SpinnExec g_spinn_exec = {0};
+
+static void *g_fallback_ws = NULL;
+static size_t g_fallback_ws_bytes = 0;
+
+void *spinn_exec_workspace(size_t bytes) {
+    if (bytes == 0) return NULL;
+    if (g_spinn_exec.workspace && g_spinn_exec.workspace_bytes >= bytes) return g_spinn_exec.workspace;
+    if (g_fallback_ws_bytes < bytes) {
+        if (g_fallback_ws) spinn_hip_free(g_fallback_ws);
+        g_fallback_ws = NULL;
+        g_fallback_ws_bytes = 0;
+        if (spinn_hip_malloc(&g_fallback_ws, bytes) != 0) return NULL;
+        g_fallback_ws_bytes = bytes;
+    }
+    return g_fallback_ws;
+}
+
+void spinn_exec_release_fallback(void) {
+    if (g_fallback_ws) spinn_hip_free(g_fallback_ws);
+    g_fallback_ws = NULL;
+    g_fallback_ws_bytes = 0;
+}
+
+/* Packed-weight buffers: device payload plus a host record of (algo, bytes). */
+typedef struct PackedRec {
+    void *dev;
+    size_t bytes;
+    int algo;
+    struct PackedRec *next;
+} PackedRec;
+static PackedRec *g_packed = NULL;
+
+int spinn_packed_alloc(void **dev, size_t bytes, int algo) {
+    PackedRec *r = (PackedRec *)calloc(1, sizeof(PackedRec));
+    if (!r) return -1;
+    int rc = spinn_hip_malloc(&r->dev, bytes);
+    if (rc) {
+        free(r);
+        return rc;
+    }
+    r->bytes = bytes;
+    r->algo = algo;
+    r->next = g_packed;
+    g_packed = r;
+    *dev = r->dev;
+    return 0;
+}
+
+int spinn_packed_matches(const void *dev, size_t bytes, int algo) {
+    for (PackedRec *r = g_packed; r; r = r->next)
+        if (r->dev == dev) return r->bytes == bytes && r->algo == algo;
+    return 0;
+}
+
+void spinn_packed_release(void *dev) {
+    PackedRec **pp = &g_packed;
+    while (*pp) {
+        if ((*pp)->dev == dev) {
+            PackedRec *r = *pp;
+            *pp = r->next;
+            spinn_hip_free(r->dev);
+            free(r);
+            return;
+        }
+        pp = &(*pp)->next;
+    }
+}
+
+static void note_workspace(size_t need) {
+    if (need > g_spinn_exec.prepare_ws_need) g_spinn_exec.prepare_ws_need = need;
+}
+
+/* ------------------------------------------------------------------------
+ * Conv (SPINN/run_time/ops/conv/conv2d.c:92-232)
+ * ---------------------------------------------------------------------- */
+int spinn_conv_desc_from_tensors(SpinnTensor **in, int n_in, const void *params, uint16_t params_size,
+                                 SpinnTensor **out, SpinnHipConvDesc *d, const float **bias, const float **res) {
+    if (n_in < 2 || !out || !out[0]) return -1;
+    const ENNF_ConvParams *p =
+        (params && params_size >= sizeof(ENNF_ConvParams)) ? (const ENNF_ConvParams *)params : NULL;
+    /* The act code is read before the inputs: with ADD / ADD_RELU the last
+     * input is the residual, not a bias (conv2d.c:96-105). */
+    const int act = p ? p->reserved : 0;
+    const int has_res = (act == SPINN_ACT_ADD || act == SPINN_ACT_ADD_RELU);
+    const int n_real = has_res ? n_in - 1 : n_in;
+    if (has_res && n_in < 3) return -1;
+    SpinnTensor *X = in[0], *W = in[1], *Y = out[0];
+    if (!X || !W || X->ndim != 4 || W->ndim != 4 || Y->ndim != 4) return -1;
+    memset(d, 0, sizeof(*d));
+    d->n = (int)X->dims[0];
+    d->c = (int)X->dims[1];
+    d->h = (int)X->dims[2];
+    d->w = (int)X->dims[3];
+    d->oc = (int)W->dims[0];
+    const int kc = (int)W->dims[1];
+    d->kh = (int)W->dims[2];
+    d->kw = (int)W->dims[3];
+    d->sh = d->sw = 1;
+    d->group = 1;
+    d->oh = (int)Y->dims[2];
+    d->ow = (int)Y->dims[3];
+    if (p) {
+        if (p->group > 0) d->group = p->group;
+        if (p->kernel_shape[0] > 0) d->kh = p->kernel_shape[0];
+        if (p->kernel_shape[1] > 0) d->kw = p->kernel_shape[1];
+        if (p->strides[0] > 0) d->sh = p->strides[0];
+        if (p->strides[1] > 0) d->sw = p->strides[1];
+        /* Only the begin pads are used; dilations are ignored (conv2d.c:131). */
+        d->ph = p->pads[0];
+        d->pw = p->pads[1];
+        if (p->auto_pad == ENNF_AUTOPAD_SAME_UPPER || p->auto_pad == ENNF_AUTOPAD_SAME_LOWER) {
+            int ph = (d->oh - 1) * d->sh + d->kh - d->h;
+            int pw = (d->ow - 1) * d->sw + d->kw - d->w;
+            if (ph < 0) ph = 0;
+            if (pw < 0) pw = 0;
+            d->ph = (p->auto_pad == ENNF_AUTOPAD_SAME_UPPER) ? ph / 2 : (ph + 1) / 2;
+            d->pw = (p->auto_pad == ENNF_AUTOPAD_SAME_UPPER) ? pw / 2 : (pw + 1) / 2;
+        }
+    }
+    d->act = act;
+    if (kc * d->group != d->c || (int)Y->dims[1] != d->oc || (int)Y->dims[0] != d->n) return -1;
+    d->algo = SPINN_CONV_ALGO_AUTO;
+    int algo = spinn_hip_conv_select_algo(d);
+    if (algo < 0) return -1;
+    if (algo == SPINN_CONV_ALGO_WINOGRAD && g_spinn_exec.conv_policy == SPINN_CONV_POLICY_IGEMM) {
+        algo = SPINN_CONV_ALGO_IMPLICIT_GEMM;
+    } else if (algo == SPINN_CONV_ALGO_IMPLICIT_GEMM && g_spinn_exec.conv_policy == SPINN_CONV_POLICY_WINOGRAD) {
+        d->algo = SPINN_CONV_ALGO_WINOGRAD;
+        if (spinn_hip_conv_packed_size(d) == 0) algo = SPINN_CONV_ALGO_IMPLICIT_GEMM; /* not eligible */
+        else algo = SPINN_CONV_ALGO_WINOGRAD;
+    }
+    d->algo = algo;
+    *bias = (n_real > 2 && in[2] && in[2]->data) ? (const float *)in[2]->data : NULL;
+    *res = has_res ? (const float *)in[n_in - 1]->data : NULL;
+    if (has_res && !*res) return -1;
+    return 0;
+}
+
+int op_conv2d(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 2 || n_out < 1) return -1;
+    SpinnHipConvDesc d;
+    const float *bias = NULL, *res = NULL;
+    if (spinn_conv_desc_from_tensors(in, n_in, params, params_size, out, &d, &bias, &res) != 0) return -1;
+    SpinnTensor *W = in[1];
+    /* Weights re-laid out once per tensor and cached on it, like the
+     * reference's lazily packed A (conv2d.c:200-207); normally done by the
+     * prepare pass of spinn_plan so no run ever allocates. The buffer keeps a
+     * host-side record of the layout it holds; a conv that would read it as
+     * another layout fails instead of reading past it. */
+    const size_t psz = spinn_hip_conv_packed_size(&d);
+    if (psz > 0) {
+        if (!W->packed_data) {
+            void *pk = NULL;
+            int rc = spinn_packed_alloc(&pk, psz, d.algo);
+            if (rc) return rc;
+            rc = spinn_hip_conv_pack_weights(&d, (const float *)W->data, (float *)pk, g_spinn_exec.stream);
+            if (rc) {
+                spinn_packed_release(pk);
+                return rc;
+            }
+            W->packed_data = pk;
+        } else if (!spinn_packed_matches(W->packed_data, psz, d.algo)) {
+            return -1;
+        }
+    }
+    const size_t wsz = spinn_hip_conv_workspace_size(&d);
+    if (g_spinn_exec.preparing) {
+        note_workspace(wsz);
+        return 0;
+    }
+    void *ws = wsz ? spinn_exec_workspace(wsz) : NULL;
+    if (wsz && !ws) return SPINN_HIP_EWORKSPACE;
+    return spinn_hip_conv(&d, (const float *)in[0]->data, (const float *)W->data, (const float *)W->packed_data,
+                          bias, res, (float *)out[0]->data, ws, wsz, g_spinn_exec.stream);
+}
+
+/* ------------------------------------------------------------------------
+ * Gemm (SPINN/run_time/ops/mm/gemm.c:7-78)
+ * ---------------------------------------------------------------------- */
+int op_gemm(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 2 || n_out < 1) return -1;
+    SpinnTensor *A = in[0], *B = in[1], *Y = out[0];
+    SpinnTensor *Cb = (n_in > 2 && in[2] && in[2]->data) ? in[2] : NULL;
+    if (A->ndim != 2 || B->ndim != 2) return -1;
+    SpinnHipGemmDesc d;
+    memset(&d, 0, sizeof(d));
+    d.alpha = 1.f;
+    d.beta = 1.f;
+    if (params && params_size >= sizeof(ENNF_GemmParams)) {
+        const ENNF_GemmParams *p = (const ENNF_GemmParams *)params;
+        d.trans_a = p->transA;
+        d.trans_b = p->transB;
+        d.alpha = p->alpha;
+        d.beta = p->beta;
+    }
+    d.m = (int)(d.trans_a ? A->dims[1] : A->dims[0]);
+    d.k = (int)(d.trans_a ? A->dims[0] : A->dims[1]);
+    d.n = (int)(d.trans_b ? B->dims[0] : B->dims[1]);
+    const int kb = (int)(d.trans_b ? B->dims[1] : B->dims[0]);
+    if (kb != d.k) return -1;
+    d.batch = 1;
+    /* C joins as beta*C only when beta != 0: an [N] vector broadcast over rows,
+     * else a full [M,N] matrix (gemm.c:31,62-67). */
+    if (Cb && d.beta != 0.0f) {
+        if (Cb->elem_count == (uint32_t)d.n) d.c_mode = 1;
+        else if (Cb->elem_count == (uint32_t)d.m * (uint32_t)d.n) d.c_mode = 2;
+        else return -1;
+    }
+    const size_t wsz = spinn_hip_gemm_workspace_size(&d);
+    if (g_spinn_exec.preparing) {
+        note_workspace(wsz);
+        return 0;
+    }
+    void *ws = wsz ? spinn_exec_workspace(wsz) : NULL;
+    if (wsz && !ws) return SPINN_HIP_EWORKSPACE;
+    return spinn_hip_gemm(&d, (const float *)A->data, (const float *)B->data, d.c_mode ? (const float *)Cb->data : NULL,
+                          (float *)Y->data, ws, wsz, g_spinn_exec.stream);
+}
+
+/* ------------------------------------------------------------------------
+ * MatMul (SPINN/run_time/ops/mm/matmul.c:6-62): 2-D x 2-D, or equal batch
+ * products over the leading dims; anything else returns -1 as there.
+ * ---------------------------------------------------------------------- */
+int op_matmul(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 2 || n_out < 1) return -1;
+    SpinnTensor *A = in[0], *B = in[1], *Y = out[0];
+    int an = A->ndim, bn = B->ndim;
+    if (an < 2 || bn < 2) return -1;
+    SpinnHipGemmDesc d;
+    memset(&d, 0, sizeof(d));
+    d.alpha = 1.f;
+    d.beta = 0.f;
+    d.m = (int)A->dims[an - 2];
+    d.k = (int)A->dims[an - 1];
+    d.n = (int)B->dims[bn - 1];
+    if ((int)B->dims[bn - 2] != d.k) return -1;
+    int batch = 1, batch_b = 1;
+    for (int i = 0; i < an - 2; i++) batch *= (int)A->dims[i];
+    for (int i = 0; i < bn - 2; i++) batch_b *= (int)B->dims[i];
+    if (an == 2 && bn == 2) batch = batch_b = 1;
+    if (batch != batch_b) return -1;
+    d.batch = batch;
+    d.stride_a = (int64_t)d.m * d.k;
+    d.stride_b = (int64_t)d.k * d.n;
+    d.stride_y = (int64_t)d.m * d.n;
+    const size_t wsz = spinn_hip_gemm_workspace_size(&d);
+    if (g_spinn_exec.preparing) {
+        note_workspace(wsz);
+        return 0;
+    }
+    void *ws = wsz ? spinn_exec_workspace(wsz) : NULL;
+    if (wsz && !ws) return SPINN_HIP_EWORKSPACE;
+    return spinn_hip_gemm(&d, (const float *)A->data, (const float *)B->data, NULL, (float *)Y->data, ws, wsz,
+                          g_spinn_exec.stream);
+}
+
+/* ------------------------------------------------------------------------
+ * MaxPool (SPINN/run_time/ops/pool/maxpool.c:5-49)
+ * ---------------------------------------------------------------------- */
+int op_maxpool(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 1 || n_out < 1) return -1;
+    SpinnTensor *X = in[0], *Y = out[0];
+    if (X->ndim != 4 || Y->ndim != 4) return -1;
+    SpinnHipPoolDesc d;
+    memset(&d, 0, sizeof(d));
+    d.n = (int)X->dims[0];
+    d.c = (int)X->dims[1];
+    d.h = (int)X->dims[2];
+    d.w = (int)X->dims[3];
+    d.oh = (int)Y->dims[2];
+    d.ow = (int)Y->dims[3];
+    d.kh = d.kw = d.sh = d.sw = 1;
+    if (params && params_size >= sizeof(ENNF_PoolParams)) {
+        const ENNF_PoolParams *p = (const ENNF_PoolParams *)params;
+        d.kh = p->kernel_shape[0];
+        d.kw = p->kernel_shape[1];
+        d.sh = p->strides[0];
+        d.sw = p->strides[1];
+        d.ph = p->pads[0];
+        d.pw = p->pads[1];
+    }
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_maxpool2d(&d, (const float *)X->data, (float *)Y->data, g_spinn_exec.stream);
+}
+
+/* GlobalAveragePool (SPINN/run_time/ops/pool/global_avg_pool.c:4-28). */
+int op_global_avg_pool(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out,
+                       int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 1 || n_out < 1) return -1;
+    SpinnTensor *X = in[0];
+    if (X->ndim != 4) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_reduce_mean((int64_t)X->dims[0] * X->dims[1], (int64_t)X->dims[2] * X->dims[3], 1,
+                                 (const float *)X->data, (float *)out[0]->data, g_spinn_exec.stream);
+}
+
+/* ReduceMean: the axis choice of SPINN/run_time/ops/reduce/reduce_mean.c:10-75,
+ * then one mean over the middle axis of an [outer, dim, inner] view. */
+int op_reduce_mean(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 1 || n_out < 1) return -1;
+    SpinnTensor *X = in[0], *Y = out[0];
+    const ENNF_ReduceParams *p =
+        (params && params_size >= sizeof(ENNF_ReduceParams)) ? (const ENNF_ReduceParams *)params : NULL;
+    const int ndim = X->ndim;
+    int axis = -1, merge = 0;
+    if (p && p->num_axes > 0) {
+        axis = p->axes[0];
+        if (axis < 0) axis += ndim;
+        if (p->num_axes > 1 && axis + p->num_axes == ndim) merge = 1;
+    }
+    if (axis == -1 && (!p || p->num_axes == 0)) {
+        if (Y->elem_count > 1 && X->ndim == Y->ndim + 1) {
+            int inferred = -1, od = 0;
+            for (int dd = 0; dd < X->ndim; dd++) {
+                if (od < Y->ndim && X->dims[dd] == Y->dims[od]) od++;
+                else if (inferred == -1) inferred = dd;
+                else { inferred = -2; break; }
+            }
+            if (inferred >= 0) axis = inferred;
+        } else if (X->ndim == Y->ndim) {
+            int first = -1, cnt = 0;
+            for (int dd = 0; dd < X->ndim; dd++) {
+                if (X->dims[dd] != Y->dims[dd]) {
+                    if (Y->dims[dd] == 1) { if (first == -1) first = dd; cnt++; }
+                    else { first = -2; break; }
+                } else if (first != -1) { first = -2; break; }
+            }
+            if (first >= 0 && first + cnt == X->ndim) { axis = first; merge = 1; }
+        }
+    }
+    int64_t outer = 1, dim, inner = 1;
+    if (axis == -1) {
+        /* mean of everything; the reference broadcasts it to every output element */
+        if (Y->elem_count != 1) return SPINN_HIP_EUNSUPPORTED;
+        outer = 1;
+        dim = X->elem_count;
+    } else {
+        if (axis < 0 || axis >= ndim) return -1;
+        for (int i = 0; i < axis; i++) outer *= X->dims[i];
+        dim = X->dims[axis];
+        if (merge) {
+            for (int i = axis + 1; i < ndim; i++) dim *= X->dims[i];
+        } else {
+            for (int i = axis + 1; i < ndim; i++) inner *= X->dims[i];
+        }
+    }
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_reduce_mean(outer, dim, inner, (const float *)X->data, (float *)Y->data, g_spinn_exec.stream);
+}
+
+/* Reshape / Flatten / Identity: a copy unless the tensors alias
+ * (SPINN/run_time/ops/shape/reshape.c:6-14, ops/tensor/flatten.c:3-8). */
+int op_copy_alias(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 1 || n_out < 1) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    if (in[0]->data == out[0]->data) return 0;
+    size_t bytes = in[0]->size < out[0]->size ? in[0]->size : out[0]->size;
+    return spinn_hip_copy(out[0]->data, in[0]->data, bytes, g_spinn_exec.stream);
+}
+
+/* ------------------------------------------------------------------------
+ * Registry and dispatcher (SPINN/run_time/spinn_ops.c:17-228)
+ * ---------------------------------------------------------------------- */
+static SpinnOpKernel g_op_registry[ENNF_OP_REGISTRY_SIZE];
+static int g_registry_ready = 0;
+
+static void registry_init(void) {
+    if (g_registry_ready) return;
+    g_op_registry[ENNF_OP_Conv] = op_conv2d;
+    g_op_registry[ENNF_OP_Gemm] = op_gemm;
+    g_op_registry[ENNF_OP_MatMul] = op_matmul;
+    g_op_registry[ENNF_OP_MaxPool] = op_maxpool;
+    g_op_registry[ENNF_OP_GlobalAveragePool] = op_global_avg_pool;
+    g_op_registry[ENNF_OP_ReduceMean] = op_reduce_mean;
+    g_op_registry[ENNF_OP_Reshape] = op_copy_alias;
+    g_op_registry[ENNF_OP_Flatten] = op_copy_alias;
+    g_op_registry[ENNF_OP_Identity] = op_copy_alias;
+    g_registry_ready = 1;
+}
+
+int spinn_dispatch_op(uint16_t op_type, SpinnTensor **inputs, int n_in, void *params, uint16_t params_size,
+                      SpinnTensor **outputs, int n_out) {
+    registry_init();
+    if (op_type >= ENNF_OP_REGISTRY_SIZE) {
+        printf("Warning: Op type %d out of range\n", op_type);
+        return -1;
+    }
+    SpinnOpKernel k = g_op_registry[op_type];
+    if (!k) {
+        if (!g_spinn_exec.preparing) printf("  -> Op %d not implemented (skip)\n", op_type);
+        return 0;
+    }
+    return k(inputs, n_in, params, params_size, outputs, n_out);
+}
+
+/* Exposed for tests: is an op id served by a device kernel? */
+int spinn_op_registered(uint16_t op_type) {
+    registry_init();
+    return op_type < ENNF_OP_REGISTRY_SIZE && g_op_registry[op_type] != NULL;
+}

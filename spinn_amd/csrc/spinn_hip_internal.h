@@ -1,0 +1,63 @@
+// spinn_hip_internal.h - declarations shared by the HIP translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <stdint.h>
+#include "../../include/spinn_hip.h"
+#include "../../include/ennf_format.h"
+
+namespace spinn {
+
+// Map the last launch error to the C-ABI code (0 when the launch was accepted).
+inline int hip_code(hipError_t e) { return e == hipSuccess ? 0 : (SPINN_HIP_ERUNTIME - (int)e); }
+inline int check_launch() { return hip_code(hipGetLastError()); }
+
+// Fused post-op after bias and residual (SPINN/run_time/ops/mm/gemm_kernel.c:324-335).
+__device__ __forceinline__ float apply_act(float v, int act) {
+    if (act == SPINN_ACT_RELU || act == SPINN_ACT_ADD_RELU) {
+        v = v < 0.f ? 0.f : v;
+    } else if (act == SPINN_ACT_SILU) {
+        v = v / (1.0f + expf(-v));
+    }
+    return v;
+}
+
+constexpr int kBK = 16; // K depth of one LDS slice of the MFMA GEMMs
+
+// Output tile (bm x bn) and K split of one MFMA GEMM launch.
+struct TileChoice {
+    int bm, bn, split, k_chunk;
+};
+TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split);
+
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cu_count();
+
+// implicit GEMM (conv_gemm.hip)
+int64_t igemm_packed_floats(const SpinnHipConvDesc *d);
+int igemm_pack(const SpinnHipConvDesc *d, const float *w, float *packed, hipStream_t st);
+size_t igemm_workspace_bytes(const SpinnHipConvDesc *d);
+int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+               const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st);
+size_t gemm_workspace_bytes(const SpinnHipGemmDesc *d);
+int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const float *C, float *Y, void *ws,
+             size_t ws_bytes, hipStream_t st);
+
+// Winograd F(2x2,3x3) (winograd.hip)
+bool winograd_eligible(const SpinnHipConvDesc *d);
+int64_t winograd_packed_floats(const SpinnHipConvDesc *d);
+int winograd_pack(const SpinnHipConvDesc *d, const float *w, float *packed, hipStream_t st);
+size_t winograd_workspace_bytes(const SpinnHipConvDesc *d);
+int winograd_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+                  const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st);
+
+// grouped / depthwise direct convolution (direct_conv.hip)
+int direct_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias, const float *res,
+                float *y, hipStream_t st);
+
+// glue (glue.hip)
+int maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, hipStream_t st);
+int reduce_mean(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, hipStream_t st);
+int fill_u32(void *dst, uint32_t value, size_t bytes, hipStream_t st);
+
+} // namespace spinn

@@ -1,0 +1,74 @@
+"""Shared fixtures: the `gpu` marker, the native library, device buffers and the
+parity bar.
+
+Parity bar (fp32, from the task's tolerance): max-abs error <= 1e-3 and
+relative L2 error <= 1e-4. For outputs whose magnitude exceeds 1 (deep
+random-init networks reach 1e3..1e6), the max-abs bound is scaled by the
+output's max-abs value, i.e. it becomes a relative max-error bound.
+"""
+from __future__ import annotations
+
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+MAX_ABS = 1e-3
+REL_L2 = 1e-4
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the HIP C ABI)")
+    config.addinivalue_line("markers", "slow: long CPU test")
+
+
+def errors(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert y.shape == ref.shape, (y.shape, ref.shape)
+    assert np.all(np.isfinite(y)), "non-finite output"
+    d = y - ref
+    max_abs = float(np.max(np.abs(d))) if d.size else 0.0
+    nref = float(np.linalg.norm(ref.ravel()))
+    rel = float(np.linalg.norm(d.ravel()) / nref) if nref > 0 else float(np.linalg.norm(d.ravel()))
+    scale = max(1.0, float(np.max(np.abs(ref)))) if ref.size else 1.0
+    return max_abs, rel, scale
+
+
+def assert_parity(y, ref, max_abs=MAX_ABS, rel_l2=REL_L2, what=""):
+    ma, rel, scale = errors(y, ref)
+    assert ma <= max_abs * scale and rel <= rel_l2, (
+        f"{what}: max_abs={ma:.3e} (bound {max_abs * scale:.3e}), rel_l2={rel:.3e} (bound {rel_l2:.1e})")
+
+
+@pytest.fixture(scope="session")
+def native():
+    """The built native library (built in-tree on first use if absent)."""
+    from spinn_amd import native as N
+    if not N.LIB_PATH.exists():
+        from spinn_amd import build
+        build.build()
+    return N
+
+
+@pytest.fixture(scope="session")
+def torch_gpu():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    torch.cuda.init()
+    return torch
+
+
+@pytest.fixture(scope="session")
+def hip(native, torch_gpu):
+    """Native library on a GPU machine; device memory comes from torch."""
+    L = native.lib()
+    native.check(L.spinn_hip_init(0), "spinn_hip_init")
+    return native

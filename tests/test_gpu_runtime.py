@@ -1,0 +1,76 @@
+"""End-to-end GPU parity: ENNF models through spinn_load / spinn_plan / spinn_run
+(every conv, Gemm and glue op on the device, activations in one HBM arena)
+against the oracle's CPU run of the same file and input."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from spinn_amd import models
+from spinn_amd import native as N
+from spinn_amd.runtime import Session
+from tests.conftest import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_both(tmp_path, g, x, name, policy=N.POLICY_AUTO, graph=False, winograd_oracle=False):
+    path = g.write(tmp_path / f"{name}.ennf")
+    out_shape = g.dims(g.outputs[0])
+    with Session(path, policy=policy, graph=graph) as s:
+        y = s.run(x)
+        y2 = s.run(x)  # a second run over the same arena must reproduce the first
+    ref = O.Model(path, winograd=winograd_oracle).run(x, out_shape)
+    return y, y2, ref
+
+
+def test_conv_bn_relu_model(hip, tmp_path):
+    g, x = models.conv_bn_relu(seed=0)
+    y, y2, ref = _run_both(tmp_path, g, x, "cfg0")
+    assert_parity(y, ref, what="conv+bn+relu")
+    assert np.array_equal(y, y2)
+
+
+@pytest.mark.parametrize("mnk", models.GEMM_SWEEP[:3], ids=str)
+def test_gemm_model(hip, tmp_path, mnk):
+    g, a = models.gemm_model(*mnk, seed=1)
+    y, _, ref = _run_both(tmp_path, g, a, "gemm")
+    assert_parity(y, ref, what=f"gemm {mnk}")
+
+
+def test_vgg_stack_small(hip, tmp_path):
+    sched = [(16, 32), (16, 32), (32, 16), (32, 16)]
+    g, x = models.vgg_stack(batch=2, seed=3, in_c=16, schedule=sched)
+    y, _, ref = _run_both(tmp_path, g, x, "vgg_small")
+    assert_parity(y, ref, what="vgg small")
+
+
+def test_vgg_stack_winograd_policy(hip, tmp_path):
+    sched = [(32, 28), (32, 28), (64, 14), (64, 14)]
+    g, x = models.vgg_stack(batch=2, seed=4, in_c=32, schedule=sched)
+    y, _, ref = _run_both(tmp_path, g, x, "vgg_wino", policy=N.POLICY_WINOGRAD)
+    assert_parity(y, ref, what="vgg winograd vs im2col oracle")
+
+
+def test_resnet50_b1(hip, tmp_path):
+    g, x = models.resnet(batch=1, seed=5, blocks=models.RESNET50_BLOCKS, hw=96)
+    y, y2, ref = _run_both(tmp_path, g, x, "r50")
+    assert_parity(y, ref, what="resnet50@96 b1")
+    assert np.array_equal(y, y2)
+
+
+def test_resnet101_b1(hip, tmp_path):
+    g, x = models.resnet101(batch=1, seed=0)
+    y, _, ref = _run_both(tmp_path, g, x, "r101")
+    print(f"[r101 b1] |ref|max={np.abs(ref).max():.3e}", flush=True)
+    assert_parity(y, ref, what="resnet101 b1")
+
+
+def test_resnet101_b1_graph_replay(hip, tmp_path):
+    g, x = models.resnet101(batch=1, seed=0)
+    path = g.write(tmp_path / "r101g.ennf")
+    with Session(path) as s:
+        y_eager = s.run(x)
+    with Session(path, graph=True) as s:
+        outs = [s.run(x) for _ in range(3)]
+    for o in outs:
+        assert np.array_equal(o, y_eager)
