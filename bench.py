@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Benchmark: ResNet-101 v1.5 fp32 forward on one MI355X through the ENNF runtime.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one forward pass of ResNet-101 (batch 32, 224x224, random-init with
+BN folded) through spinn_run over a single HBM arena, with the input already
+resident in HBM (spinn_run_resident; the node loop is replayed from a HIP
+graph). Prints ONE JSON line:
+
+  value             images/s at batch 32 (whole job = the one GPU)
+  images_per_s_b1   images/s at batch 1 (same protocol)
+  roofline          the implicit-GEMM conv kernel: direct-conv FLOPs of the
+                    layers it runs / their summed device time, from HIP events
+                    recorded around every node on the runtime's stream over
+                    K profiled steps, against the 157.3 TFLOP/s fp32 MFMA peak
+  conv_*            the same aggregate over every conv layer (Winograd layers
+                    credited at the direct-conv FLOP count)
+  cpu_baseline      the reference's own CPU runtime (or the oracle's
+                    restatement when the reference build is absent) on this
+                    host's cores, ResNet-101 batch 1, a bounded sample
+
+Per-layer GFLOP/s and % of peak go to gpurun_out/bench_layers.json.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "conv-layer fp32 GFLOP/s (% MFMA peak); ResNet-101 images/sec @ b1/b32, 1 GPU"
+PEAK_FP32_MFMA = 157.3e12  # MI355X dense fp32 matrix peak, FLOP/s
+ALGO_NAMES = {1: "implicit_gemm", 2: "winograd", 3: "direct"}
+
+
+def host_threads() -> int:
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return n
+
+
+def cpu_baseline(model_b1: Path, in_shape, out_shape, seconds: float) -> dict | None:
+    kind = "reference" if (ROOT / "oracle" / "_ref" / "libspinn_ref.so").exists() else "port"
+    threads = host_threads()
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads))
+    cmd = [sys.executable, "-m", "oracle.cpu_bench", "--kind", kind, "--model", str(model_b1),
+           "--in-shape", ",".join(map(str, in_shape)), "--out-shape", ",".join(map(str, out_shape)),
+           "--seconds", str(seconds)]
+    try:
+        r = subprocess.run(cmd, cwd=ROOT, env=env, capture_output=True, text=True, timeout=seconds * 6 + 120)
+    except subprocess.TimeoutExpired:
+        return None
+    if r.returncode != 0:
+        print(r.stderr[-2000:], file=sys.stderr)
+        return None
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    ips = res["batch"] / (res["avg_ms"] / 1e3)
+    return {"value": round(ips, 3), "unit": "images/s", "cores": threads, "kind": kind,
+            "sample": (f"ResNet-101 batch {res['batch']} forward, {res['runs']} runs after 3 warm-up "
+                       f"(reference CLI protocol), ~{seconds:.0f} s budget, OpenMP {threads} threads; "
+                       f"best {res['best_ms']:.1f} ms, mean {res['avg_ms']:.1f} ms per image")}
+
+
+def conv_table(g):
+    """Per Conv node: (node index, descriptor fields, direct-conv FLOPs)."""
+    from spinn_amd import ennf as E
+    rows = []
+    for i, nd in enumerate(g.nodes):
+        if nd.op != E.OP_CONV:
+            continue
+        p = E.unpack_conv_params(nd.params)
+        n, c, h, w = g.dims(nd.inputs[0])
+        oc, cg, kh, kw = g.dims(nd.inputs[1])
+        _, _, oh, ow = g.dims(nd.outputs[0])
+        rows.append(dict(node=i, n=n, c=c, h=h, w=w, oc=oc, oh=oh, ow=ow, kh=kh, kw=kw, sh=p["strides"][0],
+                         sw=p["strides"][1], ph=p["pads"][0], pw=p["pads"][1], group=p["group"] or 1,
+                         act=p["act"], flops=2.0 * n * oc * oh * ow * cg * kh * kw))
+    return rows
+
+
+def algo_of(N, r, policy) -> int:
+    import ctypes as C
+    d = N.ConvDesc(r["n"], r["c"], r["h"], r["w"], r["oc"], r["oh"], r["ow"], r["kh"], r["kw"], r["sh"], r["sw"],
+                   r["ph"], r["pw"], r["group"], r["act"], 0, 0)
+    a = N.lib().spinn_hip_conv_select_algo(C.byref(d))
+    if a == N.ALGO_WINOGRAD and policy == N.POLICY_IGEMM:
+        return N.ALGO_IMPLICIT_GEMM
+    if a == N.ALGO_IMPLICIT_GEMM and policy == N.POLICY_WINOGRAD and r["kh"] == 3 and r["kw"] == 3 \
+            and r["sh"] == 1 and r["sw"] == 1 and r["group"] == 1:
+        return N.ALGO_WINOGRAD
+    return a
+
+
+def time_steps(sess, steps: int, warmup: int) -> float:
+    for _ in range(warmup):
+        sess.run_resident()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        sess.run_resident()  # returns after the runtime's stream is idle
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--policy", choices=["auto", "igemm", "winograd"], default="auto")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="launch nodes one by one (for profilers)")
+    ap.add_argument("--layers-out", default=str(ROOT / "gpurun_out" / "bench_layers.json"))
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
+              "(the path shards by batch with no collective; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    from spinn_amd import models
+    from spinn_amd import native as N
+    from spinn_amd.runtime import Session
+
+    policy = {"auto": N.POLICY_AUTO, "igemm": N.POLICY_IGEMM, "winograd": N.POLICY_WINOGRAD}[a.policy]
+    tmp = Path(tempfile.mkdtemp(prefix="spinn_bench_"))
+    t_gen = time.perf_counter()
+    g1, x1 = models.resnet101(batch=1, seed=0)
+    p1 = g1.write(tmp / "r101_b1.ennf")
+    gB, xB = models.resnet101(batch=a.batch, seed=0)
+    pB = gB.write(tmp / f"r101_b{a.batch}.ennf")
+    print(f"[bench] models written in {time.perf_counter() - t_gen:.1f}s", file=sys.stderr, flush=True)
+
+    # CPU baseline first, before this process touches the GPU.
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(p1, g1.dims(g1.inputs[0]), g1.dims(g1.outputs[0]), a.cpu_seconds)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    L = N.lib()
+    N.check(L.spinn_hip_init(0), "spinn_hip_init")
+
+    # ---- batch B, graph replay, input resident ----
+    sB = Session(pB, policy=policy, graph=not a.no_graph)
+    sB.upload_input(xB)
+    ms_B = time_steps(sB, a.steps, a.warmup)
+    print(f"[bench] b{a.batch}: {ms_B:.3f} ms/step", file=sys.stderr, flush=True)
+    # PCIe-inclusive rate (host input in, logits out) for reference
+    t0 = time.perf_counter()
+    for _ in range(max(3, a.steps // 4)):
+        sB.run(xB)
+    ms_B_h2d = (time.perf_counter() - t0) / max(3, a.steps // 4) * 1e3
+    sB.close()
+
+    # ---- per-node device time from HIP events around every node ----
+    L.spinn_set_profiling(1)
+    sP = Session(pB, policy=policy, graph=False)
+    sP.upload_input(xB)
+    for _ in range(2):
+        sP.run_resident()
+    acc = None
+    for _ in range(a.steps):
+        sP.run_resident()
+        t = sP.node_times()
+        acc = t if acc is None else acc + t
+    node_ms = acc / a.steps
+    sP.close()
+    L.spinn_set_profiling(0)
+
+    # ---- batch 1 ----
+    s1 = Session(p1, policy=policy, graph=not a.no_graph)
+    s1.upload_input(x1)
+    ms_1 = time_steps(s1, max(a.steps, 50), a.warmup)
+    s1.close()
+    print(f"[bench] b1: {ms_1:.3f} ms/step", file=sys.stderr, flush=True)
+
+    rows = conv_table(gB)
+    layers = []
+    tot_f = tot_t = ig_f = ig_t = 0.0
+    n_ig = 0
+    for r in rows:
+        ms = float(node_ms[r["node"]])
+        algo = algo_of(N, r, policy)
+        gf = r["flops"] / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        layers.append(dict(node=r["node"], shape=f"{r['c']}x{r['h']}x{r['w']}->{r['oc']}x{r['oh']}x{r['ow']}",
+                           k=f"{r['kh']}x{r['kw']}/s{r['sh']}", act=r["act"], algo=ALGO_NAMES.get(algo, str(algo)),
+                           gflop=r["flops"] / 1e9, ms=ms, gflops=gf, frac_peak=gf * 1e9 / PEAK_FP32_MFMA))
+        tot_f += r["flops"]
+        tot_t += ms
+        if algo == N.ALGO_IMPLICIT_GEMM:
+            ig_f += r["flops"]
+            ig_t += ms
+            n_ig += 1
+    all_ms = float(node_ms.sum())
+    conv_tflops = tot_f / (tot_t * 1e-3) / 1e12
+    ig_tflops = ig_f / (ig_t * 1e-3) / 1e12 if ig_t > 0 else 0.0
+    out_layers = Path(a.layers_out)
+    out_layers.parent.mkdir(parents=True, exist_ok=True)
+    out_layers.write_text(json.dumps(dict(batch=a.batch, policy=a.policy, node_ms_total=all_ms,
+                                          conv_ms_total=tot_t, layers=layers), indent=1))
+
+    ips = a.batch / (ms_B * 1e-3)
+    line = {
+        "metric": METRIC,
+        "value": round(ips, 2),
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_B, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random-init ResNet-101, BN folded; input U[-1,1])",
+        "config": {"workload": f"ResNet-101 v1.5 fp32 forward, batch {a.batch}, 3x224x224, ENNF through "
+                               f"spinn_run over one HBM arena, input resident, "
+                               f"{'per-node launches' if a.no_graph else 'HIP-graph replay'}",
+                   "batch": a.batch, "image": [3, 224, 224], "conv_layers": len(rows), "conv_policy": a.policy},
+        "images_per_s_b1": round(1e3 / ms_1, 2),
+        "ms_per_step_b1": round(ms_1, 4),
+        "images_per_s_with_host_copies": round(a.batch / (ms_B_h2d * 1e-3), 2),
+        "conv_tflops_aggregate": round(conv_tflops, 3),
+        "conv_frac_mfma_peak": round(conv_tflops * 1e12 / PEAK_FP32_MFMA, 4),
+        "conv_share_of_node_time": round(tot_t / all_ms, 4) if all_ms > 0 else None,
+        "roofline": {"bound": "mfma", "achieved": round(ig_tflops, 3), "peak": PEAK_FP32_MFMA / 1e12,
+                     "unit": "TFLOP/s", "frac": round(ig_tflops * 1e12 / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "kernel": f"conv_igemm_kernel (implicit-GEMM conv, {n_ig} layers, batch {a.batch})"},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -141,6 +141,9 @@ int spinn_set_graph_mode(SpinnContext *ctx, int enable);
  * out for the chosen algorithm at plan time). Returns -1 after plan. */
 int spinn_set_conv_policy(SpinnContext *ctx, int policy);
 
+/* Turn per-node HIP-event timing on or off (overrides SPINN_PROFILE). */
+void spinn_set_profiling(int on);
+
 /* Per-node device time of the last run when SPINN_PROFILE=1 (milliseconds,
  * from HIP events around each node). Returns the number of nodes written. */
 int spinn_node_times(SpinnContext *ctx, float *ms_out, int max_nodes);

@@ -274,6 +274,8 @@ const char *spinn_hip_error_string(int code) {
     return "unknown error";
 }
 
+void spinn_hip_tune_force_tiles(int bm, int bn, int split) { force_tiles(bm, bn, split); }
+
 const char *spinn_hip_version(void) { return "spinn_amd 0.1 gfx950 fp32-mfma"; }
 
 } // extern "C"

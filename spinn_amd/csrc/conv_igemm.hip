@@ -25,12 +25,12 @@ struct ConvKArgs {
     int ldw;
     int M, K;          // per group
     ConvGeom geom;
-    float *y;
-    const float *bias;
-    const float *res;
+    float *__restrict__ y;
+    const float *__restrict__ bias;
+    const float *__restrict__ res;
     int act;
     int OC, OHW;
-    float *ws;         // split-K partials [split][OC][ntot]
+    float *__restrict__ ws; // split-K partials [split][OC][ntot]
     int k_chunk;       // K per split (multiple of kBK)
 };
 
@@ -55,12 +55,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
     const int k_end = SPLIT ? min(a.K, k_begin + a.k_chunk) : a.K;
 
     KMajorLoader<BM, BK, true> al;
-    al.src = a.wpk + group * a.wpk_group_stride + m0;
-    al.ld = a.ldw;
-    al.t_valid = a.ldw - m0;
-    al.k_end = k_end;
+    al.init(a.wpk + group * a.wpk_group_stride, (uint32_t)a.K * (uint32_t)a.ldw * 4u, (uint32_t)a.ldw, m0, a.ldw);
     BLoader bl;
     bl.init(a.geom, n0, group, tid, k_end);
+    KMajorLoader<BM, BK, true> al1 = al;
+    BLoader bl1 = bl;
 
     f32x16 acc[WT::TM][WT::TN];
 #pragma unroll
@@ -71,38 +70,21 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int nslices = (k_end - k_begin + BK - 1) / BK;
-    if (nslices > 0) {
-        al.fetch(k_begin, tid);
-        bl.fetch(k_begin, tid);
-        al.commit(As[0], tid);
-        bl.commit(Bs[0], tid);
-        __syncthreads();
-        for (int s = 0; s < nslices; ++s) {
-            const int cur = s & 1;
-            const bool more = s + 1 < nslices;
-            if (more) {
-                al.fetch(k_begin + (s + 1) * BK, tid);
-                bl.fetch(k_begin + (s + 1) * BK, tid);
-            }
-            mma_slice<BM, BN, BK>(As[cur], Bs[cur], acc, wm0, wn0, lane);
-            if (more) {
-                al.commit(As[cur ^ 1], tid);
-                bl.commit(Bs[cur ^ 1], tid);
-            }
-            __syncthreads();
-        }
-    }
+    gemm_mainloop<BM, BN, BK>(al, bl, al1, bl1, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0);
 
     // Epilogue: lane owns column jcol = n0 + wn0 + j*32 + lane%32 and rows
-    // m0 + wm0 + i*32 + 8*(r/4) + 4*(lane/32) + r%4.
+    // m0 + wm0 + i*32 + 8*(r/4) + 4*(lane/32) + r%4. All bias and residual
+    // values of a column block are loaded before any store so the loads are in
+    // flight together instead of each waiting behind the previous store.
     const int h = lane >> 5;
     const int l32 = lane & 31;
     const int ntot = a.geom.ntot;
+    constexpr int NR = WT::TM * 16;
+    if constexpr (SPLIT) {
 #pragma unroll
-    for (int j = 0; j < WT::TN; ++j) {
-        const int jcol = n0 + wn0 + j * 32 + l32;
-        if (jcol >= ntot) continue;
-        if constexpr (SPLIT) {
+        for (int j = 0; j < WT::TN; ++j) {
+            const int jcol = n0 + wn0 + j * 32 + l32;
+            if (jcol >= ntot) continue;
             float *wsz = a.ws + (int64_t)z * a.OC * ntot + jcol;
 #pragma unroll
             for (int i = 0; i < WT::TM; ++i)
@@ -111,24 +93,32 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
                     const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                     if (m < a.M) wsz[(int64_t)m * ntot] = acc[i][j][r];
                 }
-        } else {
+        }
+    } else {
+        float bv[NR];
+#pragma unroll
+        for (int q = 0; q < NR; ++q) {
+            const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
+            bv[q] = (a.bias && m < a.M) ? a.bias[group * a.M + m] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < WT::TN; ++j) {
+            const int jcol = n0 + wn0 + j * 32 + l32;
+            if (jcol >= ntot) continue;
             const int img = jcol / a.OHW;
             const int p = jcol - img * a.OHW;
-            const int64_t ybase = (int64_t)img * a.OC * a.OHW + p;
+            const int64_t ybase = ((int64_t)img * a.OC + (int64_t)group * a.M) * a.OHW + p;
+            float rv[NR];
 #pragma unroll
-            for (int i = 0; i < WT::TM; ++i)
+            for (int q = 0; q < NR; ++q) {
+                const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
+                rv[q] = (a.res && m < a.M) ? a.res[ybase + (int64_t)m * a.OHW] : 0.f;
+            }
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < a.M) {
-                        const int oc = group * a.M + m;
-                        const int64_t idx = ybase + (int64_t)oc * a.OHW;
-                        float v = acc[i][j][r];
-                        if (a.bias) v += a.bias[oc];
-                        if (a.res) v += a.res[idx];
-                        a.y[idx] = apply_act(v, a.act);
-                    }
-                }
+            for (int q = 0; q < NR; ++q) {
+                const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
+                if (m < a.M) a.y[ybase + (int64_t)m * a.OHW] = apply_act(acc[q >> 4][j][q & 15] + bv[q] + rv[q], a.act);
+            }
         }
     }
 }
@@ -256,7 +246,10 @@ int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, c
     a.K = (d->c / d->group) * d->kh * d->kw;
     a.wpk = packed;
     a.wpk_group_stride = (int64_t)a.K * a.ldw;
-    a.geom = ConvGeom{x, d->c, d->h, d->w, d->c / d->group, d->oh, d->ow, d->kh, d->kw,
+    const uint64_t x_bytes = (uint64_t)d->n * d->c * d->h * d->w * sizeof(float);
+    const uint64_t w_bytes = (uint64_t)igemm_packed_floats(d) * sizeof(float);
+    if (x_bytes > kMaxOperandBytes || w_bytes > kMaxOperandBytes) return SPINN_HIP_EUNSUPPORTED;
+    a.geom = ConvGeom{x, (uint32_t)x_bytes, d->c, d->h, d->w, d->c / d->group, d->oh, d->ow, d->kh, d->kw,
                       d->sh, d->sw, d->ph, d->pw, d->n * d->oh * d->ow};
     a.y = y;
     a.bias = bias;

@@ -16,14 +16,16 @@ namespace spinn {
 // Gemm
 // ---------------------------------------------------------------------------
 struct GemmKArgs {
-    const float *a, *b, *c;
+    const float *__restrict__ a;
+    const float *__restrict__ b;
+    const float *__restrict__ c;
     int64_t lda, ldb;
     int64_t stride_a, stride_b, stride_y;
     int M, N, K;
     int c_mode;
     float alpha, beta;
-    float *y;
-    float *ws;
+    float *__restrict__ y;
+    float *__restrict__ ws;
     int k_chunk;
 };
 
@@ -49,23 +51,21 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmKArgs a) {
 
     ALoader al;
     BLoader bl;
-    // A tile rows are m: KMajor source a[k*lda + m], RowK source a[m*lda + k].
+    // A tile rows are m: KMajor source a[k*lda + m] (K rows), RowK source a[m*lda + k] (M rows).
+    const float *abase = a.a + batch * a.stride_a;
+    const float *bbase = a.b + batch * a.stride_b;
     if constexpr (ALoader::kIsKMajor) {
-        al.src = a.a + batch * a.stride_a + m0;
+        al.init(abase, (uint32_t)(a.K * a.lda * 4), (uint32_t)a.lda, m0, a.M);
     } else {
-        al.src = a.a + batch * a.stride_a + (int64_t)m0 * a.lda;
+        al.init(abase, (uint32_t)(a.M * a.lda * 4), (uint32_t)a.lda, m0, a.M, k_end);
     }
-    al.ld = a.lda;
-    al.t_valid = a.M - m0;
-    al.k_end = k_end;
     if constexpr (BLoader::kIsKMajor) {
-        bl.src = a.b + batch * a.stride_b + n0;
+        bl.init(bbase, (uint32_t)(a.K * a.ldb * 4), (uint32_t)a.ldb, n0, a.N);
     } else {
-        bl.src = a.b + batch * a.stride_b + (int64_t)n0 * a.ldb;
+        bl.init(bbase, (uint32_t)(a.N * a.ldb * 4), (uint32_t)a.ldb, n0, a.N, k_end);
     }
-    bl.ld = a.ldb;
-    bl.t_valid = a.N - n0;
-    bl.k_end = k_end;
+    ALoader al1 = al;
+    BLoader bl1 = bl;
 
     f32x16 acc[WT::TM][WT::TN];
 #pragma unroll
@@ -76,49 +76,40 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmKArgs a) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int nslices = (k_end - k_begin + BK - 1) / BK;
-    if (nslices > 0) {
-        al.fetch(k_begin, tid);
-        bl.fetch(k_begin, tid);
-        al.commit(As[0], tid);
-        bl.commit(Bs[0], tid);
-        __syncthreads();
-        for (int s = 0; s < nslices; ++s) {
-            const int cur = s & 1;
-            const bool more = s + 1 < nslices;
-            if (more) {
-                al.fetch(k_begin + (s + 1) * BK, tid);
-                bl.fetch(k_begin + (s + 1) * BK, tid);
-            }
-            mma_slice<BM, BN, BK>(As[cur], Bs[cur], acc, wm0, wn0, lane);
-            if (more) {
-                al.commit(As[cur ^ 1], tid);
-                bl.commit(Bs[cur ^ 1], tid);
-            }
-            __syncthreads();
-        }
-    }
+    gemm_mainloop<BM, BN, BK>(al, bl, al1, bl1, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0);
 
+    // Epilogue: C values of a column block are loaded before any store.
     const int h = lane >> 5;
     const int l32 = lane & 31;
+    constexpr int NR = WT::TM * 16;
 #pragma unroll
     for (int j = 0; j < WT::TN; ++j) {
         const int n = n0 + wn0 + j * 32 + l32;
         if (n >= a.N) continue;
+        if constexpr (SPLIT) {
 #pragma unroll
-        for (int i = 0; i < WT::TM; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m >= a.M) continue;
-                if constexpr (SPLIT) {
-                    a.ws[((int64_t)z * a.M + m) * a.N + n] = acc[i][j][r];
-                } else {
-                    float v = a.alpha * acc[i][j][r];
-                    if (a.c_mode == 1) v += a.beta * a.c[n];
-                    else if (a.c_mode == 2) v += a.beta * a.c[(int64_t)m * a.N + n];
-                    a.y[batch * a.stride_y + (int64_t)m * a.N + n] = v;
-                }
+            for (int q = 0; q < NR; ++q) {
+                const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
+                if (m < a.M) a.ws[((int64_t)z * a.M + m) * a.N + n] = acc[q >> 4][j][q & 15];
             }
+        } else {
+            float cv[NR];
+#pragma unroll
+            for (int q = 0; q < NR; ++q) {
+                const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
+                float c = 0.f;
+                if (m < a.M) {
+                    if (a.c_mode == 1) c = a.c[n];
+                    else if (a.c_mode == 2) c = a.c[(int64_t)m * a.N + n];
+                }
+                cv[q] = c;
+            }
+#pragma unroll
+            for (int q = 0; q < NR; ++q) {
+                const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
+                if (m < a.M) a.y[batch * a.stride_y + (int64_t)m * a.N + n] = a.alpha * acc[q >> 4][j][q & 15] + a.beta * cv[q];
+            }
+        }
     }
 }
 
@@ -228,6 +219,10 @@ int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const fl
     a.alpha = d->alpha;
     a.beta = d->beta;
     a.y = Y;
+    // Buffer descriptors address at most 2 GiB per operand.
+    const uint64_t a_bytes = (uint64_t)d->m * d->k * sizeof(float);
+    const uint64_t b_bytes = (uint64_t)d->n * d->k * sizeof(float);
+    if (a_bytes > kMaxOperandBytes || b_bytes > kMaxOperandBytes) return SPINN_HIP_EUNSUPPORTED;
     // Vector loads need 16-byte aligned rows in every batch entry.
     const bool va = aligned16(A) && (a.lda % 4 == 0) && (batch == 1 || d->stride_a % 4 == 0);
     const bool vb = aligned16(B) && (a.ldb % 4 == 0) && (batch == 1 || d->stride_b % 4 == 0);

@@ -273,6 +273,8 @@ static void prof_free(SpinnContext *ctx) {
 }
 
 /* Top-12 op types by accumulated device time (SPINN/run_time/spinn_runtime.c:269-296). */
+void spinn_set_profiling(int on) { g_prof_enabled = on ? 1 : 0; }
+
 void spinn_profile_dump(void) {
     if (g_prof_enabled <= 0) return;
     double total = 0;

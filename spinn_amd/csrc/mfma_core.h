@@ -4,9 +4,7 @@
 // tile. Each wave owns a (BM/2) x (BN/2) sub-tile made of 32x32 blocks computed
 // with v_mfma_f32_32x32x2f32 (4096 flop per instruction, 64 cycles, the full
 // fp32 matrix rate of a SIMD). The K loop stages BK-deep slices of both
-// operands through LDS, double buffered: the next slice is fetched into
-// registers while the current one feeds the matrix cores, then written to the
-// other LDS buffer, one barrier per slice.
+// operands through two LDS buffers and two register stages (gemm_mainloop).
 //
 // LDS layout of both operands is k-major, [BK][BT + PAD] with T (the M or N
 // index) contiguous, so the operand fetch of an MFMA (lane l reads element
@@ -45,76 +43,72 @@ struct WaveTiling {
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32x32");
 };
 
-// acc += A_lds[k-slice] x B_lds[k-slice] for one BK slice.
-template <int BM, int BN, int BK>
-__device__ __forceinline__ void mma_slice(const float *__restrict__ As, const float *__restrict__ Bs,
-                                          f32x16 (&acc)[WaveTiling<BM, BN>::TM][WaveTiling<BM, BN>::TN],
-                                          int wm0, int wn0, int lane) {
-    constexpr int SA = LdsPad<BM>::stride;
-    constexpr int SB = LdsPad<BN>::stride;
-    constexpr int TM = WaveTiling<BM, BN>::TM;
-    constexpr int TN = WaveTiling<BM, BN>::TN;
-    const int h = lane >> 5;
-    const int l32 = lane & 31;
-    const float *ap = As + h * SA + wm0 + l32;
-    const float *bp = Bs + h * SB + wn0 + l32;
-#pragma unroll
-    for (int s = 0; s < BK / 2; ++s) {
-        float a[TM], b[TN];
-#pragma unroll
-        for (int i = 0; i < TM; ++i) a[i] = ap[(2 * s) * SA + i * 32];
-#pragma unroll
-        for (int j = 0; j < TN; ++j) b[j] = bp[(2 * s) * SB + j * 32];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Tile loaders. Each stages a BK x BT slice of one operand: fetch() issues the
 // global loads into registers for slice [k0, k0+BK), commit() writes them to
-// a k-major LDS buffer. Elements outside [0,T) x [k_begin,k_end) are zero.
+// a k-major LDS buffer.
+//
+// All loads are raw buffer loads through a resource descriptor whose size is
+// the operand's extent: an offset at or past it returns 0 in hardware. Every
+// element that must read as zero (conv padding, tile edges, the K tail) gets
+// the offset kOOB instead of a branch, so the loads are unconditional and the
+// compiler can wait on exactly the pipeline stage it needs.
 // ---------------------------------------------------------------------------
+constexpr uint32_t kOOB = 0x80000000u;         // any offset >= the operand's byte size
+constexpr uint32_t kMaxOperandBytes = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, uint32_t bytes) {
+    // dword3 0x00020000: 32-bit data format, the gfx9-family raw-buffer setting
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float buf_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ f32x4 buf_f32x4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
 
 // Source laid out [K][ld] with the tile index contiguous (packed conv weights
-// W^T, a transposed Gemm A, a plain Gemm B). VEC: float4 along T, which needs
-// ld % 4 == 0, a 16-byte aligned base and T padded to a multiple of 4.
+// W^T, a transposed Gemm A, a plain Gemm B); `bytes` covers rows [0, K).
+// VEC: float4 along T, which needs ld % 4 == 0, a 16-byte aligned base and a
+// tile width T that is a multiple of 4 (or zero-padded to one).
 template <int BT, int BK, bool VEC>
 struct KMajorLoader {
+    static constexpr bool kIsKMajor = true;
     static constexpr int S = LdsPad<BT>::stride;
     static constexpr int NV = VEC ? (BK * BT / 4) / kThreads : (BK * BT) / kThreads;
     static_assert(NV >= 1, "tile too small for 256 threads");
-    const float *src; // already offset to (batch/group) and tile start t0
-    int64_t ld;
-    int t_valid;      // T - t0 (elements of the tile that exist)
-    int k_end;
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t ld;
+    uint32_t t0;  // first tile index (m0 or n0)
+    int t_valid;  // elements of the tile that exist: T - t0
     f32x4 rv[VEC ? NV : 1];
     float rs[VEC ? 1 : NV];
 
+    __device__ __forceinline__ void init(const float *base, uint32_t bytes, uint32_t ld_, int t0_, int t_total) {
+        rsrc = make_rsrc(base, bytes);
+        ld = ld_;
+        t0 = (uint32_t)t0_;
+        t_valid = t_total - t0_;
+    }
     __device__ __forceinline__ void fetch(int k0, int tid) {
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                int c = tid + i * kThreads;
-                int k = c / (BT / 4);
-                int t = (c % (BT / 4)) * 4;
-                int kk = k0 + k;
-                if (kk < k_end && t < t_valid)
-                    rv[i] = *reinterpret_cast<const f32x4 *>(src + (int64_t)kk * ld + t);
-                else
-                    rv[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const int c = tid + i * kThreads;
+                const int k = c / (BT / 4);
+                const int t = (c % (BT / 4)) * 4;
+                const uint32_t off = t < t_valid ? ((uint32_t)(k0 + k) * ld + t0 + t) * 4u : kOOB;
+                rv[i] = buf_f32x4(rsrc, off);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                int e = tid + i * kThreads;
-                int k = e / BT;
-                int t = e % BT;
-                int kk = k0 + k;
-                rs[i] = (kk < k_end && t < t_valid) ? src[(int64_t)kk * ld + t] : 0.f;
+                const int e = tid + i * kThreads;
+                const int k = e / BT;
+                const int t = e % BT;
+                const uint32_t off = t < t_valid ? ((uint32_t)(k0 + k) * ld + t0 + t) * 4u : kOOB;
+                rs[i] = buf_f32(rsrc, off);
             }
         }
     }
@@ -122,15 +116,13 @@ struct KMajorLoader {
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                int c = tid + i * kThreads;
-                int k = c / (BT / 4);
-                int t = (c % (BT / 4)) * 4;
-                *reinterpret_cast<f32x4 *>(lds + k * S + t) = rv[i];
+                const int c = tid + i * kThreads;
+                *reinterpret_cast<f32x4 *>(lds + (c / (BT / 4)) * S + (c % (BT / 4)) * 4) = rv[i];
             }
         } else {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                int e = tid + i * kThreads;
+                const int e = tid + i * kThreads;
                 lds[(e / BT) * S + (e % BT)] = rs[i];
             }
         }
@@ -138,41 +130,47 @@ struct KMajorLoader {
 };
 
 // Source laid out [T][ld] with K contiguous (a plain Gemm A, a transposed
-// Gemm B). Each thread reads 4 consecutive k of one row (float4 when VEC:
-// ld % 4 == 0 and aligned base) and scatters them to 4 LDS rows; consecutive
-// lanes take consecutive rows so the LDS writes are conflict-free.
+// Gemm B); `bytes` covers rows [0, T). Each thread reads 4 consecutive k of
+// one row (float4 when VEC: ld % 4 == 0 and an aligned base) and scatters
+// them to 4 LDS rows; consecutive lanes take consecutive rows so the LDS
+// writes are conflict-free. k >= k_end reads 0.
 template <int BT, int BK, bool VEC>
 struct RowKLoader {
+    static constexpr bool kIsKMajor = false;
     static constexpr int S = LdsPad<BT>::stride;
-    static constexpr int NQ = (BK / 4) * BT / kThreads; // float4 groups per thread
+    static constexpr int NQ = (BK / 4) * BT / kThreads;
     static_assert(NQ >= 1 && BK % 4 == 0, "tile too small");
-    const float *src;
-    int64_t ld;
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t ld;
+    uint32_t t0;
     int t_valid;
     int k_end;
     f32x4 r[NQ];
 
+    __device__ __forceinline__ void init(const float *base, uint32_t bytes, uint32_t ld_, int t0_, int t_total,
+                                         int kend) {
+        rsrc = make_rsrc(base, bytes);
+        ld = ld_;
+        t0 = (uint32_t)t0_;
+        t_valid = t_total - t0_;
+        k_end = kend;
+    }
     __device__ __forceinline__ void fetch(int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
-            int c = tid + i * kThreads;
-            int t = c % BT;
-            int kq = (c / BT) * 4;
-            int kk = k0 + kq;
-            const float *p = src + (int64_t)t * ld + kk;
-            if (t < t_valid && kk + 3 < k_end) {
-                if constexpr (VEC) {
-                    r[i] = *reinterpret_cast<const f32x4 *>(p);
-                } else {
-                    r[i] = f32x4{p[0], p[1], p[2], p[3]};
-                }
+            const int c = tid + i * kThreads;
+            const int t = c % BT;
+            const int kk = k0 + (c / BT) * 4;
+            const uint32_t row = (t0 + t) * ld;
+            if constexpr (VEC) {
+                // ld % 4 == 0 makes k_end - kk a multiple of 4 too, except at a
+                // split-K chunk end, which is a multiple of 16
+                r[i] = buf_f32x4(rsrc, (t < t_valid && kk < k_end) ? (row + kk) * 4u : kOOB);
             } else {
-                f32x4 v = {0.f, 0.f, 0.f, 0.f};
-                if (t < t_valid) {
-                    if (kk + 0 < k_end) v[0] = p[0];
-                    if (kk + 1 < k_end) v[1] = p[1];
-                    if (kk + 2 < k_end) v[2] = p[2];
-                }
+                f32x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[e] = buf_f32(rsrc, (t < t_valid && kk + e < k_end) ? (row + kk + e) * 4u : kOOB);
                 r[i] = v;
             }
         }
@@ -180,9 +178,9 @@ struct RowKLoader {
     __device__ __forceinline__ void commit(float *lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
-            int c = tid + i * kThreads;
-            int t = c % BT;
-            int kq = (c / BT) * 4;
+            const int c = tid + i * kThreads;
+            const int t = c % BT;
+            const int kq = (c / BT) * 4;
             lds[(kq + 0) * S + t] = r[i][0];
             lds[(kq + 1) * S + t] = r[i][1];
             lds[(kq + 2) * S + t] = r[i][2];
@@ -195,7 +193,8 @@ struct RowKLoader {
 // pixel (img, oh, ow) = (j / OHW, (j % OHW) / OW, j % OW); row k is a tap
 // (c, kh, kw) of the convolution window.
 struct ConvGeom {
-    const float *x; // input of group 0, image 0
+    const float *x; // input tensor base
+    uint32_t x_bytes;
     int C, H, W;    // full input tensor dims
     int Cg;         // input channels per group
     int OH, OW;
@@ -203,38 +202,46 @@ struct ConvGeom {
     int ntot;       // N * OH * OW
 };
 
+// Per-thread output pixel of a gather loader: element offset of its image
+// (and group) plane and the window origin; `valid` false past the last pixel.
+struct PixelOrigin {
+    uint32_t base;
+    int ih0, iw0;
+    bool valid;
+    __device__ __forceinline__ void init(const ConvGeom &g, int j, int group) {
+        const int ohw = g.OH * g.OW;
+        valid = j < g.ntot;
+        const int jj = valid ? j : 0;
+        const int img = jj / ohw;
+        const int p = jj - img * ohw;
+        const int oh = p / g.OW;
+        const int ow = p - oh * g.OW;
+        ih0 = oh * g.SH - g.PH;
+        iw0 = ow * g.SW - g.PW;
+        base = ((uint32_t)img * g.C + (uint32_t)group * g.Cg) * (uint32_t)(g.H * g.W);
+    }
+};
+
 // im2col gather, K in (c, kh, kw) order - the row order of the reference's
 // im2col (SPINN/run_time/ops/conv/conv2d.c:58-76). Any shape; per element it
-// decomposes k with compile-time KH, KW (KHW = KH*KW, 0 = runtime).
+// decomposes k with compile-time KH, KW when given (0 = runtime).
 template <int BN, int BK, int KHC, int KWC>
 struct Im2colLoader {
     static constexpr int S = LdsPad<BN>::stride;
     static constexpr int NV = BK * BN / kThreads;
     static constexpr int KSTEP = kThreads / BN;
     static_assert(kThreads % BN == 0, "BN must divide 256");
+    __amdgpu_buffer_rsrc_t rsrc;
     ConvGeom g;
-    const float *base; // this thread's image (and group) base, or null if the column is out of range
-    int ih0, iw0;
+    PixelOrigin px;
     int k_end;
     float r[NV];
 
     __device__ __forceinline__ void init(const ConvGeom &geom, int n0, int group, int tid, int kend) {
         g = geom;
+        rsrc = make_rsrc(g.x, g.x_bytes);
         k_end = kend;
-        int j = n0 + (tid % BN);
-        int ohw = g.OH * g.OW;
-        if (j < g.ntot) {
-            int img = j / ohw;
-            int p = j - img * ohw;
-            int oh = p / g.OW;
-            int ow = p - oh * g.OW;
-            ih0 = oh * g.SH - g.PH;
-            iw0 = ow * g.SW - g.PW;
-            base = g.x + ((int64_t)img * g.C + (int64_t)group * g.Cg) * g.H * g.W;
-        } else {
-            base = nullptr;
-            ih0 = iw0 = 0;
-        }
+        px.init(g, n0 + (tid % BN), group);
     }
     __device__ __forceinline__ void fetch(int k0, int tid) {
         const int KH = KHC > 0 ? KHC : g.KH;
@@ -243,19 +250,15 @@ struct Im2colLoader {
         const int kt = tid / BN;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            int k = k0 + kt + i * KSTEP;
-            float v = 0.f;
-            if (base && k < k_end) {
-                int c = k / KHW;
-                int rr = k - c * KHW;
-                int kh = rr / KW;
-                int kw = rr - kh * KW;
-                int ih = ih0 + kh;
-                int iw = iw0 + kw;
-                if ((unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W)
-                    v = base[((int64_t)c * g.H + ih) * g.W + iw];
-            }
-            r[i] = v;
+            const int k = k0 + kt + i * KSTEP;
+            const int c = k / KHW;
+            const int rr = k - c * KHW;
+            const int kh = rr / KW;
+            const int kw = rr - kh * KW;
+            const int ih = px.ih0 + kh;
+            const int iw = px.iw0 + kw;
+            const bool ok = px.valid && k < k_end && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+            r[i] = buf_f32(rsrc, ok ? (px.base + ((uint32_t)c * g.H + ih) * g.W + iw) * 4u : kOOB);
         }
     }
     __device__ __forceinline__ void commit(float *lds, int tid) const {
@@ -267,48 +270,37 @@ struct Im2colLoader {
 };
 
 // im2col gather, K in (kh, kw, c) order; needs Cg % BK == 0 so one BK slice is
-// a single tap (kh, kw) over BK consecutive channels: one bounds check per
-// thread per slice, then BK/KSTEP strided loads.
+// a single tap (kh, kw) over BK consecutive channels: one bounds test per
+// thread per slice, then BK/KSTEP loads strided by one channel plane.
 template <int BN, int BK>
 struct Im2colTapLoader {
     static constexpr int S = LdsPad<BN>::stride;
     static constexpr int NV = BK * BN / kThreads;
     static constexpr int KSTEP = kThreads / BN;
+    __amdgpu_buffer_rsrc_t rsrc;
     ConvGeom g;
-    const float *base;
-    int ih0, iw0;
-    int64_t hw;
+    PixelOrigin px;
+    uint32_t hw;
     float r[NV];
 
     __device__ __forceinline__ void init(const ConvGeom &geom, int n0, int group, int tid, int /*kend*/) {
         g = geom;
-        hw = (int64_t)g.H * g.W;
-        int j = n0 + (tid % BN);
-        int ohw = g.OH * g.OW;
-        if (j < g.ntot) {
-            int img = j / ohw;
-            int p = j - img * ohw;
-            int oh = p / g.OW;
-            int ow = p - oh * g.OW;
-            ih0 = oh * g.SH - g.PH;
-            iw0 = ow * g.SW - g.PW;
-            base = g.x + ((int64_t)img * g.C + (int64_t)group * g.Cg) * hw;
-        } else {
-            base = nullptr;
-            ih0 = iw0 = 0;
-        }
+        rsrc = make_rsrc(g.x, g.x_bytes);
+        hw = (uint32_t)(g.H * g.W);
+        px.init(g, n0 + (tid % BN), group);
     }
     __device__ __forceinline__ void fetch(int k0, int tid) {
         const int tap = k0 / g.Cg;
         const int c0 = k0 - tap * g.Cg;
         const int kh = tap / g.KW;
         const int kw = tap - kh * g.KW;
-        const int ih = ih0 + kh;
-        const int iw = iw0 + kw;
-        const bool ok = base && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
-        const float *p = ok ? base + (int64_t)(c0 + tid / BN) * hw + (int64_t)ih * g.W + iw : nullptr;
+        const int ih = px.ih0 + kh;
+        const int iw = px.iw0 + kw;
+        // taps past the window (fetches beyond the end of K) read zeros too
+        const bool ok = px.valid && kh < g.KH && (unsigned)ih < (unsigned)g.H && (unsigned)iw < (unsigned)g.W;
+        const uint32_t off0 = (px.base + (uint32_t)(c0 + tid / BN) * hw + (uint32_t)ih * g.W + iw) * 4u;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) r[i] = ok ? p[(int64_t)i * KSTEP * hw] : 0.f;
+        for (int i = 0; i < NV; ++i) r[i] = buf_f32(rsrc, ok ? off0 + (uint32_t)(i * KSTEP) * hw * 4u : kOOB);
     }
     __device__ __forceinline__ void commit(float *lds, int tid) const {
         const int kt = tid / BN;
@@ -317,5 +309,106 @@ struct Im2colTapLoader {
         for (int i = 0; i < NV; ++i) lds[(kt + i * KSTEP) * S + n] = r[i];
     }
 };
+
+// Reads all operand fragments of one LDS slice (issued together, so their
+// latency overlaps the MFMAs that follow).
+template <int BM, int BN, int BK>
+__device__ __forceinline__ void load_fragments(const float *__restrict__ As, const float *__restrict__ Bs,
+                                               float (&a)[BK / 2][WaveTiling<BM, BN>::TM],
+                                               float (&b)[BK / 2][WaveTiling<BM, BN>::TN], int wm0, int wn0,
+                                               int lane) {
+    constexpr int SA = LdsPad<BM>::stride;
+    constexpr int SB = LdsPad<BN>::stride;
+    const float *ap = As + (lane >> 5) * SA + wm0 + (lane & 31);
+    const float *bp = Bs + (lane >> 5) * SB + wn0 + (lane & 31);
+#pragma unroll
+    for (int q = 0; q < BK / 2; ++q) {
+#pragma unroll
+        for (int i = 0; i < WaveTiling<BM, BN>::TM; ++i) a[q][i] = ap[(2 * q) * SA + i * 32];
+#pragma unroll
+        for (int j = 0; j < WaveTiling<BM, BN>::TN; ++j) b[q][j] = bp[(2 * q) * SB + j * 32];
+    }
+}
+
+template <int BM, int BN, int BK, int Q0, int Q1>
+__device__ __forceinline__ void mfma_steps(const float (&a)[BK / 2][WaveTiling<BM, BN>::TM],
+                                           const float (&b)[BK / 2][WaveTiling<BM, BN>::TN],
+                                           f32x16 (&acc)[WaveTiling<BM, BN>::TM][WaveTiling<BM, BN>::TN]) {
+#pragma unroll
+    for (int q = Q0; q < Q1; ++q)
+#pragma unroll
+        for (int i = 0; i < WaveTiling<BM, BN>::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < WaveTiling<BM, BN>::TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q][i], b[q][j], acc[i][j], 0, 0, 0);
+}
+
+// One pipelined slice: MFMAs of slice s (from LDS buffer `cur`), with the
+// LDS write of slice s+1 (register stage `al/bl`) and the global fetch of
+// slice s+3 (into the same, now free, register stage) between its halves.
+// Both happen unconditionally: a fetch past the end of K reads through the
+// operand's bounded buffer descriptor (zeros, or data the loop never
+// consumes), so no branch hides the load count from the wait-count logic.
+template <int BM, int BN, int BK, class AL, class BL>
+__device__ __forceinline__ void pipelined_slice(AL &al, BL &bl, const float *As_cur, const float *Bs_cur,
+                                                float *As_nxt, float *Bs_nxt,
+                                                f32x16 (&acc)[WaveTiling<BM, BN>::TM][WaveTiling<BM, BN>::TN],
+                                                int k_fetch, int tid, int lane, int wm0, int wn0) {
+    float a[BK / 2][WaveTiling<BM, BN>::TM], b[BK / 2][WaveTiling<BM, BN>::TN];
+    load_fragments<BM, BN, BK>(As_cur, Bs_cur, a, b, wm0, wn0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_steps<BM, BN, BK, 0, BK / 4>(a, b, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    al.commit(As_nxt, tid);
+    bl.commit(Bs_nxt, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    al.fetch(k_fetch, tid);
+    bl.fetch(k_fetch, tid);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_steps<BM, BN, BK, BK / 4, BK / 2>(a, b, acc);
+    __syncthreads();
+}
+
+// The K loop shared by every MFMA GEMM kernel: BK slices through two LDS
+// buffers and two register stages. Slice j is fetched from global memory into
+// register stage j%2 during slice j-3, written to LDS buffer j%2 during slice
+// j-1 and consumed in slice j, so a global load has two full slices of MFMA
+// work to arrive, and the LDS writes, address math and loads all overlap the
+// matrix pipe. One barrier per slice. The loop is unrolled by two so both
+// register stages are addressed statically. `al0/bl0` and `al1/bl1` are the
+// two register stages of the A and B loaders (same geometry).
+template <int BM, int BN, int BK, class AL, class BL>
+__device__ __forceinline__ void gemm_mainloop(AL &al0, BL &bl0, AL &al1, BL &bl1,
+                                              float (*As)[BK * LdsPad<BM>::stride],
+                                              float (*Bs)[BK * LdsPad<BN>::stride],
+                                              f32x16 (&acc)[WaveTiling<BM, BN>::TM][WaveTiling<BM, BN>::TN],
+                                              int k_begin, int nslices, int tid, int lane, int wm0, int wn0) {
+    if (nslices <= 0) return;
+    // prologue: slice 0 -> LDS 0; slice 1 -> regs 1; slice 2 -> regs 0
+    al0.fetch(k_begin, tid);
+    bl0.fetch(k_begin, tid);
+    al0.commit(As[0], tid);
+    bl0.commit(Bs[0], tid);
+    al1.fetch(k_begin + BK, tid);
+    bl1.fetch(k_begin + BK, tid);
+    al0.fetch(k_begin + 2 * BK, tid);
+    bl0.fetch(k_begin + 2 * BK, tid);
+    __syncthreads();
+    int s = 0;
+    for (; s + 1 < nslices; s += 2) {
+        // even slice s: LDS 0; commit s+1 from regs 1; fetch s+3 into regs 1
+        pipelined_slice<BM, BN, BK>(al1, bl1, As[0], Bs[0], As[1], Bs[1], acc, k_begin + (s + 3) * BK, tid, lane,
+                                    wm0, wn0);
+        // odd slice s+1: LDS 1; commit s+2 from regs 0; fetch s+4 into regs 0
+        pipelined_slice<BM, BN, BK>(al0, bl0, As[1], Bs[1], As[0], Bs[0], acc, k_begin + (s + 4) * BK, tid, lane,
+                                    wm0, wn0);
+    }
+    if (s < nslices) {
+        // last (even) slice: nothing left to stage
+        float a[BK / 2][WaveTiling<BM, BN>::TM], b[BK / 2][WaveTiling<BM, BN>::TN];
+        load_fragments<BM, BN, BK>(As[0], Bs[0], a, b, wm0, wn0, lane);
+        mfma_steps<BM, BN, BK, 0, BK / 2>(a, b, acc);
+    }
+}
 
 } // namespace spinn

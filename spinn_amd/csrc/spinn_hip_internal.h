@@ -29,6 +29,7 @@ struct TileChoice {
     int bm, bn, split, k_chunk;
 };
 TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split);
+void force_tiles(int bm, int bn, int split);
 
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cu_count();

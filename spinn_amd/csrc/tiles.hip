@@ -6,36 +6,54 @@ namespace spinn {
 // Pick the output tile and K split for an (M x N) problem repeated `reps`
 // times (groups or batch). Larger tiles do more MFMA work per byte staged,
 // but a launch needs enough workgroups to occupy every CU (2 resident per CU).
+static int g_force_bm = 0, g_force_bn = 0, g_force_split = 0;
+
+void force_tiles(int bm, int bn, int split) {
+    g_force_bm = bm;
+    g_force_bn = bn;
+    g_force_split = split;
+}
+
+static bool valid_tile(int bm, int bn) { return (bm == 64 || bm == 128) && (bn == 64 || bn == 128); }
+
 TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
-    static const int cand[4][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}};
-    const int cus = device_cu_count();
-    double best = 1e300;
-    TileChoice tc{64, 64, 1, K};
-    for (auto &c : cand) {
-        const int bm = c[0], bn = c[1];
-        const int64_t tiles = (int64_t)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * reps;
-        // Each CU works through ceil(tiles / CUs) tiles; a tile costs bm*bn*K
-        // MFMA work at an efficiency that drops for smaller tiles (more bytes
-        // staged per flop, fewer MFMAs per barrier).
-        const double tile_eff = (bm == 128 && bn == 128) ? 1.0 : (bm * bn == 128 * 64 ? 0.92 : 0.80);
-        const double rounds = (double)((tiles + cus - 1) / cus);
-        const double est = rounds * bm * bn / tile_eff;
-        if (est < best - 1e-9) {
-            best = est;
-            tc = TileChoice{bm, bn, 1, K};
+    if (g_force_bm && valid_tile(g_force_bm, g_force_bn)) {
+        TileChoice tc{g_force_bm, g_force_bn, 1, K};
+        if (allow_split && g_force_split > 1) {
+            int chunk = (K + g_force_split - 1) / g_force_split;
+            chunk = (chunk + kBK - 1) / kBK * kBK;
+            tc.split = (K + chunk - 1) / chunk;
+            tc.k_chunk = chunk;
+            if (tc.split <= 1) tc.k_chunk = K;
         }
+        return tc;
     }
-    if (allow_split) {
-        const int64_t tiles = (int64_t)((M + tc.bm - 1) / tc.bm) * ((N + tc.bn - 1) / tc.bn) * reps;
-        if (tiles < cus && K >= 4 * kBK * 2) {
-            int split = (int)std::min<int64_t>((cus + tiles - 1) / tiles, K / (4 * kBK));
-            split = std::max(1, std::min(split, 32));
-            if (split > 1) {
-                int chunk = (K + split - 1) / split;
-                chunk = (chunk + kBK - 1) / kBK * kBK;
-                split = (K + chunk - 1) / chunk;
-                tc.split = split;
-                tc.k_chunk = chunk;
+    const int cus = device_cu_count();
+    const int64_t work = (int64_t)M * N * reps;
+    TileChoice tc{64, 64, 1, K};
+    if (work >= (int64_t)64 * cus * 128 * 128) {
+        // Large problems (>= 64 full 128x128 tiles per CU): the bigger tile
+        // stages half the bytes per flop and still fills the machine.
+        tc.bm = tc.bn = 128;
+        return tc;
+    }
+    // Conv-sized problems: 64x64 tiles run up to six blocks per CU, which is
+    // what hides the load latency of a short K loop (measured faster than
+    // 128-wide tiles on every ResNet-101 layer shape at batch 32).
+    const int64_t tiles = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * reps;
+    if (allow_split && K >= 512 && tiles < 2 * cus) {
+        // Split K only when each split still runs >= 128 deep: the partial
+        // sums cost a write and a read of the output per split.
+        int split = (int)std::min<int64_t>((4 * cus + tiles - 1) / tiles, K / 128);
+        split = std::max(1, std::min(split, 8));
+        if (split > 1) {
+            int chunk = (K + split - 1) / split;
+            chunk = (chunk + kBK - 1) / kBK * kBK;
+            tc.split = (K + chunk - 1) / chunk;
+            tc.k_chunk = chunk;
+            if (tc.split <= 1) {
+                tc.split = 1;
+                tc.k_chunk = K;
             }
         }
     }

@@ -141,6 +141,7 @@ _SIGS = {
     "spinn_hip_graph_destroy": (C.c_int, [C.c_void_p]),
     "spinn_hip_error_string": (C.c_char_p, [C.c_int]),
     "spinn_hip_version": (C.c_char_p, []),
+    "spinn_hip_tune_force_tiles": (None, [C.c_int, C.c_int, C.c_int]),
     # host runtime
     "spinn_load": (C.POINTER(SpinnContext), [C.c_char_p]),
     "spinn_plan": (C.c_int, [C.POINTER(SpinnContext), C.c_uint32]),
@@ -158,6 +159,7 @@ _SIGS = {
     "spinn_node_times": (C.c_int, [C.POINTER(SpinnContext), C.POINTER(C.c_float), C.c_int]),
     "spinn_op_registered": (C.c_int, [C.c_uint16]),
     "spinn_set_conv_policy": (C.c_int, [C.POINTER(SpinnContext), C.c_int]),
+    "spinn_set_profiling": (None, [C.c_int]),
 }
 
 
