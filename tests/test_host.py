@@ -1,0 +1,232 @@
+"""CPU tests of the host side: ENNF format, the native loader, the planner
+(against the reference planner's offsets), the operator registry's error
+conventions and the exported C ABI. No GPU calls."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from spinn_amd import ennf as E
+from spinn_amd import models
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLD = ROOT / "tests" / "golden"
+
+
+def test_struct_sizes(native):
+    assert C.sizeof(native.ENNFHeader) == 64
+    assert C.sizeof(native.ConvDesc) == 17 * 4
+    assert len(E.conv_params(3, 3)) == 44
+    assert len(E.pool_params(3, 3, 2, 2)) == 48
+    assert len(E.gemm_params()) == 12
+    assert len(E.reduce_params([2, 3])) == 36
+
+
+def test_ennf_roundtrip(tmp_path):
+    g, x = models.resnet(batch=2, seed=4, blocks=(1, 1, 1, 1), hw=32, num_classes=10)
+    path = g.write(tmp_path / "m.ennf")
+    m = E.read(path)
+    h = m["header"]
+    assert h["magic"] == E.ENNF_MAGIC and h["version_major"] == 2
+    assert h["num_nodes"] == len(g.nodes) and h["num_tensors"] == len(g.tensors)
+    assert h["reserved"][0] == 64  # dense weight-entry table right after the header
+    assert h["weight_data_offset"] % 16 == 0
+    assert m["inputs"] == g.inputs and m["outputs"] == g.outputs
+    for nd, gn in zip(m["nodes"], g.nodes):
+        assert nd["op"] == gn.op and nd["inputs"] == gn.inputs and nd["outputs"] == gn.outputs
+        assert nd["params"] == gn.params and nd["flags"] == gn.flags
+    ref = {t.id: 0 for t in g.tensors}
+    for n in g.nodes:
+        for i in n.inputs:
+            ref[i] += 1
+    for t in g.tensors:
+        mt = m["tensors"][t.id]
+        assert mt["dims"] == t.dims and mt["ref_count"] == ref[t.id] and mt["is_weight"] == int(t.is_weight)
+        if t.is_weight:
+            assert np.array_equal(m["weights"][t.id], t.data)
+    # the fused residual is the conv's last input, with ADD_RELU in params.reserved
+    convs = [nd for nd in m["nodes"] if nd["op"] == E.OP_CONV]
+    res = [nd for nd in convs if E.unpack_conv_params(nd["params"])["act"] == E.ACT_ADD_RELU]
+    assert len(res) == 4 and all(len(nd["inputs"]) == 4 for nd in res)
+
+
+def test_resnet101_fusion_mix():
+    """67 RELU / 33 ADD_RELU / 4 NONE convs, as the reference's fusion leaves ResNet-101."""
+    g, _ = models.resnet101(batch=1, seed=0)
+    acts = [E.unpack_conv_params(n.params)["act"] for n in g.nodes if n.op == E.OP_CONV]
+    assert len(acts) == 104
+    assert acts.count(E.ACT_RELU) == 67 and acts.count(E.ACT_ADD_RELU) == 33 and acts.count(E.ACT_NONE) == 4
+    flops = sum(f for _, f in models.conv_flops(g))
+    assert abs(flops / 1e9 - 15.599) < 0.01  # 15.60 GFLOP of convolution per image
+
+
+def _load_ctx(native, path):
+    L = native.lib()
+    ctx = L.spinn_load(str(path).encode())
+    assert ctx
+    return L, ctx
+
+
+def test_native_loader_parses_model(native, tmp_path):
+    g, _ = models.vgg_stack(batch=2, seed=3, in_c=16, schedule=[(16, 32), (32, 16)])
+    path = g.write(tmp_path / "v.ennf")
+    L, ctx = _load_ctx(native, path)
+    try:
+        c = ctx.contents
+        assert c.num_nodes == len(g.nodes) and c.num_tensors == len(g.tensors)
+        assert c.input_ids[0] == g.inputs[0] and c.output_ids[0] == g.outputs[0]
+        for i, nd in enumerate(g.nodes):
+            n = c.nodes[i]
+            assert n.op_type == nd.op and n.num_inputs == len(nd.inputs)
+            assert list(n.input_ids[:n.num_inputs]) == nd.inputs
+            assert C.string_at(n.params, n.params_size) == nd.params
+        for t in g.tensors:
+            ct = c.tensors[t.id]
+            assert tuple(ct.dims[:ct.ndim]) == t.dims and ct.size == 4 * t.elem_count
+            if t.is_weight:
+                p = L.spinn_get_weight(ctx, t.id)
+                got = np.frombuffer(C.string_at(p, t.data.nbytes), np.float32).reshape(t.dims)
+                assert np.array_equal(got, t.data)
+    finally:
+        L.spinn_free(ctx)
+
+
+@pytest.mark.parametrize("name,maker", [
+    ("conv0", lambda: models.conv_bn_relu(seed=0)[0]),
+    ("resnet101_b1", lambda: models.resnet101(batch=1, seed=0)[0]),
+    ("resnet101_b4", lambda: models.resnet101(batch=4, seed=0)[0]),
+    ("vgg_b2", lambda: models.vgg_stack(batch=2, seed=3, in_c=16, schedule=[(16, 32), (16, 32), (32, 16), (32, 16)])[0]),
+    ("gemm_32", lambda: models.gemm_model(32, 1000, 2048, seed=1)[0]),
+])
+def test_planner_matches_reference(native, tmp_path, name, maker):
+    """Offsets and peak equal the reference planner's (golden, from its compiled code)."""
+    z = np.load(GOLD / "planner_offsets.npz", allow_pickle=False)
+    path = maker().write(tmp_path / f"{name}.ennf")
+    L, ctx = _load_ctx(native, path)
+    try:
+        peak = L.spinn_plan_memory(ctx, 0)
+        assert peak == int(z[f"{name}_peak"][0])
+        c = ctx.contents
+        ids = z[f"{name}_ids"].tolist()
+        got = [c.tensors[i].offset for i in ids]
+        assert got == z[f"{name}_offsets"].tolist()
+        # invariants: 16-byte alignment, inside the peak
+        for i in ids:
+            t = c.tensors[i]
+            assert t.offset % 16 == 0 and t.offset + t.size <= peak
+        _check_no_live_overlap(c)
+    finally:
+        L.spinn_free(ctx)
+    # a cap below the peak fails like the reference (SPINN_MEM_ERR_NOMEM)
+    L, ctx = _load_ctx(native, path)
+    try:
+        assert L.spinn_plan_memory(ctx, max(16, peak // 2)) == int(z[f"{name}_capped_rc"][0]) == -2
+    finally:
+        L.spinn_free(ctx)
+
+
+def _check_no_live_overlap(c):
+    """Replays node order: tensors alive at the same time never share bytes."""
+    n_t = c.num_tensors
+    remaining = [c.tensors[i].ref_count for i in range(n_t)]
+    outputs = {c.output_ids[i] for i in range(c.header.num_outputs)}
+    live = {c.input_ids[i] for i in range(c.header.num_inputs)}
+
+    def span(i):
+        t = c.tensors[i]
+        return t.offset, t.offset + ((t.size + 15) & ~15)
+
+    for k in range(c.num_nodes):
+        nd = c.nodes[k]
+        for o in nd.output_ids[:nd.num_outputs]:
+            t = c.tensors[o]
+            if t.is_weight or t.size == 0:
+                continue
+            a0, a1 = span(o)
+            for l in live:
+                b0, b1 = span(l)
+                assert a1 <= b0 or b1 <= a0, f"tensor {o} overlaps live tensor {l}"
+            live.add(o)
+        for i in nd.input_ids[:nd.num_inputs]:
+            t = c.tensors[i]
+            if t.is_weight or t.size == 0 or i in outputs:
+                continue
+            if remaining[i] > 0:
+                remaining[i] -= 1
+                if remaining[i] == 0:
+                    live.discard(i)
+
+
+def test_loader_rejects_bad_files(native, tmp_path):
+    L = native.lib()
+    bad = tmp_path / "bad.ennf"
+    data = bytearray(models.conv_bn_relu(seed=0)[0].to_bytes())
+    data[0:4] = b"XXXX"
+    bad.write_bytes(bytes(data))
+    assert not L.spinn_load(str(bad).encode())
+    assert not L.spinn_load(str(tmp_path / "missing.ennf").encode())
+    trunc = tmp_path / "trunc.ennf"
+    trunc.write_bytes(bytes(data[:50]))
+    assert not L.spinn_load(str(trunc).encode())
+
+
+def test_dispatch_conventions(native):
+    """op >= 512 -> -1; an unregistered op is skipped with 0; bad arity -> -1
+    (SPINN/run_time/spinn_ops.c:210-228, ops/conv/conv2d.c:95)."""
+    L = native.lib()
+    empty = (C.POINTER(native.SpinnTensor) * 1)()
+    assert L.spinn_dispatch_op(600, empty, 0, None, 0, empty, 0) == -1
+    assert L.spinn_dispatch_op(1, empty, 0, None, 0, empty, 0) == 0  # Abs: not served by this runtime
+    assert L.spinn_dispatch_op(E.OP_CONV, empty, 1, None, 0, empty, 1) == -1
+    assert L.spinn_dispatch_op(E.OP_GEMM, empty, 1, None, 0, empty, 1) == -1
+    for op in (E.OP_CONV, E.OP_GEMM, E.OP_MATMUL, E.OP_MAXPOOL, E.OP_REDUCEMEAN, E.OP_RESHAPE, E.OP_FLATTEN,
+               E.OP_GAP):
+        assert L.spinn_op_registered(op) == 1
+
+
+def test_conv_algo_selection(native):
+    L = native.lib()
+
+    def algo(*a):
+        n, c, h, w, oc, k, s, p, g = a
+        oh = (h + 2 * p - k) // s + 1
+        d = native.ConvDesc(n, c, h, w, oc, oh, oh, k, k, s, s, p, p, g, 0, 0, 0)
+        return L.spinn_hip_conv_select_algo(C.byref(d))
+
+    assert algo(1, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM
+    assert algo(1, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_WINOGRAD
+    assert algo(1, 256, 14, 14, 256, 3, 2, 1, 1) == native.ALGO_IMPLICIT_GEMM
+    assert algo(1, 128, 20, 20, 128, 3, 2, 1, 128) == native.ALGO_DIRECT
+    assert algo(1, 6, 8, 8, 4, 3, 1, 1, 4) == native.SPINN_HIP_EINVAL  # C % group != 0
+
+
+def _declared_functions():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"static inline[^{]*\{.*?\n\}", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w \*]*?\b(spinn_\w+)\s*\(", text, flags=re.M):
+            names.add(m.group(1))
+    return names
+
+
+def test_library_exports_every_declared_symbol(native):
+    names = _declared_functions()
+    assert len(names) >= 40
+    L = C.CDLL(str(native.LIB_PATH))
+    missing = [n for n in sorted(names) if not hasattr(L, n)]
+    assert not missing, missing
+    # the ctypes signature table covers the header
+    assert not (names - set(native.exported_symbols()) - {"spinn_op_registered"}), \
+        names - set(native.exported_symbols())
+
+
+def test_bench_refuses_multi_gpu():
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr

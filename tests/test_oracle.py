@@ -1,0 +1,242 @@
+"""Pins the oracle (CPU restatement of the reference's conv/GEMM path).
+
+Each check is chosen so that a plausible mistake in the restatement fails it:
+  * the reference's own outputs on seeded inputs (golden fixtures written by
+    tests/golden/make_golden.py from the reference's compiled C code):
+    raw accumulator of the shipped group==1 path, grouped/depthwise convs with
+    the full epilogue, the sgemm_nn epilogue for every act code, op_gemm,
+    op_matmul, and the reference Winograd;
+  * the reference's known-answer tests: the Winograd identity KAT
+    (SPINN/run_time/test_winograd2.c:56-63) and the direct / im2col /
+    Winograd agreement case of SPINN/run_time/test_winograd.c:64-75;
+  * closed forms: float64 direct convolution and GEMM, and the float64
+    library routine torch.nn.functional.conv2d (CPU);
+  * the BN fold against BatchNorm applied after the convolution;
+  * a whole ENNF model run by the oracle against a float64 torch
+    interpretation of the same graph.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from spinn_amd import ennf as E
+from spinn_amd import models
+from tests.conftest import assert_parity, errors
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def _load(name):
+    return np.load(GOLD / name, allow_pickle=False)
+
+
+# ---------------- golden fixtures from the reference ----------------
+
+def test_conv_raw_accumulator_matches_reference():
+    """group == 1: the reference's packed path returns the raw accumulator."""
+    z = _load("conv_raw.npz")
+    ids = sorted({k.split("_")[0] for k in z.files})
+    assert ids
+    for i in ids:
+        n, c, h, w, oc, k, s, p, g, act = z[f"{i}_spec"].tolist()
+        d = O.conv_desc(n, c, h, w, oc, k, k, s, s, p, p, g, act)
+        r = z[f"{i}_r"] if f"{i}_r" in z.files else None
+        y = O.conv2d(d, z[f"{i}_x"], z[f"{i}_w"], z[f"{i}_b"], r, as_shipped=True)
+        ma, rel, _ = errors(y, z[f"{i}_y"])
+        assert ma <= 1e-5 and rel <= 1e-6, (i, ma, rel)
+        # and the specified epilogue really differs from the shipped output when it applies
+        if act != 0:
+            spec = O.conv2d(d, z[f"{i}_x"], z[f"{i}_w"], z[f"{i}_b"], r)
+            assert np.abs(spec - z[f"{i}_y"]).max() > 1e-3
+
+
+def test_conv_grouped_matches_reference():
+    """group > 1: full epilogue (bias, residual, ReLU/SiLU) as the reference applies it."""
+    z = _load("conv_grouped.npz")
+    for i in sorted({k.split("_")[0] for k in z.files}):
+        n, c, h, w, oc, k, s, p, g, act = z[f"{i}_spec"].tolist()
+        d = O.conv_desc(n, c, h, w, oc, k, k, s, s, p, p, g, act)
+        r = z[f"{i}_r"] if f"{i}_r" in z.files else None
+        y = O.conv2d(d, z[f"{i}_x"], z[f"{i}_w"], z[f"{i}_b"], r)
+        ma, rel, _ = errors(y, z[f"{i}_y"])
+        assert ma <= 1e-5 and rel <= 1e-6, (i, ma, rel)
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3, 4, 5])
+def test_epilogue_matches_reference(act):
+    """sgemm_nn epilogue, every act code (CLIP=2 is declared but applies nothing)."""
+    z = _load("epilogue.npz")
+    a, b, bias, r = z["a"], z["b"], z["bias"], z["r"]
+    m, k = a.shape
+    n = b.shape[1]
+    # the GEMM as a 1x1 convolution over a 1 x n image: W = a [m,k,1,1], X = b [1,k,1,n]
+    d = O.conv_desc(1, k, 1, n, m, 1, 1, act=act)
+    y = O.conv2d(d, np.ascontiguousarray(b.reshape(1, k, 1, n)), np.ascontiguousarray(a.reshape(m, k, 1, 1)), bias,
+                 np.ascontiguousarray(r.reshape(1, m, 1, n)) if act in (4, 5) else None)
+    ma, rel, _ = errors(y.reshape(m, n), z[f"y_act{act}"])
+    assert ma <= 1e-5 and rel <= 1e-6, (ma, rel)
+    # closed form of the specified order: v = acc + bias; ADD*: + R; RELU*: max0; SILU: v/(1+e^-v)
+    v = a.astype(np.float64) @ b.astype(np.float64) + bias[:, None]
+    if act in (4, 5):
+        v = v + r
+    if act in (1, 5):
+        v = np.maximum(v, 0)
+    elif act == 3:
+        v = v / (1 + np.exp(-v))
+    assert_parity(z[f"y_act{act}"], v, what="reference epilogue vs closed form")
+
+
+def test_gemm_matches_reference():
+    z = _load("gemm.npz")
+    for i in sorted({k.split("_")[0] for k in z.files if k.startswith("g")}):
+        m, n, k, ta, tb, cm = z[f"{i}_spec"].tolist()
+        c = z[f"{i}_c"] if f"{i}_c" in z.files else None
+        y = O.gemm(z[f"{i}_a"], z[f"{i}_b"], c, 1.0, 1.0, ta, tb)
+        ma, rel, _ = errors(y, z[f"{i}_y"])
+        assert ma <= 1e-5 and rel <= 1e-6, (i, ma, rel)
+        assert_parity(y, O.gemm_f64(z[f"{i}_a"], z[f"{i}_b"], c, 1.0, 1.0, ta, tb), what="vs float64")
+    y = O.matmul(z["mm_a"], z["mm_b"])
+    assert np.abs(y - z["mm_y"]).max() <= 1e-5
+
+
+def test_winograd_matches_reference_and_kat():
+    z = _load("winograd.npz")
+    # identity KAT: Y == X exactly (SPINN/run_time/test_winograd2.c:56-63)
+    x, w = z["kat_x"], z["kat_w"]
+    d = O.conv_desc(1, 1, 4, 4, 1, 3, 3, 1, 1, 1, 1, act=1)
+    y = O.winograd(d, x, w)
+    assert np.array_equal(y, x)
+    assert np.array_equal(z["kat_y"], x)
+    # seeded case with bias and ReLU against the reference's Winograd
+    x, w, b = z["rand_x"], z["rand_w"], z["rand_b"]
+    n, c, h, ww = x.shape
+    d = O.conv_desc(n, c, h, ww, w.shape[0], 3, 3, 1, 1, 1, 1, act=1)
+    y = O.winograd(d, x, w, b)
+    ma, rel, _ = errors(y, z["rand_y"])
+    assert ma <= 1e-5 and rel <= 1e-6
+    assert_parity(y, O.conv2d_f64(d, x, w, b), what="winograd vs direct float64")
+
+
+def test_winograd_direct_im2col_agree_reference_case():
+    """SPINN/run_time/test_winograd.c:64-75: C=2, H=W=4, OC=3, X[i]=i+1,
+    W[i]=(i%5-2)*0.5, bias {1,2,3}, pad 1; direct, im2col and Winograd agree."""
+    x = (np.arange(2 * 16, dtype=np.float32) + 1).reshape(1, 2, 4, 4)
+    w = (((np.arange(3 * 2 * 9) % 5) - 2) * 0.5).astype(np.float32).reshape(3, 2, 3, 3)
+    b = np.array([1, 2, 3], np.float32)
+    d = O.conv_desc(1, 2, 4, 4, 3, 3, 3, 1, 1, 1, 1)
+    direct = O.conv2d_f64(d, x, w, b)
+    assert np.abs(O.conv2d(d, x, w, b) - direct).max() < 1e-4
+    assert np.abs(O.winograd(d, x, w, b) - direct).max() < 1e-4
+    # exact integer-valued answer: the weights are multiples of 0.5 and X integral
+    assert np.array_equal(np.round(direct * 2), direct * 2)
+
+
+# ---------------- closed forms ----------------
+
+CONV_SHAPES = [
+    (2, 16, 12, 12, 24, 3, 1, 1, 1, 1),
+    (1, 3, 21, 17, 10, 7, 2, 3, 1, 3),
+    (2, 32, 9, 9, 40, 1, 2, 0, 1, 0),
+    (1, 24, 10, 10, 24, 3, 2, 1, 24, 3),
+    (1, 16, 8, 8, 32, 3, 1, 1, 4, 5),
+    (3, 8, 5, 7, 6, 3, 1, 0, 1, 4),
+]
+
+
+@pytest.mark.parametrize("spec", CONV_SHAPES, ids=[str(s) for s in CONV_SHAPES])
+def test_oracle_conv_vs_float64_and_torch(spec):
+    import torch
+    import torch.nn.functional as F
+    n, c, h, w, oc, k, s, p, g, act = spec
+    rng = np.random.default_rng(sum(spec))
+    x = rng.uniform(-1, 1, (n, c, h, w)).astype(np.float32)
+    wt = rng.normal(0, 0.4, (oc, c // g, k, k)).astype(np.float32)
+    b = rng.normal(0, 0.1, oc).astype(np.float32)
+    d = O.conv_desc(n, c, h, w, oc, k, k, s, s, p, p, g, act)
+    r = rng.uniform(-1, 1, (n, oc, d.oh, d.ow)).astype(np.float32) if act in (4, 5) else None
+    y = O.conv2d(d, x, wt, b, r)
+    ref64 = O.conv2d_f64(d, x, wt, b, r)
+    assert_parity(y, ref64, what="oracle vs float64 direct")
+    t = F.conv2d(torch.from_numpy(x).double(), torch.from_numpy(wt).double(), torch.from_numpy(b).double(), s, p,
+                 1, g)
+    if r is not None:
+        t = t + torch.from_numpy(r).double()
+    if act in (1, 5):
+        t = torch.relu(t)
+    elif act == 3:
+        t = t * torch.sigmoid(t)
+    assert_parity(ref64, t.numpy(), rel_l2=1e-12, max_abs=1e-10, what="float64 direct vs torch float64")
+
+
+def test_oracle_gemm_vs_float64():
+    rng = np.random.default_rng(3)
+    for (m, n, k) in models.GEMM_SWEEP[:2] + [(19, 23, 5)]:
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        b = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+        c = rng.normal(0, 0.01, n).astype(np.float32)
+        assert_parity(O.gemm(a, b, c, trans_b=1), a.astype(np.float64) @ b.T.astype(np.float64) + c)
+
+
+def test_bn_fold_closed_form():
+    """Conv with folded weights == BatchNorm(conv) (SPINN/graph_opt.c:181-198)."""
+    rng = np.random.default_rng(11)
+    oc, c = 8, 5
+    w = models.kaiming(rng, oc, c, 3, 3)
+    gamma, beta, mean, var = models.bn_params(rng, oc)
+    w2, b2 = models.fold_bn(w, None, gamma, beta, mean, var)
+    x = rng.uniform(-1, 1, (2, c, 7, 7)).astype(np.float32)
+    d = O.conv_desc(2, c, 7, 7, oc, 3, 3, 1, 1, 1, 1)
+    conv = O.conv2d_f64(d, x, w)
+    bn = (conv - mean[None, :, None, None]) / np.sqrt(var.astype(np.float64) + 1e-5)[None, :, None, None] \
+        * gamma[None, :, None, None] + beta[None, :, None, None]
+    assert_parity(O.conv2d_f64(d, x, w2, b2), bn, max_abs=1e-5, rel_l2=1e-6)
+
+
+# ---------------- whole model ----------------
+
+def _torch_graph(g_path, x):
+    """Interpret an ENNF file with float64 torch ops (independent of the oracle)."""
+    import torch
+    import torch.nn.functional as F
+    m = E.read(g_path)
+    vals = {m["inputs"][0]: torch.from_numpy(x).double()}
+    W = {k: torch.from_numpy(np.array(v)).double() for k, v in m["weights"].items()}
+    for nd in m["nodes"]:
+        ins = nd["inputs"]
+        if nd["op"] == E.OP_CONV:
+            p = E.unpack_conv_params(nd["params"])
+            act = p["act"]
+            has_res = act in (4, 5)
+            nreal = len(ins) - (1 if has_res else 0)
+            bias = W[ins[2]] if nreal > 2 else None
+            y = F.conv2d(vals[ins[0]], W[ins[1]], bias, p["strides"][:2], p["pads"][:2], 1, p["group"])
+            if has_res:
+                y = y + vals[ins[-1]]
+            if act in (1, 5):
+                y = torch.relu(y)
+            elif act == 3:
+                y = y * torch.sigmoid(y)
+        elif nd["op"] == E.OP_MAXPOOL:
+            kh, kw = np.frombuffer(nd["params"][:4], np.uint16)
+            sh, sw = np.frombuffer(nd["params"][8:12], np.uint16)
+            ph, pw = np.frombuffer(nd["params"][16:20], np.uint16)
+            y = F.max_pool2d(vals[ins[0]], (int(kh), int(kw)), (int(sh), int(sw)), (int(ph), int(pw)))
+        elif nd["op"] == E.OP_REDUCEMEAN:
+            y = vals[ins[0]].mean(dim=(2, 3), keepdim=True)
+        elif nd["op"] == E.OP_RESHAPE:
+            y = vals[ins[0]].reshape(vals[ins[0]].shape[0], -1)
+        elif nd["op"] == E.OP_GEMM:
+            y = vals[ins[0]] @ W[ins[1]].T + W[ins[2]]
+        else:
+            raise AssertionError(nd["op"])
+        vals[nd["outputs"][0]] = y
+    return vals[m["outputs"][0]].numpy()
+
+
+def test_oracle_model_matches_torch_float64(tmp_path):
+    g, x = models.resnet(batch=2, seed=2, blocks=(1, 2, 1, 1), hw=64, num_classes=37)
+    path = g.write(tmp_path / "tiny_resnet.ennf")
+    y = O.Model(path).run(x, g.dims(g.outputs[0]))
+    assert_parity(y, _torch_graph(path, x), what="oracle model vs torch float64")
