@@ -122,6 +122,91 @@ def profiled_node_ms(N, Session, path, x, policy, steps: int, warmup: int):
     return acc / steps
 
 
+def suite(N, Session, models, reps: int = 100) -> dict:
+    """The other benchmark configurations, each on its own:
+    cfg0   single fused Conv3x3+BN+ReLU 1x64x56x56 through spinn_hip_conv
+           (launch-bound: 2*reps back-to-back launches timed with events) and
+           through spinn_run with host copies;
+    gemm   the Gemm sweep (transB=1, bias vector, alpha=beta=1) through spinn_hip_gemm,
+           against the MFMA roofline or, for arithmetic intensity under the
+           19.7 flop/B ridge, the HBM roofline;
+    vgg    the 8-layer 3x3 stack at batch 8 under the implicit-GEMM and the
+           Winograd policy: images/s, direct-conv-equivalent TFLOP/s and how far
+           the two outputs are apart (relative L2)."""
+    import ctypes as C
+    from spinn_amd.devbuf import DeviceBuffer, time_launches
+    L = N.lib()
+    out = {}
+    g, x = models.conv_bn_relu(seed=0)
+    wt, bias = g.tensors[1].data, g.tensors[2].data
+    d = N.ConvDesc(1, 64, 56, 56, 64, 56, 56, 3, 3, 1, 1, 1, 1, 1, N.ACT_RELU, 0, 0)
+    d.algo = L.spinn_hip_conv_select_algo(C.byref(d))
+    bx, bw, bb = DeviceBuffer.from_array(x), DeviceBuffer.from_array(wt), DeviceBuffer.from_array(bias)
+    by = DeviceBuffer(4 * 64 * 56 * 56)
+    bp = DeviceBuffer(L.spinn_hip_conv_packed_size(C.byref(d)))
+    wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
+    bws = DeviceBuffer(wsz) if wsz else None
+    N.check(L.spinn_hip_conv_pack_weights(C.byref(d), bw.ptr, bp.ptr, None), "pack")
+    ms = time_launches(lambda: L.spinn_hip_conv(C.byref(d), bx.ptr, bw.ptr, bp.ptr, bb.ptr, None, by.ptr,
+                                                bws.ptr if bws else None, wsz, None), 2 * reps)
+    flops = 2.0 * 64 * 56 * 56 * 64 * 9
+    byts = 4.0 * (x.size + wt.size + bias.size + 64 * 56 * 56)
+    tmp = Path(tempfile.mkdtemp(prefix="spinn_suite_"))
+    with Session(g.write(tmp / "cfg0.ennf")) as s0:
+        for _ in range(5):
+            s0.run(x)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            s0.run(x)
+        run_ms = (time.perf_counter() - t0) / reps * 1e3
+    out["cfg0_conv3x3_bn_relu"] = {"kernel_us": round(ms * 1e3, 3), "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
+                                   "frac_mfma_peak": round(flops / (ms * 1e-3) / PEAK_FP32_MFMA, 4),
+                                   "roofline_us": round(max(flops / PEAK_FP32_MFMA, byts / 8e12) * 1e6, 3),
+                                   "spinn_run_ms_with_host_copies": round(run_ms, 4)}
+    for b_ in (bx, bw, bb, by, bp) + ((bws,) if bws else ()):
+        b_.free()
+    gemms = []
+    for (m, n, k) in models.GEMM_SWEEP:
+        rng = np.random.default_rng(m * 7 + n)
+        a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+        b = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+        c = rng.normal(0, 0.01, n).astype(np.float32)
+        gd = N.GemmDesc(m, n, k, 0, 1, 1, 1.0, 1.0, 1, 0, 0, 0, 0)
+        ba, bb2, bc, by2 = (DeviceBuffer.from_array(a), DeviceBuffer.from_array(b), DeviceBuffer.from_array(c),
+                            DeviceBuffer(4 * m * n))
+        wsz = L.spinn_hip_gemm_workspace_size(C.byref(gd))
+        bws = DeviceBuffer(wsz) if wsz else None
+        ms = time_launches(lambda: L.spinn_hip_gemm(C.byref(gd), ba.ptr, bb2.ptr, bc.ptr, by2.ptr,
+                                                    bws.ptr if bws else None, wsz, None), reps)
+        f = 2.0 * m * n * k
+        byts = 4.0 * (m * k + n * k + n + m * n)
+        bound = "hbm" if f / byts < PEAK_FP32_MFMA / 8e12 else "mfma"
+        frac = (byts / (ms * 1e-3) / 8e12) if bound == "hbm" else (f / (ms * 1e-3) / PEAK_FP32_MFMA)
+        gemms.append({"mnk": [m, n, k], "us": round(ms * 1e3, 3), "gflops": round(f / (ms * 1e-3) / 1e9, 1),
+                      "gbps": round(byts / (ms * 1e-3) / 1e9, 1), "bound": bound, "frac_roofline": round(frac, 4)})
+        for b_ in (ba, bb2, bc, by2) + ((bws,) if bws else ()):
+            b_.free()
+    out["gemm_sweep"] = gemms
+    gv, xv = models.vgg_stack(batch=8, seed=0)
+    pv = gv.write(tmp / "vgg_b8.ennf")
+    vgg_flops = sum(f for _, f in models.conv_flops(gv))
+    res = {}
+    outs = {}
+    for name, pol in (("implicit_gemm", N.POLICY_IGEMM), ("winograd", N.POLICY_WINOGRAD)):
+        with Session(pv, policy=pol, graph=True) as sv:
+            sv.upload_input(xv)
+            msv = time_steps(sv, max(10, reps // 10), 3)
+            outs[name] = sv.download(sv.output_id)
+        res[name] = {"ms": round(msv, 4), "images_per_s": round(8 / (msv * 1e-3), 1),
+                     "tflops_direct_equiv": round(vgg_flops / (msv * 1e-3) / 1e12, 2)}
+    dv = outs["winograd"].astype(np.float64) - outs["implicit_gemm"]
+    res["winograd_vs_igemm_rel_l2"] = float(np.linalg.norm(dv) / np.linalg.norm(outs["implicit_gemm"]))
+    res["winograd_vs_igemm_max_abs"] = float(np.abs(dv).max())
+    res["gflop_direct_equiv"] = round(vgg_flops / 1e9, 2)
+    out["vgg3x3_stack_b8"] = res
+    return out
+
+
 def time_steps(sess, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         sess.run_resident()
@@ -145,6 +230,7 @@ def main() -> int:
                     help="only the per-node-event pass at batch B (warmup + steps, eager launches): the run a "
                          "kernel profiler wraps, so its kernel statistics cover exactly the measured launches")
     ap.add_argument("--layers-out", default=str(ROOT / "gpurun_out" / "bench_layers.json"))
+    ap.add_argument("--no-suite", action="store_true", help="skip the config-0 / Gemm sweep / VGG measurements")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
@@ -211,6 +297,10 @@ def main() -> int:
     s1.close()
     print(f"[bench] b1: {ms_1:.3f} ms/step", file=sys.stderr, flush=True)
 
+    other = None if a.no_suite else suite(N, Session, models)
+    if other is not None:
+        print(f"[bench] suite: {json.dumps(other)}", file=sys.stderr, flush=True)
+
     rows = conv_table(gB)
     layers = []
     tot_f = tot_t = ig_f = ig_t = 0.0
@@ -264,6 +354,7 @@ def main() -> int:
                      "unit": "TFLOP/s", "frac": round(ig_tflops * 1e12 / PEAK_FP32_MFMA, 4), "traffic": None,
                      "kernel": f"conv_igemm_kernel (implicit-GEMM conv, {n_ig} layers, batch {a.batch})"},
         "cpu_baseline": cpu,
+        "other_configs": other,
     }
     print(json.dumps(line), flush=True)
     return 0

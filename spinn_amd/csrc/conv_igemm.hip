@@ -47,8 +47,10 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
     const int wave = tid >> 6;
     const int wm0 = (wave >> 1) * WT::WM;
     const int wn0 = (wave & 1) * WT::WN;
-    const int n0 = blockIdx.x * BN;
-    const int m0 = blockIdx.y * BM;
+    int tile_m, tile_n;
+    xcd_tile(gridDim.y, gridDim.x, tile_m, tile_n);
+    const int n0 = tile_n * BN;
+    const int m0 = tile_m * BM;
     const int z = blockIdx.z;
     const int group = SPLIT ? 0 : z;
     const int k_begin = SPLIT ? z * a.k_chunk : 0;

@@ -310,6 +310,25 @@ struct Im2colTapLoader {
     }
 };
 
+// Output tile of this workgroup. Workgroups are dispatched round-robin over
+// the 8 XCDs (each with its own L2), so consecutive block ids land on
+// different XCDs. Remap so that each XCD walks a contiguous run of the tile
+// space, M fastest: blocks sharing an L2 share the same input columns (the B
+// operand, usually the larger one) and stream the weight rows in order.
+// A bijection on [0, tiles_m * tiles_n) for each blockIdx.z.
+__device__ __forceinline__ void xcd_tile(int tiles_m, int tiles_n, int &tm, int &tn) {
+    constexpr int kXcds = 8;
+    const int total = tiles_m * tiles_n;
+    const int id = blockIdx.x + blockIdx.y * gridDim.x;
+    const int xcd = id % kXcds;
+    const int idx = id / kXcds;
+    const int base = total / kXcds;
+    const int rem = total % kXcds;
+    const int t = xcd * base + min(xcd, rem) + idx;
+    tm = t % tiles_m;
+    tn = t / tiles_m;
+}
+
 // Reads all operand fragments of one LDS slice (issued together, so their
 // latency overlaps the MFMAs that follow).
 template <int BM, int BN, int BK>
