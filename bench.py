@@ -207,6 +207,104 @@ def suite(N, Session, models, reps: int = 100) -> dict:
     return out
 
 
+TRAFFIC_FILE = ROOT / "profiles" / "conv_igemm_traffic_resnet101_b32.json"
+CALIB_BYTES = 256 << 20
+
+
+def calibration_kernels() -> None:
+    """Known-size traffic for scaling the FETCH_SIZE / WRITE_SIZE counters:
+    three 256 MiB fills (write only) then three 256 MiB device copies (read +
+    write) through the library's own kernels."""
+    from spinn_amd import native as N
+    from spinn_amd.devbuf import DeviceBuffer
+    L = N.lib()
+    N.check(L.spinn_hip_init(0), "spinn_hip_init")
+    a, b = DeviceBuffer(CALIB_BYTES), DeviceBuffer(CALIB_BYTES)
+    for _ in range(3):
+        N.check(L.spinn_hip_fill_u32(a.ptr, 7, CALIB_BYTES, None), "fill")
+    for _ in range(3):
+        N.check(L.spinn_hip_copy(b.ptr, a.ptr, CALIB_BYTES, None), "copy")
+    N.check(L.spinn_hip_stream_sync(None), "sync")
+    a.free()
+    b.free()
+    print("[bench] calibration kernels done", flush=True)
+
+
+def igemm_algorithmic_bytes(batch: int, policy: str) -> float:
+    """Mean algorithmic bytes per implicit-GEMM conv launch of ResNet-101 at
+    `batch`: input + weights + bias + output (+ residual for the fused add),
+    each read or written once, fp32."""
+    from spinn_amd import models
+    from spinn_amd import native as N
+    pol = {"auto": N.POLICY_AUTO, "igemm": N.POLICY_IGEMM, "winograd": N.POLICY_WINOGRAD}[policy]
+    g, _ = models.resnet101(batch=batch, seed=0)
+    alg = []
+    for r in conv_table(g):
+        if algo_of(N, r, pol) != N.ALGO_IMPLICIT_GEMM:
+            continue
+        x = r["n"] * r["c"] * r["h"] * r["w"]
+        w = r["oc"] * (r["c"] // r["group"]) * r["kh"] * r["kw"]
+        y = r["n"] * r["oc"] * r["oh"] * r["ow"]
+        res = y if r["act"] in (4, 5) else 0
+        alg.append(4.0 * (x + w + r["oc"] + y + res))
+    return sum(alg) / len(alg)
+
+
+def traffic_summary(d: Path, batch: int, policy: str, commands: list) -> dict:
+    """Reduce the four rocprofv3 --pmc counter CSVs under `d` (calib_{FETCH,WRITE}_SIZE
+    from the calibration kernels, r101_{FETCH,WRITE}_SIZE from --profile-pass) to
+    calibrated HBM-side bytes per conv_igemm_kernel dispatch."""
+    import csv
+
+    def rows(name):
+        with open(d / f"{name}_counter_collection.csv") as f:
+            return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in csv.DictReader(f)]
+
+    kib = CALIB_BYTES / 1024
+
+    def calib(counter, kind):
+        v = [x for n, x in rows(f"calib_{counter}") if kind in n.lower()]
+        v = v[1:] if len(v) > 1 else v  # first launch of each warms the caches
+        return sum(v) / len(v)
+
+    f_fetch = kib / calib("FETCH_SIZE", "copy")
+    f_write = kib / calib("WRITE_SIZE", "fill")
+    per = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        v = [x for n, x in rows(f"r101_{counter}") if "conv_igemm_kernel" in n]
+        per[counter] = (len(v), sum(v) / len(v))
+    fetch_b = per["FETCH_SIZE"][1] * 1024 * f_fetch
+    write_b = per["WRITE_SIZE"][1] * 1024 * f_write
+    return {
+        "kernel": f"conv_igemm_kernel (all tile instantiations), implicit-GEMM layers of ResNet-101 v1.5 fp32 "
+                  f"batch {batch}",
+        "conv_policy": policy, "batch": batch, "commands": commands,
+        "calibration": {"method": "256 MiB fills (spinn_hip_fill_u32) and 256 MiB device copies (spinn_hip_copy) "
+                                  "under the same counters (bench.py --calibration-kernels); factor = true KiB / "
+                                  "counter KiB, first launch of each dropped",
+                        "fetch_factor": round(f_fetch, 4), "write_factor": round(f_write, 4)},
+        "dispatches": per["FETCH_SIZE"][0],
+        "fetch_kib_per_dispatch_raw": round(per["FETCH_SIZE"][1], 1),
+        "write_kib_per_dispatch_raw": round(per["WRITE_SIZE"][1], 1),
+        "fetch_bytes_per_launch": round(fetch_b), "write_bytes_per_launch": round(write_b),
+        "traffic_bytes_per_launch": round(fetch_b + write_b),
+        "algorithmic_bytes_per_launch": round(igemm_algorithmic_bytes(batch, policy)),
+        "note": "FETCH_SIZE / WRITE_SIZE count traffic between the L2s and the memory fabric, so hits in the "
+                "Infinity Cache (MALL) count as HBM traffic here",
+    }
+
+
+def measured_traffic(batch: int, policy: str):
+    """Calibrated HBM-side bytes per implicit-GEMM launch from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes, when they match this workload."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    d = json.loads(TRAFFIC_FILE.read_text())
+    if d.get("batch") != batch or d.get("conv_policy") != policy:
+        return None
+    return d.get("traffic_bytes_per_launch")
+
+
 def time_steps(sess, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         sess.run_resident()
@@ -231,11 +329,27 @@ def main() -> int:
                          "kernel profiler wraps, so its kernel statistics cover exactly the measured launches")
     ap.add_argument("--layers-out", default=str(ROOT / "gpurun_out" / "bench_layers.json"))
     ap.add_argument("--no-suite", action="store_true", help="skip the config-0 / Gemm sweep / VGG measurements")
+    ap.add_argument("--calibration-kernels", action="store_true",
+                    help="only run the known-size fill/copy kernels that scale the HBM byte counters")
+    ap.add_argument("--traffic-summary", metavar="DIR",
+                    help="reduce rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE CSVs in DIR to the traffic file (no GPU)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
               "(the path shards by batch with no collective; see DESIGN.md)", file=sys.stderr)
         return 2
+    if a.calibration_kernels:
+        calibration_kernels()
+        return 0
+    if a.traffic_summary:
+        cmds = [f"rocprofv3 --pmc {c} --output-format csv -d {a.traffic_summary} -o {o}_{c} -- python -u bench.py {f}"
+                for c in ("FETCH_SIZE", "WRITE_SIZE")
+                for o, f in (("calib", "--calibration-kernels"),
+                             ("r101", f"--profile-pass --steps 2 --warmup 1 --no-cpu --batch {a.batch}"))]
+        s = traffic_summary(Path(a.traffic_summary), a.batch, a.policy, cmds)
+        TRAFFIC_FILE.write_text(json.dumps(s, indent=1) + "\n")
+        print(json.dumps(s))
+        return 0
 
     from spinn_amd import models
     from spinn_amd import native as N
@@ -351,7 +465,8 @@ def main() -> int:
         "conv_frac_mfma_peak": round(conv_tflops * 1e12 / PEAK_FP32_MFMA, 4),
         "conv_share_of_node_time": round(tot_t / all_ms, 4) if all_ms > 0 else None,
         "roofline": {"bound": "mfma", "achieved": round(ig_tflops, 3), "peak": PEAK_FP32_MFMA / 1e12,
-                     "unit": "TFLOP/s", "frac": round(ig_tflops * 1e12 / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(ig_tflops * 1e12 / PEAK_FP32_MFMA, 4),
+                     "traffic": measured_traffic(a.batch, a.policy),
                      "kernel": f"conv_igemm_kernel (implicit-GEMM conv, {n_ig} layers, batch {a.batch})"},
         "cpu_baseline": cpu,
         "other_configs": other,

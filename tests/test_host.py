@@ -230,3 +230,34 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_bench_traffic_summary_scaling(tmp_path, monkeypatch):
+    """The counter reduction: calibration factors from the known-size copy/fill,
+    first launch of each dropped, only conv_igemm_kernel dispatches averaged."""
+    import sys
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    kib = bench.CALIB_BYTES // 1024
+
+    def write(name, rows):
+        lines = ["Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value"]
+        lines += [f"{i},{k},X,{v}" for i, (k, v) in enumerate(rows)]
+        (tmp_path / f"{name}_counter_collection.csv").write_text("\n".join(lines) + "\n")
+
+    # counters read half the copy's true bytes and the fill's exactly; cold first launches differ
+    write("calib_FETCH_SIZE", [("fill_u32_kernel", 7), ("fill_u32_kernel", 5), ("copy_kernel", 999),
+                               ("copy_kernel", kib / 2), ("copy_kernel", kib / 2)])
+    write("calib_WRITE_SIZE", [("fill_u32_kernel", 1), ("fill_u32_kernel", kib), ("fill_u32_kernel", kib),
+                               ("copy_kernel", kib)])
+    write("r101_FETCH_SIZE", [("void conv_igemm_kernel<64>", 100.0), ("maxpool_kernel", 5000.0),
+                              ("void conv_igemm_kernel<128>", 300.0)])
+    write("r101_WRITE_SIZE", [("void conv_igemm_kernel<64>", 10.0), ("void conv_igemm_kernel<128>", 30.0)])
+    monkeypatch.setattr(bench, "igemm_algorithmic_bytes", lambda b, p: 1.0)
+    s = bench.traffic_summary(tmp_path, 32, "auto", [])
+    assert s["calibration"]["fetch_factor"] == 2.0 and s["calibration"]["write_factor"] == 1.0
+    assert s["dispatches"] == 2
+    assert s["fetch_bytes_per_launch"] == 200 * 1024 * 2
+    assert s["write_bytes_per_launch"] == 20 * 1024
+    assert s["traffic_bytes_per_launch"] == 200 * 1024 * 2 + 20 * 1024
