@@ -208,6 +208,17 @@ typedef struct {
     int32_t axis;
 } ENNF_AxisParams; /* Softmax, Flatten, Concat (SPINN/ennf_op_params.h:114-168) */
 
+typedef struct {
+    int32_t axis;
+    uint32_t num_outputs; /* split sizes come from the output tensors' dims */
+} ENNF_SplitParams;       /* SPINN/ennf_op_params.h:171-175 */
+
+typedef struct {
+    uint8_t perm[ENNF_MAX_DIMS];
+    uint8_t num_dims;
+    uint8_t reserved[3];
+} ENNF_TransposeParams; /* SPINN/ennf_op_params.h:147-151 */
+
 #if defined(__cplusplus)
 #define ENNF_STATIC_ASSERT(c, m) static_assert(c, m)
 #else
@@ -221,6 +232,9 @@ ENNF_STATIC_ASSERT(sizeof(ENNF_ConvParams) == 44, "ENNF_ConvParams must be 44 by
 ENNF_STATIC_ASSERT(sizeof(ENNF_PoolParams) == 48, "ENNF_PoolParams must be 48 bytes");
 ENNF_STATIC_ASSERT(sizeof(ENNF_GemmParams) == 12, "ENNF_GemmParams must be 12 bytes");
 ENNF_STATIC_ASSERT(sizeof(ENNF_ReduceParams) == 36, "ENNF_ReduceParams must be 36 bytes");
+ENNF_STATIC_ASSERT(sizeof(ENNF_SplitParams) == 8, "ENNF_SplitParams must be 8 bytes");
+ENNF_STATIC_ASSERT(sizeof(ENNF_TransposeParams) == 12, "ENNF_TransposeParams must be 12 bytes");
+ENNF_STATIC_ASSERT(sizeof(ENNF_BatchNormParams) == 12, "ENNF_BatchNormParams must be 12 bytes");
 
 static inline size_t ennf_dtype_bytes(int dtype) {
     switch (dtype) {

@@ -122,6 +122,61 @@ int spinn_hip_reduce_mean(int64_t outer, int64_t dim, int64_t inner, const float
  * (SPINN/run_time/ops/shape/reshape.c:6-14, SPINN/run_time/ops/tensor/flatten.c:3-8). */
 int spinn_hip_copy(void *dst, const void *src, size_t bytes, void *stream);
 
+/* ---- unfused graph nodes: elementwise, normalisation, layout (fp32) ---- */
+
+enum { SPINN_BINARY_ADD = 0, SPINN_BINARY_SUB = 1, SPINN_BINARY_MUL = 2, SPINN_BINARY_DIV = 3 };
+
+/* y[i] = a[i % na] (op) b[i % nb] for 0 <= i < n: the reference's broadcast rule
+ * (SPINN/run_time/ops/math/add.c:14-19, sub.c:16-18, mul.c:20-60). DIV replaces
+ * a divisor with |b| < 1e-6 by +1e-6 (SPINN/run_time/ops/math/div.c:24-28).
+ * n, na, nb < 2^32 (the reference's element counts are uint32). */
+int spinn_hip_binary(int op, const float *a, int64_t na, const float *b, int64_t nb, float *y, int64_t n,
+                     void *stream);
+
+enum { SPINN_UNARY_RELU = 0, SPINN_UNARY_SIGMOID = 1, SPINN_UNARY_SILU = 2 };
+
+/* y = max(x, 0) (SPINN/run_time/ops/activation/relu.c:4-16), y = 1/(1+exp(-x))
+ * (SPINN/run_time/ops/activation/sigmoid.c:7-25), y = x/(1+exp(-x)). */
+int spinn_hip_unary(int op, const float *x, float *y, int64_t n, void *stream);
+
+/* Inference BatchNormalization over x [n, c, spatial]:
+ * alpha = scale[c] / sqrt(var[c] + eps), y = x * alpha + (bias[c] - mean[c] * alpha)
+ * (SPINN/run_time/ops/norm/batch_norm.c:17-76). */
+int spinn_hip_batchnorm(int64_t n, int64_t c, int64_t spatial, const float *x, const float *scale,
+                        const float *bias, const float *mean, const float *var, float eps, float *y,
+                        void *stream);
+
+/* Softmax over the middle axis of an [outer, dim, inner] view: y = exp(x - max) / sum
+ * (SPINN/run_time/ops/activation/softmax.c:109-170). */
+int spinn_hip_softmax(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, void *stream);
+
+/* One strided block copy of a Concat input or a Split output: for o < outer and
+ * j < len, dst[o * dst_row + dst_off + j] = src[o * src_row + src_off + j] (elements). */
+typedef struct {
+    const float *src;
+    float *dst;
+    int64_t src_row, src_off;
+    int64_t dst_row, dst_off;
+    int64_t len;
+} SpinnHipBlockCopy;
+
+#define SPINN_HIP_MAX_BLOCKS 16
+
+/* Concat (SPINN/run_time/ops/tensor/concat.c:5-26) and Split
+ * (SPINN/run_time/ops/tensor/split.c:5-26) as up to SPINN_HIP_MAX_BLOCKS block
+ * copies in one launch; blocks must not overlap in dst. */
+int spinn_hip_block_copy(const SpinnHipBlockCopy *blocks, int n_blocks, int64_t outer, void *stream);
+
+/* Transpose of an ndim <= 8 tensor of < 2^32 elements: y's dim d is x's dim perm[d]
+ * (SPINN/run_time/ops/shape/transpose.c:14-104; perm = NULL reverses the dims, as there). */
+int spinn_hip_transpose(int ndim, const int64_t *dims, const int32_t *perm, const float *x, float *y,
+                        void *stream);
+
+/* Nearest Resize of nc planes h x w -> oh x ow: y[p, i, j] = x[p, i*h/oh, j*w/ow]
+ * with integer division (SPINN/run_time/ops/tensor/resize.c:4-31). */
+int spinn_hip_resize_nearest(int64_t nc, int32_t h, int32_t w, int32_t oh, int32_t ow, const float *x, float *y,
+                             void *stream);
+
 /* ---- device, memory, stream, event and graph plumbing for the host runtime ---- */
 
 int spinn_hip_init(int device);

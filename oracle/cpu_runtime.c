@@ -226,6 +226,82 @@ static int run_node(OracleModel *m, ON *n) {
     case ENNF_OP_Identity:
         memcpy(Y->data, X->data, X->bytes < Y->bytes ? X->bytes : Y->bytes);
         return 0;
+    case ENNF_OP_Add:
+    case ENNF_OP_Sub:
+    case ENNF_OP_Mul:
+    case ENNF_OP_Div: {
+        OT *B = &m->t[n->in[1]];
+        if (n->nin < 2 || X->elems == 0 || B->elems == 0) return n->nin < 2 ? -1 : 0;
+        const int op = n->op == ENNF_OP_Add ? 0 : n->op == ENNF_OP_Sub ? 1 : n->op == ENNF_OP_Mul ? 2 : 3;
+        oracle_binary(op, (const float *)X->data, X->elems, (const float *)B->data, B->elems, (float *)Y->data,
+                      Y->elems);
+        return 0;
+    }
+    case ENNF_OP_Relu:
+    case ENNF_OP_Sigmoid:
+        oracle_unary(n->op == ENNF_OP_Relu ? 0 : 1, (const float *)X->data, (float *)Y->data, X->elems);
+        return 0;
+    case ENNF_OP_BatchNormalization: {
+        if (n->nin < 5) return -1;
+        const ENNF_BatchNormParams *p =
+            n->psize >= sizeof(ENNF_BatchNormParams) ? (const ENNF_BatchNormParams *)n->params : NULL;
+        long spatial = 1;
+        for (int d = 2; d < X->ndim; d++) spatial *= X->dims[d];
+        oracle_batchnorm(X->dims[0], X->dims[1], spatial, (const float *)X->data,
+                         (const float *)m->t[n->in[1]].data, (const float *)m->t[n->in[2]].data,
+                         (const float *)m->t[n->in[3]].data, (const float *)m->t[n->in[4]].data,
+                         p ? p->epsilon : 1e-5f, (float *)Y->data);
+        return 0;
+    }
+    case ENNF_OP_Softmax:
+    case ENNF_OP_Concat:
+    case ENNF_OP_Split: {
+        /* axis defaults: Softmax -1, Concat / Split 0 (softmax.c:113, concat.c:7, split.c:7) */
+        int axis = n->op == ENNF_OP_Softmax ? -1 : 0;
+        if (n->psize >= 4) memcpy(&axis, n->params, 4);
+        if (axis < 0) axis += X->ndim;
+        if (axis < 0 || axis >= X->ndim) return -1;
+        long outer = 1, inner = 1;
+        for (int d = 0; d < axis; d++) outer *= X->dims[d];
+        for (int d = axis + 1; d < X->ndim; d++) inner *= X->dims[d];
+        if (n->op == ENNF_OP_Softmax) {
+            oracle_softmax(outer, X->dims[axis], inner, (const float *)X->data, (float *)Y->data);
+        } else if (n->op == ENNF_OP_Concat) {
+            const float *xs[16];
+            long sizes[16];
+            for (int t = 0; t < n->nin; t++) {
+                xs[t] = (const float *)m->t[n->in[t]].data;
+                sizes[t] = m->t[n->in[t]].dims[axis];
+            }
+            oracle_concat(n->nin, xs, sizes, outer, inner, (float *)Y->data);
+        } else {
+            float *ys[16];
+            long sizes[16];
+            for (int t = 0; t < n->nout; t++) {
+                ys[t] = (float *)m->t[n->out[t]].data;
+                sizes[t] = m->t[n->out[t]].dims[axis];
+            }
+            oracle_split(n->nout, ys, sizes, outer, inner, (const float *)X->data);
+        }
+        return 0;
+    }
+    case ENNF_OP_Transpose: {
+        long dims[8];
+        int perm[8];
+        for (int d = 0; d < X->ndim; d++) {
+            dims[d] = X->dims[d];
+            perm[d] = X->ndim - 1 - d;
+        }
+        if (n->psize >= sizeof(ENNF_TransposeParams))
+            for (int d = 0; d < X->ndim; d++) perm[d] = ((const ENNF_TransposeParams *)n->params)->perm[d];
+        oracle_transpose(X->ndim, dims, perm, (const float *)X->data, (float *)Y->data);
+        return 0;
+    }
+    case ENNF_OP_Resize:
+        if (X->ndim != 4 || Y->ndim != 4) return -1;
+        oracle_resize_nearest((long)X->dims[0] * X->dims[1], X->dims[2], X->dims[3], Y->dims[2], Y->dims[3],
+                              (const float *)X->data, (float *)Y->data);
+        return 0;
     default:
         fprintf(stderr, "oracle: op %d not implemented\n", n->op);
         return -2;

@@ -31,6 +31,15 @@ int oracle_matmul(int batch, int M, int N, int K, const float *A, const float *B
 void oracle_maxpool(int N, int C, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW, int PH, int PW,
                     const float *X, float *Y);
 void oracle_reduce_mean(long outer, long dim, long inner, const float *X, float *Y);
+void oracle_binary(int op, const float *a, uint32_t na, const float *b, uint32_t nb, float *y, uint32_t n);
+void oracle_unary(int op, const float *x, float *y, long n);
+void oracle_batchnorm(long N, long C, long spatial, const float *X, const float *scale, const float *bias,
+                      const float *mean, const float *var, float eps, float *Y);
+void oracle_softmax(long outer, long dim, long inner, const float *X, float *Y);
+void oracle_concat(int n_in, const float *const *xs, const long *sizes, long outer, long inner, float *Y);
+void oracle_split(int n_out, float *const *ys, const long *sizes, long outer, long inner, const float *X);
+void oracle_transpose(int ndim, const long *dims, const int *perm, const float *X, float *Y);
+void oracle_resize_nearest(long planes, int H, int W, int OH, int OW, const float *X, float *Y);
 int oracle_num_threads(void);
 void oracle_set_num_threads(int n);
 

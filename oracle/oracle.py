@@ -63,6 +63,14 @@ def lib() -> C.CDLL:
         L.oracle_model_tensor.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]
         L.oracle_model_set_winograd.argtypes = [C.c_void_p, C.c_int]
         L.oracle_model_num_nodes.argtypes = [C.c_void_p]
+        L.oracle_binary.argtypes = [C.c_int, _FP, C.c_uint32, _FP, C.c_uint32, _FP, C.c_uint32]
+        L.oracle_unary.argtypes = [C.c_int, _FP, _FP, C.c_long]
+        L.oracle_batchnorm.argtypes = [C.c_long, C.c_long, C.c_long, _FP, _FP, _FP, _FP, _FP, C.c_float, _FP]
+        L.oracle_softmax.argtypes = [C.c_long, C.c_long, C.c_long, _FP, _FP]
+        L.oracle_concat.argtypes = [C.c_int, C.POINTER(_FP), C.POINTER(C.c_long), C.c_long, C.c_long, _FP]
+        L.oracle_split.argtypes = [C.c_int, C.POINTER(_FP), C.POINTER(C.c_long), C.c_long, C.c_long, _FP]
+        L.oracle_transpose.argtypes = [C.c_int, C.POINTER(C.c_long), C.POINTER(C.c_int), _FP, _FP]
+        L.oracle_resize_nearest.argtypes = [C.c_long, C.c_int, C.c_int, C.c_int, C.c_int, _FP, _FP]
         _lib = L
     return _lib
 
@@ -152,6 +160,91 @@ def maxpool(x, oh, ow, kh, kw, sh, sw, ph, pw) -> np.ndarray:
 def reduce_mean(x, outer, dim, inner) -> np.ndarray:
     y = np.zeros(outer * inner, np.float32)
     lib().oracle_reduce_mean(outer, dim, inner, _f(np.ascontiguousarray(x, np.float32)), _f(y))
+    return y
+
+
+BINARY_OPS = {"add": 0, "sub": 1, "mul": 2, "div": 3}
+UNARY_OPS = {"relu": 0, "sigmoid": 1, "silu": 2}
+
+
+def _c(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def binary(op: str, a, b, out_shape) -> np.ndarray:
+    """y[i] = a[i % a.size] op b[i % b.size] over prod(out_shape) outputs."""
+    a, b = _c(a), _c(b)
+    y = np.zeros(out_shape, np.float32)
+    lib().oracle_binary(BINARY_OPS[op], _f(a), a.size, _f(b), b.size, _f(y), y.size)
+    return y
+
+
+def unary(op: str, x) -> np.ndarray:
+    x = _c(x)
+    y = np.zeros_like(x)
+    lib().oracle_unary(UNARY_OPS[op], _f(x), _f(y), x.size)
+    return y
+
+
+def batchnorm(x, scale, bias, mean, var, eps=1e-5) -> np.ndarray:
+    x = _c(x)
+    y = np.zeros_like(x)
+    spatial = int(np.prod(x.shape[2:])) if x.ndim > 2 else 1
+    lib().oracle_batchnorm(x.shape[0], x.shape[1], spatial, _f(x), _f(_c(scale)), _f(_c(bias)), _f(_c(mean)),
+                           _f(_c(var)), eps, _f(y))
+    return y
+
+
+def _view(shape, axis):
+    axis = axis % len(shape)
+    return int(np.prod(shape[:axis])), int(np.prod(shape[axis + 1:])), axis
+
+
+def softmax(x, axis=-1) -> np.ndarray:
+    x = _c(x)
+    y = np.zeros_like(x)
+    outer, inner, axis = _view(x.shape, axis)
+    lib().oracle_softmax(outer, x.shape[axis], inner, _f(x), _f(y))
+    return y
+
+
+def concat(xs, axis) -> np.ndarray:
+    xs = [_c(x) for x in xs]
+    outer, inner, axis = _view(xs[0].shape, axis)
+    shape = list(xs[0].shape)
+    shape[axis] = sum(x.shape[axis] for x in xs)
+    y = np.zeros(shape, np.float32)
+    ptrs = (_FP * len(xs))(*[_f(x) for x in xs])
+    sizes = (C.c_long * len(xs))(*[x.shape[axis] for x in xs])
+    lib().oracle_concat(len(xs), ptrs, sizes, outer, inner, _f(y))
+    return y
+
+
+def split(x, sizes, axis) -> list:
+    x = _c(x)
+    outer, inner, axis = _view(x.shape, axis)
+    ys = []
+    for s in sizes:
+        shape = list(x.shape)
+        shape[axis] = s
+        ys.append(np.zeros(shape, np.float32))
+    ptrs = (_FP * len(ys))(*[_f(y) for y in ys])
+    lib().oracle_split(len(ys), ptrs, (C.c_long * len(sizes))(*sizes), outer, inner, _f(x))
+    return ys
+
+
+def transpose(x, perm) -> np.ndarray:
+    x = _c(x)
+    y = np.zeros([x.shape[p] for p in perm], np.float32)
+    lib().oracle_transpose(x.ndim, (C.c_long * x.ndim)(*x.shape), (C.c_int * x.ndim)(*perm), _f(x), _f(y))
+    return y
+
+
+def resize_nearest(x, oh, ow) -> np.ndarray:
+    x = _c(x)
+    n, c, h, w = x.shape
+    y = np.zeros((n, c, oh, ow), np.float32)
+    lib().oracle_resize_nearest(n * c, h, w, oh, ow, _f(x), _f(y))
     return y
 
 

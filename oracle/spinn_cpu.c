@@ -18,6 +18,8 @@
  *   conv operator          SPINN/run_time/ops/conv/conv2d.c:92-232
  *   Gemm / MatMul          SPINN/run_time/ops/mm/gemm.c:7-78, matmul.c:6-62
  *   Winograd F(2x2,3x3)    SPINN/run_time/ops/conv/winograd.c:23-210
+ *   unfused nodes          SPINN/run_time/ops/math/{add,sub,mul,div}.c, activation/{relu,sigmoid,softmax}.c,
+ *                          norm/batch_norm.c, tensor/{concat,split,resize}.c, shape/transpose.c
  *
  * Deliberate differences from the reference (documented defects):
  *   - the conv epilogue (bias, residual, ReLU/SiLU) is applied on every path;
@@ -528,6 +530,123 @@ void oracle_reduce_mean(long outer, long dim, long inner, const float *X, float 
             for (long j = 0; j < dim; j++) s += X[(i * dim + j) * inner + k];
             Y[i * inner + k] = s / (float)dim;
         }
+}
+
+/* ---------------- unfused graph nodes ---------------- */
+/* y[i] = a[i % na] op b[i % nb] (SPINN/run_time/ops/math/add.c:14-19, sub.c:16-18,
+ * mul.c:20-60 - the scalar and same-size fast paths compute the same values;
+ * div.c:22-28 with its |b| < 1e-6 -> 1e-6 substitution). op: 0 add 1 sub 2 mul 3 div. */
+void oracle_binary(int op, const float *a, uint32_t na, const float *b, uint32_t nb, float *y, uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) {
+        const float x = a[i % na];
+        float v = b[i % nb];
+        switch (op) {
+        case 0: y[i] = x + v; break;
+        case 1: y[i] = x - v; break;
+        case 2: y[i] = x * v; break;
+        default:
+            if (fabsf(v) < 1e-6f) v = 1e-6f;
+            y[i] = x / v;
+        }
+    }
+}
+
+/* op 0: ReLU (SPINN/run_time/ops/activation/relu.c:12-14); op 1: Sigmoid
+ * 1/(1+expf(-x)) (sigmoid.c:21-23); op 2: SiLU x/(1+expf(-x)) (gemm_kernel.c:333). */
+void oracle_unary(int op, const float *x, float *y, long n) {
+    for (long i = 0; i < n; i++) {
+        const float v = x[i];
+        y[i] = op == 0 ? (v > 0 ? v : 0) : op == 1 ? 1.0f / (1.0f + expf(-v)) : v / (1.0f + expf(-v));
+    }
+}
+
+/* Inference BatchNormalization (SPINN/run_time/ops/norm/batch_norm.c:37-73). */
+void oracle_batchnorm(long N, long C, long spatial, const float *X, const float *scale, const float *bias,
+                      const float *mean, const float *var, float eps, float *Y) {
+    for (long n = 0; n < N; n++)
+        for (long c = 0; c < C; c++) {
+            const float inv_std = 1.0f / sqrtf(var[c] + eps);
+            const float alpha = scale[c] * inv_std;
+            const float beta = bias[c] - mean[c] * alpha;
+            const float *x = X + (n * C + c) * spatial;
+            float *y = Y + (n * C + c) * spatial;
+            for (long i = 0; i < spatial; i++) y[i] = fmaf(x[i], alpha, beta);
+        }
+}
+
+/* Softmax over the middle axis of [outer, dim, inner]: max, exp(x - max) with a
+ * running sum, then one scale by 1/sum, sum 0 -> 1e-10
+ * (SPINN/run_time/ops/activation/softmax.c:139-168). */
+void oracle_softmax(long outer, long dim, long inner, const float *X, float *Y) {
+    for (long i = 0; i < outer; i++)
+        for (long k = 0; k < inner; k++) {
+            const long base = i * dim * inner + k;
+            float mx = X[base];
+            for (long j = 1; j < dim; j++)
+                if (X[base + j * inner] > mx) mx = X[base + j * inner];
+            float sum = 0;
+            for (long j = 0; j < dim; j++) {
+                const float v = expf(X[base + j * inner] - mx);
+                Y[base + j * inner] = v;
+                sum += v;
+            }
+            if (sum == 0) sum = 1e-10f;
+            const float s = 1.0f / sum;
+            for (long j = 0; j < dim; j++) Y[base + j * inner] *= s;
+        }
+}
+
+/* Concat: per outer row, each input's sizes[t] * inner floats in turn
+ * (SPINN/run_time/ops/tensor/concat.c:13-24). */
+void oracle_concat(int n_in, const float *const *xs, const long *sizes, long outer, long inner, float *Y) {
+    long off = 0;
+    for (long o = 0; o < outer; o++)
+        for (int t = 0; t < n_in; t++) {
+            const long len = sizes[t] * inner;
+            memcpy(Y + off, xs[t] + o * len, (size_t)len * sizeof(float));
+            off += len;
+        }
+}
+
+/* Split: the inverse walk (SPINN/run_time/ops/tensor/split.c:13-24). */
+void oracle_split(int n_out, float *const *ys, const long *sizes, long outer, long inner, const float *X) {
+    long off = 0;
+    for (long o = 0; o < outer; o++)
+        for (int t = 0; t < n_out; t++) {
+            const long len = sizes[t] * inner;
+            memcpy(ys[t] + o * len, X + off, (size_t)len * sizeof(float));
+            off += len;
+        }
+}
+
+/* Transpose: output dim d is input dim perm[d]; output order walk
+ * (SPINN/run_time/ops/shape/transpose.c:22-104). */
+void oracle_transpose(int ndim, const long *dims, const int *perm, const float *X, float *Y) {
+    long in_stride[8], odims[8], step[8], coord[8] = {0}, total = 1;
+    in_stride[ndim - 1] = 1;
+    for (int d = ndim - 2; d >= 0; d--) in_stride[d] = in_stride[d + 1] * dims[d + 1];
+    for (int d = 0; d < ndim; d++) {
+        odims[d] = dims[perm[d]];
+        step[d] = in_stride[perm[d]];
+        total *= odims[d];
+    }
+    for (long e = 0; e < total; e++) {
+        long off = 0;
+        for (int d = 0; d < ndim; d++) off += coord[d] * step[d];
+        Y[e] = X[off];
+        for (int d = ndim - 1; d >= 0; d--) {
+            if (++coord[d] < odims[d]) break;
+            coord[d] = 0;
+        }
+    }
+}
+
+/* Nearest Resize with integer source index i*H/OH (SPINN/run_time/ops/tensor/resize.c:18-29). */
+void oracle_resize_nearest(long planes, int H, int W, int OH, int OW, const float *X, float *Y) {
+    for (long p = 0; p < planes; p++)
+        for (int h = 0; h < OH; h++)
+            for (int w = 0; w < OW; w++)
+                Y[(p * OH + h) * OW + w] = X[(p * H + (long)h * H / OH) * W + (long)w * W / OW];
 }
 
 int oracle_num_threads(void) {

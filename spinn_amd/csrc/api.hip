@@ -164,6 +164,75 @@ int spinn_hip_copy(void *dst, const void *src, size_t bytes, void *stream) {
     return hip_code(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
 }
 
+int spinn_hip_binary(int op, const float *a, int64_t na, const float *b, int64_t nb, float *y, int64_t n,
+                     void *stream) {
+    constexpr int64_t kMax = (int64_t)UINT32_MAX;
+    if (op < SPINN_BINARY_ADD || op > SPINN_BINARY_DIV || n < 0 || n > kMax || na > kMax || nb > kMax)
+        return SPINN_HIP_EINVAL;
+    if (n == 0) return SPINN_HIP_OK;
+    if (!a || !b || !y || na <= 0 || nb <= 0) return SPINN_HIP_EINVAL;
+    return binary_op(op, a, na, b, nb, y, n, (hipStream_t)stream);
+}
+
+int spinn_hip_unary(int op, const float *x, float *y, int64_t n, void *stream) {
+    if (op < SPINN_UNARY_RELU || op > SPINN_UNARY_SILU || n < 0) return SPINN_HIP_EINVAL;
+    if (n == 0) return SPINN_HIP_OK;
+    if (!x || !y) return SPINN_HIP_EINVAL;
+    return unary_op(op, x, y, n, (hipStream_t)stream);
+}
+
+int spinn_hip_batchnorm(int64_t n, int64_t c, int64_t spatial, const float *x, const float *scale,
+                        const float *bias, const float *mean, const float *var, float eps, float *y,
+                        void *stream) {
+    if (n < 0 || c < 0 || spatial < 0) return SPINN_HIP_EINVAL;
+    if (n * c * spatial == 0) return SPINN_HIP_OK;
+    if (!x || !scale || !bias || !mean || !var || !y) return SPINN_HIP_EINVAL;
+    return batchnorm(n, c, spatial, x, scale, bias, mean, var, eps, y, (hipStream_t)stream);
+}
+
+int spinn_hip_softmax(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, void *stream) {
+    if (outer < 0 || dim < 0 || inner < 0) return SPINN_HIP_EINVAL;
+    if (outer * dim * inner == 0) return SPINN_HIP_OK;
+    if (!x || !y) return SPINN_HIP_EINVAL;
+    return softmax(outer, dim, inner, x, y, (hipStream_t)stream);
+}
+
+int spinn_hip_block_copy(const SpinnHipBlockCopy *blocks, int n_blocks, int64_t outer, void *stream) {
+    if (!blocks || n_blocks < 0 || n_blocks > SPINN_HIP_MAX_BLOCKS || outer < 0) return SPINN_HIP_EINVAL;
+    for (int i = 0; i < n_blocks; ++i) {
+        const SpinnHipBlockCopy &b = blocks[i];
+        if (b.len < 0 || b.src_row < 0 || b.dst_row < 0 || b.src_off < 0 || b.dst_off < 0) return SPINN_HIP_EINVAL;
+        if (b.len > 0 && outer > 0 && (!b.src || !b.dst)) return SPINN_HIP_EINVAL;
+    }
+    return block_copy(blocks, n_blocks, outer, (hipStream_t)stream);
+}
+
+int spinn_hip_transpose(int ndim, const int64_t *dims, const int32_t *perm, const float *x, float *y,
+                        void *stream) {
+    if (ndim < 1 || ndim > 8 || !dims) return SPINN_HIP_EINVAL;
+    int64_t total = 1;
+    unsigned seen = 0;
+    for (int d = 0; d < ndim; ++d) {
+        if (dims[d] < 0) return SPINN_HIP_EINVAL;
+        total *= dims[d];
+        if (perm) {
+            if (perm[d] < 0 || perm[d] >= ndim || (seen >> perm[d] & 1u)) return SPINN_HIP_EINVAL;
+            seen |= 1u << perm[d];
+        }
+    }
+    if (total == 0) return SPINN_HIP_OK;
+    if (!x || !y || total > (int64_t)UINT32_MAX) return SPINN_HIP_EINVAL;
+    return transpose(ndim, dims, perm, x, y, (hipStream_t)stream);
+}
+
+int spinn_hip_resize_nearest(int64_t nc, int32_t h, int32_t w, int32_t oh, int32_t ow, const float *x, float *y,
+                             void *stream) {
+    if (nc < 0 || h <= 0 || w <= 0 || oh < 0 || ow < 0) return SPINN_HIP_EINVAL;
+    if (nc * oh * ow == 0) return SPINN_HIP_OK;
+    if (!x || !y) return SPINN_HIP_EINVAL;
+    return resize_nearest(nc, h, w, oh, ow, x, y, (hipStream_t)stream);
+}
+
 int spinn_hip_init(int device) { return hip_code(hipSetDevice(device)); }
 
 int spinn_hip_device_count(int *count) {

@@ -383,6 +383,211 @@ int op_copy_alias(SpinnTensor **in, int n_in, void *params, uint16_t params_size
 }
 
 /* ------------------------------------------------------------------------
+ * Unfused graph nodes: what graph_opt leaves behind when a Conv cannot absorb
+ * the activation or the Add (SPINN/graph_opt.c:301-374), and the tensor ops of
+ * detector heads and attention blocks.
+ * ---------------------------------------------------------------------- */
+
+/* Add / Sub / Mul / Div with the reference's modulo broadcast
+ * (SPINN/run_time/ops/math/add.c:4-21, sub.c:5-20, mul.c:11-63, div.c:5-30). */
+static int binary_node(int op, SpinnTensor **in, int n_in, SpinnTensor **out, int n_out) {
+    if (n_in < 2 || n_out < 1) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_binary(op, (const float *)in[0]->data, in[0]->elem_count, (const float *)in[1]->data,
+                            in[1]->elem_count, (float *)out[0]->data, out[0]->elem_count, g_spinn_exec.stream);
+}
+
+int op_add(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    return binary_node(SPINN_BINARY_ADD, in, n_in, out, n_out);
+}
+
+int op_sub(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    return binary_node(SPINN_BINARY_SUB, in, n_in, out, n_out);
+}
+
+int op_mul(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    return binary_node(SPINN_BINARY_MUL, in, n_in, out, n_out);
+}
+
+/* Div: fp32 only here (the reference also divides int32/int64 tensors,
+ * div.c:31-48, which the conv path never produces); an empty operand is a no-op. */
+int op_div(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 2 || n_out < 1) return -1;
+    if (in[0]->elem_count == 0 || in[1]->elem_count == 0) return 0;
+    if (in[0]->dtype != ENNF_TYPE_FLOAT32) return SPINN_HIP_EUNSUPPORTED;
+    return binary_node(SPINN_BINARY_DIV, in, n_in, out, n_out);
+}
+
+static int unary_node(int op, SpinnTensor **in, int n_in, SpinnTensor **out, int n_out) {
+    if (n_in < 1 || n_out < 1) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_unary(op, (const float *)in[0]->data, (float *)out[0]->data, in[0]->elem_count,
+                           g_spinn_exec.stream);
+}
+
+/* SPINN/run_time/ops/activation/relu.c:4-16 */
+int op_relu(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    return unary_node(SPINN_UNARY_RELU, in, n_in, out, n_out);
+}
+
+/* SPINN/run_time/ops/activation/sigmoid.c:7-25 */
+int op_sigmoid(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    return unary_node(SPINN_UNARY_SIGMOID, in, n_in, out, n_out);
+}
+
+/* BatchNormalization, inputs X, scale, B, mean, var; eps from the params,
+ * default 1e-5 (SPINN/run_time/ops/norm/batch_norm.c:17-76). */
+int op_batch_norm(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 5 || n_out < 1) return -1;
+    SpinnTensor *X = in[0];
+    if (X->ndim < 2) return -1;
+    float eps = 1e-5f;
+    if (params && params_size >= sizeof(ENNF_BatchNormParams)) eps = ((const ENNF_BatchNormParams *)params)->epsilon;
+    int64_t spatial = 1;
+    for (int d = 2; d < X->ndim; d++) spatial *= X->dims[d];
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_batchnorm(X->dims[0], X->dims[1], spatial, (const float *)X->data, (const float *)in[1]->data,
+                               (const float *)in[2]->data, (const float *)in[3]->data, (const float *)in[4]->data,
+                               eps, (float *)out[0]->data, g_spinn_exec.stream);
+}
+
+/* [outer, dim, inner] view of `t` around `axis` (already normalised). */
+static void axis_view(const SpinnTensor *t, int axis, int64_t *outer, int64_t *inner) {
+    int64_t o = 1, i = 1;
+    for (int d = 0; d < axis; d++) o *= t->dims[d];
+    for (int d = axis + 1; d < t->ndim; d++) i *= t->dims[d];
+    *outer = o;
+    *inner = i;
+}
+
+/* Softmax along `axis` (default -1) (SPINN/run_time/ops/activation/softmax.c:109-170). */
+int op_softmax(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 1 || n_out < 1) return -1;
+    int axis = -1;
+    if (params && params_size >= sizeof(ENNF_AxisParams)) axis = ((const ENNF_AxisParams *)params)->axis;
+    const int ndim = in[0]->ndim;
+    if (axis < 0) axis += ndim;
+    if (axis < 0 || axis >= ndim) return -1;
+    int64_t outer, inner;
+    axis_view(in[0], axis, &outer, &inner);
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_softmax(outer, in[0]->dims[axis], inner, (const float *)in[0]->data, (float *)out[0]->data,
+                             g_spinn_exec.stream);
+}
+
+/* Concat along `axis` (default 0 without params): each input is one run of
+ * dims[axis] * inner floats per outer row (SPINN/run_time/ops/tensor/concat.c:5-26). */
+int op_concat(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 1 || n_out < 1) return -1;
+    int axis = 0;
+    if (params && params_size >= sizeof(ENNF_AxisParams)) axis = ((const ENNF_AxisParams *)params)->axis;
+    const int ndim = in[0]->ndim;
+    if (axis < 0) axis += ndim;
+    if (axis < 0 || axis >= ndim) return -1;
+    int64_t outer, inner;
+    axis_view(in[0], axis, &outer, &inner);
+    int64_t row = 0;
+    for (int t = 0; t < n_in; t++) {
+        if (in[t]->ndim <= axis) return -1;
+        row += (int64_t)in[t]->dims[axis] * inner;
+    }
+    if (outer * row > (int64_t)out[0]->elem_count) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    SpinnHipBlockCopy blocks[SPINN_HIP_MAX_BLOCKS];
+    int64_t off = 0;
+    for (int t0 = 0; t0 < n_in; t0 += SPINN_HIP_MAX_BLOCKS) {
+        int nb = 0;
+        for (int t = t0; t < n_in && nb < SPINN_HIP_MAX_BLOCKS; t++, nb++) {
+            const int64_t len = (int64_t)in[t]->dims[axis] * inner;
+            blocks[nb] = (SpinnHipBlockCopy){(const float *)in[t]->data, (float *)out[0]->data, len, 0, row, off, len};
+            off += len;
+        }
+        int rc = spinn_hip_block_copy(blocks, nb, outer, g_spinn_exec.stream);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+/* Split along `axis` (default 0); the piece sizes are the outputs' dims[axis]
+ * (SPINN/run_time/ops/tensor/split.c:5-26). */
+int op_split(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 1 || n_out < 1) return -1;
+    int axis = 0;
+    if (params && params_size >= sizeof(ENNF_SplitParams)) axis = ((const ENNF_SplitParams *)params)->axis;
+    const int ndim = in[0]->ndim;
+    if (axis < 0) axis += ndim;
+    if (axis < 0 || axis >= ndim) return -1;
+    int64_t outer, inner;
+    axis_view(in[0], axis, &outer, &inner);
+    int64_t row = 0;
+    for (int t = 0; t < n_out; t++) {
+        if (out[t]->ndim <= axis) return -1;
+        row += (int64_t)out[t]->dims[axis] * inner;
+    }
+    if (outer * row > (int64_t)in[0]->elem_count) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    SpinnHipBlockCopy blocks[SPINN_HIP_MAX_BLOCKS];
+    int64_t off = 0;
+    for (int t0 = 0; t0 < n_out; t0 += SPINN_HIP_MAX_BLOCKS) {
+        int nb = 0;
+        for (int t = t0; t < n_out && nb < SPINN_HIP_MAX_BLOCKS; t++, nb++) {
+            const int64_t len = (int64_t)out[t]->dims[axis] * inner;
+            blocks[nb] = (SpinnHipBlockCopy){(const float *)in[0]->data, (float *)out[t]->data, row, off, len, 0, len};
+            off += len;
+        }
+        int rc = spinn_hip_block_copy(blocks, nb, outer, g_spinn_exec.stream);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+/* Transpose by perm from the params, else reversed dims
+ * (SPINN/run_time/ops/shape/transpose.c:14-104). */
+int op_transpose(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    if (n_in < 1 || n_out < 1) return -1;
+    const int ndim = in[0]->ndim;
+    if (ndim < 1 || ndim > ENNF_MAX_DIMS) return -1;
+    int64_t dims[ENNF_MAX_DIMS];
+    int32_t perm[ENNF_MAX_DIMS];
+    for (int d = 0; d < ndim; d++) {
+        dims[d] = in[0]->dims[d];
+        perm[d] = ndim - 1 - d;
+    }
+    if (params && params_size >= sizeof(ENNF_TransposeParams)) {
+        const ENNF_TransposeParams *p = (const ENNF_TransposeParams *)params;
+        for (int d = 0; d < ndim; d++) perm[d] = p->perm[d];
+    }
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_transpose(ndim, dims, perm, (const float *)in[0]->data, (float *)out[0]->data,
+                               g_spinn_exec.stream);
+}
+
+/* Resize, nearest only, sizes from the tensors (SPINN/run_time/ops/tensor/resize.c:4-31). */
+int op_resize(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 1 || n_out < 1) return -1;
+    SpinnTensor *X = in[0], *Y = out[0];
+    if (X->ndim != 4 || Y->ndim != 4) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_resize_nearest((int64_t)X->dims[0] * X->dims[1], (int)X->dims[2], (int)X->dims[3],
+                                    (int)Y->dims[2], (int)Y->dims[3], (const float *)X->data, (float *)Y->data,
+                                    g_spinn_exec.stream);
+}
+
+/* ------------------------------------------------------------------------
  * Registry and dispatcher (SPINN/run_time/spinn_ops.c:17-228)
  * ---------------------------------------------------------------------- */
 static SpinnOpKernel g_op_registry[ENNF_OP_REGISTRY_SIZE];
@@ -399,6 +604,18 @@ static void registry_init(void) {
     g_op_registry[ENNF_OP_Reshape] = op_copy_alias;
     g_op_registry[ENNF_OP_Flatten] = op_copy_alias;
     g_op_registry[ENNF_OP_Identity] = op_copy_alias;
+    g_op_registry[ENNF_OP_Add] = op_add;
+    g_op_registry[ENNF_OP_Sub] = op_sub;
+    g_op_registry[ENNF_OP_Mul] = op_mul;
+    g_op_registry[ENNF_OP_Div] = op_div;
+    g_op_registry[ENNF_OP_Relu] = op_relu;
+    g_op_registry[ENNF_OP_Sigmoid] = op_sigmoid;
+    g_op_registry[ENNF_OP_BatchNormalization] = op_batch_norm;
+    g_op_registry[ENNF_OP_Softmax] = op_softmax;
+    g_op_registry[ENNF_OP_Concat] = op_concat;
+    g_op_registry[ENNF_OP_Split] = op_split;
+    g_op_registry[ENNF_OP_Transpose] = op_transpose;
+    g_op_registry[ENNF_OP_Resize] = op_resize;
     g_registry_ready = 1;
 }
 

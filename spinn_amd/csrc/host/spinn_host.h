@@ -41,6 +41,20 @@ int op_global_avg_pool(SpinnTensor **in, int n_in, void *params, uint16_t params
                        int n_out);
 int op_reduce_mean(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out);
 int op_copy_alias(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out);
+#define SPINN_DECLARE_OP(name) \
+    int name(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out)
+SPINN_DECLARE_OP(op_add);
+SPINN_DECLARE_OP(op_sub);
+SPINN_DECLARE_OP(op_mul);
+SPINN_DECLARE_OP(op_div);
+SPINN_DECLARE_OP(op_relu);
+SPINN_DECLARE_OP(op_sigmoid);
+SPINN_DECLARE_OP(op_batch_norm);
+SPINN_DECLARE_OP(op_softmax);
+SPINN_DECLARE_OP(op_concat);
+SPINN_DECLARE_OP(op_split);
+SPINN_DECLARE_OP(op_transpose);
+SPINN_DECLARE_OP(op_resize);
 
 /* Build the conv descriptor exactly as op_conv2d reads its operands. */
 int spinn_conv_desc_from_tensors(SpinnTensor **in, int n_in, const void *params, uint16_t params_size,

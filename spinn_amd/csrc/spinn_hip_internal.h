@@ -61,4 +61,14 @@ int maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, hipStream_t s
 int reduce_mean(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, hipStream_t st);
 int fill_u32(void *dst, uint32_t value, size_t bytes, hipStream_t st);
 
+// unfused graph nodes (tensor_ops.hip)
+int binary_op(int op, const float *a, int64_t na, const float *b, int64_t nb, float *y, int64_t n, hipStream_t st);
+int unary_op(int op, const float *x, float *y, int64_t n, hipStream_t st);
+int batchnorm(int64_t n, int64_t c, int64_t spatial, const float *x, const float *scale, const float *bias,
+              const float *mean, const float *var, float eps, float *y, hipStream_t st);
+int softmax(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, hipStream_t st);
+int block_copy(const SpinnHipBlockCopy *blocks, int n_blocks, int64_t outer, hipStream_t st);
+int transpose(int ndim, const int64_t *dims, const int32_t *perm, const float *x, float *y, hipStream_t st);
+int resize_nearest(int64_t nc, int h, int w, int oh, int ow, const float *x, float *y, hipStream_t st);
+
 } // namespace spinn

@@ -1,0 +1,437 @@
+// tensor_ops.hip - bandwidth kernels for the graph nodes that stay unfused:
+// broadcast binary ops, activations, inference BatchNorm, Softmax, Concat /
+// Split block copies, Transpose and nearest Resize. All fp32, all HBM-bound:
+// float4 loads and stores wherever sizes and addresses allow, consecutive
+// lanes on consecutive addresses, no division in the per-element loop except
+// the broadcast modulo the reference's rule needs.
+#include "spinn_hip_internal.h"
+
+#include <math.h>
+
+namespace spinn {
+namespace {
+
+constexpr int kThreads = 256;
+
+int grid_1d(int64_t work_items, int cap = 1 << 16) {
+    return (int)std::max<int64_t>(1, std::min<int64_t>((work_items + kThreads - 1) / kThreads, cap));
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <int OP>
+__device__ __forceinline__ float binop(float a, float b) {
+    if constexpr (OP == SPINN_BINARY_ADD) {
+        return a + b;
+    } else if constexpr (OP == SPINN_BINARY_SUB) {
+        return a - b;
+    } else if constexpr (OP == SPINN_BINARY_MUL) {
+        return a * b;
+    } else {
+        if (fabsf(b) < 1e-6f) b = 1e-6f; // SPINN/run_time/ops/math/div.c:26
+        return a / b;
+    }
+}
+
+// y[i] = a[i % na] op b[i % nb]. VEC: n, na, nb are multiples of 4 and every
+// pointer is 16-byte aligned, so each group of 4 outputs reads 4 consecutive
+// elements of a and of b.
+template <int OP, bool VEC>
+__global__ __launch_bounds__(kThreads) void binary_kernel(const float *__restrict__ a, uint32_t na,
+                                                          const float *__restrict__ b, uint32_t nb,
+                                                          float *__restrict__ y, uint32_t n) {
+    const uint64_t stride = (uint64_t)gridDim.x * kThreads;
+    if constexpr (VEC) {
+        const uint64_t n4 = n / 4;
+        for (uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x; e < n4; e += stride) {
+            const uint32_t i = (uint32_t)(e * 4);
+            const uint32_t ia = (na == n) ? i : i % na;
+            const uint32_t ib = (nb == n) ? i : i % nb;
+            const float4 va = *reinterpret_cast<const float4 *>(a + ia);
+            const float4 vb = *reinterpret_cast<const float4 *>(b + ib);
+            float4 r;
+            r.x = binop<OP>(va.x, vb.x);
+            r.y = binop<OP>(va.y, vb.y);
+            r.z = binop<OP>(va.z, vb.z);
+            r.w = binop<OP>(va.w, vb.w);
+            *reinterpret_cast<float4 *>(y + i) = r;
+        }
+    } else {
+        for (uint64_t e = (uint64_t)blockIdx.x * kThreads + threadIdx.x; e < n; e += stride) {
+            const uint32_t i = (uint32_t)e;
+            const uint32_t ia = (na == n) ? i : i % na;
+            const uint32_t ib = (nb == n) ? i : i % nb;
+            y[i] = binop<OP>(a[ia], b[ib]);
+        }
+    }
+}
+
+template <int OP>
+__device__ __forceinline__ float unop(float x) {
+    if constexpr (OP == SPINN_UNARY_RELU) {
+        return x > 0.f ? x : 0.f;
+    } else if constexpr (OP == SPINN_UNARY_SIGMOID) {
+        return 1.0f / (1.0f + expf(-x));
+    } else {
+        return x / (1.0f + expf(-x));
+    }
+}
+
+template <int OP, bool VEC>
+__global__ __launch_bounds__(kThreads) void unary_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                         int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    if constexpr (VEC) {
+        for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < n / 4; e += stride) {
+            const float4 v = reinterpret_cast<const float4 *>(x)[e];
+            float4 r;
+            r.x = unop<OP>(v.x);
+            r.y = unop<OP>(v.y);
+            r.z = unop<OP>(v.z);
+            r.w = unop<OP>(v.w);
+            reinterpret_cast<float4 *>(y)[e] = r;
+        }
+    } else {
+        for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < n; e += stride) y[e] = unop<OP>(x[e]);
+    }
+}
+
+// One (image, channel) plane per blockIdx.y (grid-strided), lanes along the plane.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void batchnorm_kernel(const float *__restrict__ x,
+                                                             const float *__restrict__ scale,
+                                                             const float *__restrict__ bias,
+                                                             const float *__restrict__ mean,
+                                                             const float *__restrict__ var, float eps,
+                                                             float *__restrict__ y, int64_t planes, int64_t c,
+                                                             int64_t spatial) {
+    for (int64_t p = blockIdx.y; p < planes; p += gridDim.y) {
+        const int64_t ch = p % c;
+        const float inv_std = 1.0f / sqrtf(var[ch] + eps);
+        const float alpha = scale[ch] * inv_std;
+        const float beta = bias[ch] - mean[ch] * alpha;
+        const float *xp = x + p * spatial;
+        float *yp = y + p * spatial;
+        if constexpr (VEC) {
+            for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < spatial / 4;
+                 e += (int64_t)gridDim.x * kThreads) {
+                const float4 v = reinterpret_cast<const float4 *>(xp)[e];
+                float4 r;
+                r.x = fmaf(v.x, alpha, beta);
+                r.y = fmaf(v.y, alpha, beta);
+                r.z = fmaf(v.z, alpha, beta);
+                r.w = fmaf(v.w, alpha, beta);
+                reinterpret_cast<float4 *>(yp)[e] = r;
+            }
+        } else {
+            for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < spatial;
+                 e += (int64_t)gridDim.x * kThreads)
+                yp[e] = fmaf(xp[e], alpha, beta);
+        }
+    }
+}
+
+// Running (max, sum of exp(x - max)) pair; merging keeps sum relative to the larger max.
+struct MaxSum {
+    float m, s;
+};
+
+__device__ __forceinline__ MaxSum ms_push(MaxSum a, float v) {
+    if (v > a.m) {
+        a.s = a.s * expf(a.m - v) + 1.0f;
+        a.m = v;
+    } else {
+        a.s += expf(v - a.m);
+    }
+    return a;
+}
+
+__device__ __forceinline__ MaxSum ms_merge(MaxSum a, MaxSum b) {
+    if (b.s == 0.f) return a;
+    if (a.s == 0.f) return b;
+    const float m = fmaxf(a.m, b.m);
+    return {m, a.s * expf(a.m - m) + b.s * expf(b.m - m)};
+}
+
+// inner == 1: one wave per row; lanes stride the row, then a shuffle tree.
+__global__ __launch_bounds__(kThreads) void softmax_rows_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                                int64_t rows, int64_t dim) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * kThreads) >> 6;
+    for (int64_t r = wave; r < rows; r += nwaves) {
+        const float *xp = x + r * dim;
+        float *yp = y + r * dim;
+        MaxSum acc{-INFINITY, 0.f};
+        for (int64_t j = lane; j < dim; j += 64) acc = ms_push(acc, xp[j]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            MaxSum o{__shfl_xor(acc.m, off, 64), __shfl_xor(acc.s, off, 64)};
+            acc = ms_merge(acc, o);
+        }
+        const float sum = acc.s == 0.f ? 1e-10f : acc.s; // SPINN/run_time/ops/activation/softmax.c:94
+        const float inv = 1.0f / sum;
+        for (int64_t j = lane; j < dim; j += 64) yp[j] = expf(xp[j] - acc.m) * inv;
+    }
+}
+
+// inner > 1: one thread per (outer, inner) column, consecutive threads on inner.
+__global__ __launch_bounds__(kThreads) void softmax_cols_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                                int64_t outer, int64_t dim, int64_t inner) {
+    const int64_t total = outer * inner;
+    for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < total; e += (int64_t)gridDim.x * kThreads) {
+        const int64_t o = e / inner;
+        const int64_t k = e - o * inner;
+        const float *xp = x + o * dim * inner + k;
+        float *yp = y + o * dim * inner + k;
+        MaxSum acc{-INFINITY, 0.f};
+        for (int64_t j = 0; j < dim; ++j) acc = ms_push(acc, xp[j * inner]);
+        const float sum = acc.s == 0.f ? 1e-10f : acc.s;
+        const float inv = 1.0f / sum;
+        for (int64_t j = 0; j < dim; ++j) yp[j * inner] = expf(xp[j * inner] - acc.m) * inv;
+    }
+}
+
+struct BlockCopyArgs {
+    SpinnHipBlockCopy b[SPINN_HIP_MAX_BLOCKS];
+    int64_t outer;
+};
+
+// blockIdx.y selects the block copy, blockIdx.z strides the outer rows and
+// x-lanes run along the contiguous run. VEC: every length, row, offset and
+// pointer is a multiple of 4 floats, so the run moves as float4.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void block_copy_kernel(BlockCopyArgs args) {
+    const SpinnHipBlockCopy bk = args.b[blockIdx.y];
+    for (int64_t o = blockIdx.z; o < args.outer; o += gridDim.z) {
+        const float *s = bk.src + o * bk.src_row + bk.src_off;
+        float *d = bk.dst + o * bk.dst_row + bk.dst_off;
+        if constexpr (VEC) {
+            for (int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x; j < bk.len / 4;
+                 j += (int64_t)gridDim.x * kThreads)
+                reinterpret_cast<float4 *>(d)[j] = reinterpret_cast<const float4 *>(s)[j];
+        } else {
+            for (int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x; j < bk.len; j += (int64_t)gridDim.x * kThreads)
+                d[j] = s[j];
+        }
+    }
+}
+
+constexpr int kMaxDims = 8;
+
+struct TransposeArgs {
+    int ndim;
+    uint32_t odims[kMaxDims]; // output dims
+    int64_t step[kMaxDims];   // input stride of each output dim
+    int64_t total;
+};
+
+// General permutation: one thread per output element in output order (stores
+// coalesced), the input offset assembled from the output coordinates.
+__global__ __launch_bounds__(kThreads) void transpose_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                             TransposeArgs t) {
+    for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < t.total; e += (int64_t)gridDim.x * kThreads) {
+        uint64_t rem = (uint64_t)e;
+        int64_t off = 0;
+        for (int d = t.ndim - 1; d >= 0; --d) {
+            const uint64_t q = rem / t.odims[d];
+            off += (int64_t)(rem - q * t.odims[d]) * t.step[d];
+            rem = q;
+        }
+        y[e] = x[off];
+    }
+}
+
+// Batched 2-D transpose [batch][rows][cols] -> [batch][cols][rows] through a
+// 32 x 33 LDS tile: reads and writes both run along rows of 32 lanes.
+__global__ __launch_bounds__(kThreads) void transpose2d_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                               int64_t batch, int64_t rows, int64_t cols) {
+    __shared__ float tile[32][33];
+    const int64_t tiles_r = (rows + 31) / 32, tiles_c = (cols + 31) / 32;
+    const int64_t per_batch = tiles_r * tiles_c;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5; // 32 x 8
+    for (int64_t t = blockIdx.x; t < batch * per_batch; t += gridDim.x) {
+        const int64_t bidx = t / per_batch;
+        const int64_t rem = t - bidx * per_batch;
+        const int64_t r0 = (rem / tiles_c) * 32, c0 = (rem % tiles_c) * 32;
+        const float *xb = x + bidx * rows * cols;
+        float *yb = y + bidx * rows * cols;
+#pragma unroll
+        for (int k = 0; k < 32; k += 8) {
+            const int64_t r = r0 + ty + k, c = c0 + tx;
+            if (r < rows && c < cols) tile[ty + k][tx] = xb[r * cols + c];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 32; k += 8) {
+            const int64_t c = c0 + ty + k, r = r0 + tx;
+            if (r < rows && c < cols) yb[c * rows + r] = tile[tx][ty + k];
+        }
+        __syncthreads();
+    }
+}
+
+// blockIdx.y strides the output rows (plane * oh + i), x-lanes run along a row.
+__global__ __launch_bounds__(kThreads) void resize_nearest_kernel(const float *__restrict__ x,
+                                                                  float *__restrict__ y, int64_t nc, int h, int w,
+                                                                  int oh, int ow) {
+    for (int64_t row = blockIdx.y; row < nc * oh; row += gridDim.y) {
+        const int64_t p = row / oh;
+        const int i = (int)(row - p * oh);
+        const int hi = (int)((int64_t)i * h / oh);
+        const float *xr = x + (p * h + hi) * (int64_t)w;
+        float *yr = y + row * (int64_t)ow;
+        for (int j = blockIdx.x * kThreads + threadIdx.x; j < ow; j += gridDim.x * kThreads)
+            yr[j] = xr[(int64_t)j * w / ow];
+    }
+}
+
+template <int OP>
+int launch_binary(const float *a, uint32_t na, const float *b, uint32_t nb, float *y, uint32_t n, hipStream_t st) {
+    const bool vec = n % 4 == 0 && na % 4 == 0 && nb % 4 == 0 && aligned16(a) && aligned16(b) && aligned16(y);
+    if (vec)
+        hipLaunchKernelGGL((binary_kernel<OP, true>), dim3(grid_1d(n / 4)), dim3(kThreads), 0, st, a, na, b, nb, y, n);
+    else
+        hipLaunchKernelGGL((binary_kernel<OP, false>), dim3(grid_1d(n)), dim3(kThreads), 0, st, a, na, b, nb, y, n);
+    return check_launch();
+}
+
+template <int OP>
+int launch_unary(const float *x, float *y, int64_t n, hipStream_t st) {
+    if (n % 4 == 0 && aligned16(x) && aligned16(y))
+        hipLaunchKernelGGL((unary_kernel<OP, true>), dim3(grid_1d(n / 4)), dim3(kThreads), 0, st, x, y, n);
+    else
+        hipLaunchKernelGGL((unary_kernel<OP, false>), dim3(grid_1d(n)), dim3(kThreads), 0, st, x, y, n);
+    return check_launch();
+}
+
+} // namespace
+
+int binary_op(int op, const float *a, int64_t na, const float *b, int64_t nb, float *y, int64_t n, hipStream_t st) {
+    if (n == 0) return 0;
+    const uint32_t un = (uint32_t)n, ua = (uint32_t)na, ub = (uint32_t)nb;
+    switch (op) {
+    case SPINN_BINARY_ADD: return launch_binary<SPINN_BINARY_ADD>(a, ua, b, ub, y, un, st);
+    case SPINN_BINARY_SUB: return launch_binary<SPINN_BINARY_SUB>(a, ua, b, ub, y, un, st);
+    case SPINN_BINARY_MUL: return launch_binary<SPINN_BINARY_MUL>(a, ua, b, ub, y, un, st);
+    case SPINN_BINARY_DIV: return launch_binary<SPINN_BINARY_DIV>(a, ua, b, ub, y, un, st);
+    default: return SPINN_HIP_EINVAL;
+    }
+}
+
+int unary_op(int op, const float *x, float *y, int64_t n, hipStream_t st) {
+    if (n == 0) return 0;
+    switch (op) {
+    case SPINN_UNARY_RELU: return launch_unary<SPINN_UNARY_RELU>(x, y, n, st);
+    case SPINN_UNARY_SIGMOID: return launch_unary<SPINN_UNARY_SIGMOID>(x, y, n, st);
+    case SPINN_UNARY_SILU: return launch_unary<SPINN_UNARY_SILU>(x, y, n, st);
+    default: return SPINN_HIP_EINVAL;
+    }
+}
+
+int batchnorm(int64_t n, int64_t c, int64_t spatial, const float *x, const float *scale, const float *bias,
+              const float *mean, const float *var, float eps, float *y, hipStream_t st) {
+    const int64_t planes = n * c;
+    if (planes == 0 || spatial == 0) return 0;
+    const bool vec = spatial % 4 == 0 && aligned16(x) && aligned16(y);
+    const int64_t lanes = vec ? spatial / 4 : spatial;
+    const dim3 grid((unsigned)grid_1d(lanes, 64), (unsigned)std::min<int64_t>(planes, 65535));
+    if (vec)
+        hipLaunchKernelGGL(batchnorm_kernel<true>, grid, dim3(kThreads), 0, st, x, scale, bias, mean, var, eps, y,
+                           planes, c, spatial);
+    else
+        hipLaunchKernelGGL(batchnorm_kernel<false>, grid, dim3(kThreads), 0, st, x, scale, bias, mean, var, eps, y,
+                           planes, c, spatial);
+    return check_launch();
+}
+
+int softmax(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, hipStream_t st) {
+    if (outer * inner == 0 || dim == 0) return 0;
+    if (inner == 1)
+        hipLaunchKernelGGL(softmax_rows_kernel, dim3(grid_1d(outer * 64)), dim3(kThreads), 0, st, x, y, outer, dim);
+    else
+        hipLaunchKernelGGL(softmax_cols_kernel, dim3(grid_1d(outer * inner)), dim3(kThreads), 0, st, x, y, outer,
+                           dim, inner);
+    return check_launch();
+}
+
+int block_copy(const SpinnHipBlockCopy *blocks, int n_blocks, int64_t outer, hipStream_t st) {
+    if (outer == 0 || n_blocks == 0) return 0;
+    BlockCopyArgs args;
+    args.outer = outer;
+    bool vec = true;
+    int64_t longest = 0;
+    for (int i = 0; i < n_blocks; ++i) {
+        const SpinnHipBlockCopy &b = blocks[i];
+        args.b[i] = b;
+        vec = vec && aligned16(b.src) && aligned16(b.dst) && b.len % 4 == 0 && b.src_row % 4 == 0 &&
+              b.dst_row % 4 == 0 && b.src_off % 4 == 0 && b.dst_off % 4 == 0;
+        longest = std::max(longest, b.len);
+    }
+    if (longest == 0) return 0;
+    const dim3 grid((unsigned)grid_1d(vec ? longest / 4 : longest, 1024), (unsigned)n_blocks,
+                    (unsigned)std::min<int64_t>(outer, 65535));
+    if (vec)
+        hipLaunchKernelGGL(block_copy_kernel<true>, grid, dim3(kThreads), 0, st, args);
+    else
+        hipLaunchKernelGGL(block_copy_kernel<false>, grid, dim3(kThreads), 0, st, args);
+    return check_launch();
+}
+
+int transpose(int ndim, const int64_t *dims, const int32_t *perm, const float *x, float *y, hipStream_t st) {
+    int p[kMaxDims];
+    int64_t in_stride[kMaxDims];
+    int64_t total = 1;
+    for (int d = 0; d < ndim; ++d) total *= dims[d];
+    if (total == 0) return 0;
+    for (int d = 0; d < ndim; ++d) p[d] = perm ? perm[d] : ndim - 1 - d;
+    in_stride[ndim - 1] = 1;
+    for (int d = ndim - 2; d >= 0; --d) in_stride[d] = in_stride[d + 1] * dims[d + 1];
+    // Output dims with their input strides; drop size-1 dims, then merge
+    // neighbours that are also neighbours (in order) in the input.
+    int64_t od[kMaxDims], os[kMaxDims];
+    int m = 0;
+    for (int d = 0; d < ndim; ++d) {
+        const int64_t sz = dims[p[d]], stv = in_stride[p[d]];
+        if (sz == 1) continue;
+        if (m > 0 && os[m - 1] == stv * sz) {
+            od[m - 1] *= sz;
+            os[m - 1] = stv;
+        } else {
+            od[m] = sz;
+            os[m] = stv;
+            ++m;
+        }
+    }
+    if (m == 0 || (m == 1 && os[0] == 1))
+        return hip_code(hipMemcpyAsync(y, x, (size_t)total * sizeof(float), hipMemcpyDeviceToDevice, st));
+    // [batch][rows][cols] -> [batch][cols][rows]: output dims (batch?, cols, rows)
+    // with input strides (rows*cols, 1, cols).
+    if ((m == 2 && os[0] == 1 && os[1] == od[0]) ||
+        (m == 3 && os[1] == 1 && os[2] == od[1] && os[0] == od[1] * od[2])) {
+        const int64_t batch = m == 3 ? od[0] : 1;
+        const int64_t cols = od[m - 2], rows = od[m - 1];
+        const int64_t tiles = batch * ((rows + 31) / 32) * ((cols + 31) / 32);
+        hipLaunchKernelGGL(transpose2d_kernel, dim3((unsigned)std::min<int64_t>(tiles, 1 << 16)), dim3(kThreads), 0,
+                           st, x, y, batch, rows, cols);
+        return check_launch();
+    }
+    TransposeArgs t;
+    t.ndim = m;
+    t.total = total;
+    for (int d = 0; d < m; ++d) {
+        t.odims[d] = (uint32_t)od[d];
+        t.step[d] = os[d];
+    }
+    hipLaunchKernelGGL(transpose_kernel, dim3(grid_1d(total)), dim3(kThreads), 0, st, x, y, t);
+    return check_launch();
+}
+
+int resize_nearest(int64_t nc, int h, int w, int oh, int ow, const float *x, float *y, hipStream_t st) {
+    if (nc * oh * ow == 0) return 0;
+    const dim3 grid((unsigned)((ow + kThreads - 1) / kThreads), (unsigned)std::min<int64_t>(nc * oh, 65535));
+    hipLaunchKernelGGL(resize_nearest_kernel, grid, dim3(kThreads), 0, st, x, y, nc, h, w, oh, ow);
+    return check_launch();
+}
+
+} // namespace spinn

@@ -31,7 +31,7 @@ DT_FLOAT32, DT_INT64 = 1, 7
 _NP_DTYPE = {DT_FLOAT32: np.float32, DT_INT64: np.int64}
 
 # op ids (SPINN/ennf_op_types.h numeric values)
-OP_ADD, OP_MUL = 4, 39
+OP_ADD, OP_DIV, OP_MUL, OP_SUB = 4, 23, 39, 50
 OP_CONV, OP_AVGPOOL, OP_GAP, OP_MAXPOOL = 60, 80, 81, 85
 OP_BN, OP_RELU, OP_SIGMOID, OP_SOFTMAX = 100, 130, 133, 134
 OP_GEMM, OP_MATMUL = 160, 161

@@ -29,6 +29,9 @@ ALGO_AUTO, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_DIRECT = 0, 1, 2, 3
 ACT_NONE, ACT_RELU, ACT_CLIP, ACT_SILU, ACT_ADD, ACT_ADD_RELU = 0, 1, 2, 3, 4, 5
 ENNF_MAX_DIMS = 8
 POLICY_AUTO, POLICY_IGEMM, POLICY_WINOGRAD = 0, 1, 2
+BINARY_ADD, BINARY_SUB, BINARY_MUL, BINARY_DIV = 0, 1, 2, 3
+UNARY_RELU, UNARY_SIGMOID, UNARY_SILU = 0, 1, 2
+MAX_BLOCKS = 16
 
 
 class ConvDesc(C.Structure):
@@ -50,6 +53,11 @@ class GemmDesc(C.Structure):
 class PoolDesc(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n", "c", "h", "w", "oh", "ow", "kh", "kw", "sh", "sw", "ph", "pw")]
+
+
+class BlockCopy(C.Structure):
+    _fields_ = [("src", C.c_void_p), ("dst", C.c_void_p), ("src_row", C.c_int64), ("src_off", C.c_int64),
+                ("dst_row", C.c_int64), ("dst_off", C.c_int64), ("len", C.c_int64)]
 
 
 class SpinnTensor(C.Structure):
@@ -121,6 +129,17 @@ _SIGS = {
     "spinn_hip_maxpool2d": (C.c_int, [C.POINTER(PoolDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
     "spinn_hip_reduce_mean": (C.c_int, [C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]),
     "spinn_hip_copy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "spinn_hip_binary": (C.c_int, [C.c_int, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
+                                   C.c_void_p]),
+    "spinn_hip_unary": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
+    "spinn_hip_batchnorm": (C.c_int, [C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p,
+                                      C.c_void_p, C.c_void_p, C.c_float, C.c_void_p, C.c_void_p]),
+    "spinn_hip_softmax": (C.c_int, [C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "spinn_hip_block_copy": (C.c_int, [C.POINTER(BlockCopy), C.c_int, C.c_int64, C.c_void_p]),
+    "spinn_hip_transpose": (C.c_int, [C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_int32), C.c_void_p,
+                                      C.c_void_p, C.c_void_p]),
+    "spinn_hip_resize_nearest": (C.c_int, [C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
+                                           C.c_void_p, C.c_void_p]),
     "spinn_hip_init": (C.c_int, [C.c_int]),
     "spinn_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "spinn_hip_malloc": (C.c_int, [C.POINTER(C.c_void_p), C.c_size_t]),

@@ -5,7 +5,7 @@ with oracle/Makefile (the reference's run_time C sources compiled in place) and
 calls the reference functions on small seeded inputs. Each fixture is an .npz
 of inputs and the reference's outputs (no code), loaded with allow_pickle=False.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [planner conv epilogue gemm winograd tensor_ops]
 
 Fixtures:
   planner_offsets.npz   spinn_load + spinn_plan_memory offsets and peak for
@@ -18,6 +18,9 @@ Fixtures:
   gemm.npz              op_gemm (transB, bias vector / matrix) and op_matmul (batched)
   winograd.npz          winograd_pack_weight + winograd_conv_3x3 (SPINN/run_time/ops/conv/winograd.c)
                         on the identity KAT of SPINN/run_time/test_winograd2.c:56-63 and a seeded case
+  tensor_ops.npz        op_add / op_sub / op_mul / op_div (modulo broadcast), op_relu, op_sigmoid,
+                        op_batch_norm, op_softmax, op_concat, op_split, op_transpose, op_resize and
+                        op_maxpool 5x5 s1 p2 on small seeded inputs (the unfused nodes of a detector)
 """
 from __future__ import annotations
 
@@ -36,6 +39,8 @@ from spinn_amd import models  # noqa: E402
 from spinn_amd.native import SpinnTensor, SpinnContext  # noqa: E402  (same struct layout as the reference's)
 
 REF_LIB = ROOT / "oracle" / "_ref" / "libspinn_ref.so"
+TENSOR_OPS = ("op_add", "op_sub", "op_mul", "op_div", "op_relu", "op_sigmoid", "op_batch_norm", "op_softmax",
+              "op_concat", "op_split", "op_transpose", "op_resize", "op_maxpool")
 FP = C.POINTER(C.c_float)
 
 
@@ -48,7 +53,7 @@ def ref_lib() -> C.CDLL:
     L.spinn_free.argtypes = [C.c_void_p]
     sig = [C.POINTER(C.POINTER(SpinnTensor)), C.c_int, C.c_void_p, C.c_uint16, C.POINTER(C.POINTER(SpinnTensor)),
            C.c_int]
-    for f in ("op_conv2d", "op_gemm", "op_matmul"):
+    for f in ("op_conv2d", "op_gemm", "op_matmul") + TENSOR_OPS:
         getattr(L, f).argtypes = sig
         getattr(L, f).restype = C.c_int
     L.sgemm_nn.argtypes = [C.c_int, C.c_int, C.c_int, FP, C.c_int, FP, C.c_int, FP, C.c_int, FP, C.c_int, FP]
@@ -175,6 +180,63 @@ def epilogue(L):
     np.savez_compressed(HERE / "epilogue.npz", **out)
 
 
+def tensor_ops(L):
+    """The unfused operators on small seeded inputs: each case stores its inputs,
+    the params it was called with and the reference's outputs."""
+    import struct
+    from spinn_amd.ennf import pool_params
+    rng = np.random.default_rng(2024)
+    out = {}
+
+    def u(*shape, lo=-2.0, hi=2.0):
+        return rng.uniform(lo, hi, shape).astype(np.float32)
+
+    def case(name, op, ins, params, out_shapes):
+        ys = [np.zeros(sh, np.float32) for sh in out_shapes]
+        call_op(L, op, ins, params, ys)
+        for i, a in enumerate(ins):
+            out[f"{name}_in{i}"] = a
+        for i, y in enumerate(ys):
+            out[f"{name}_out{i}"] = y
+        out[f"{name}_params"] = np.frombuffer(params, np.uint8).copy() if params else np.zeros(0, np.uint8)
+
+    axis = lambda a: struct.pack("<i", a)  # noqa: E731
+    case("add_same", "op_add", [u(2, 3, 9), u(2, 3, 9)], b"", [(2, 3, 9)])
+    case("add_bcast", "op_add", [u(2, 3, 4), u(4)], b"", [(2, 3, 4)])
+    case("sub_anchor", "op_sub", [u(1, 2, 12), u(3, 2, 12)], b"", [(3, 2, 12)])
+    case("mul_stride", "op_mul", [u(2, 4, 12), u(1, 12)], b"", [(2, 4, 12)])
+    case("mul_scalar", "op_mul", [u(3, 11), np.array([0.17677669], np.float32)], b"", [(3, 11)])
+    case("mul_same", "op_mul", [u(5, 13), u(5, 13)], b"", [(5, 13)])
+    den = u(4, 5)
+    den[0, :3] = [0.0, 4e-7, -5e-7]
+    case("div_eps", "op_div", [u(4, 5), den], b"", [(4, 5)])
+    case("relu", "op_relu", [u(3, 7, 5)], b"", [(3, 7, 5)])
+    case("sigmoid", "op_sigmoid", [u(2, 19, lo=-9, hi=9)], b"", [(2, 19)])
+    c = 3
+    case("batch_norm", "op_batch_norm",
+         [u(2, c, 5, 5), u(c, lo=0.5, hi=1.5), u(c, lo=-0.2, hi=0.2), u(c, lo=-0.1, hi=0.1), u(c, lo=0.5, hi=1.5)],
+         struct.pack("<ffB3x", 1e-3, 0.9, 0), [(2, c, 5, 5)])
+    case("softmax_last", "op_softmax", [u(6, 21, lo=-5, hi=5)], axis(-1), [(6, 21)])
+    case("softmax_short", "op_softmax", [u(4, 5)], axis(1), [(4, 5)])
+    case("softmax_mid", "op_softmax", [u(2, 16, 4, 10, lo=-4, hi=4)], axis(1), [(2, 16, 4, 10)])
+    case("concat_c", "op_concat", [u(2, 2, 3, 3), u(2, 4, 3, 3), u(2, 1, 3, 3)], axis(1), [(2, 7, 3, 3)])
+    case("concat_last", "op_concat", [u(1, 5, 6), u(1, 5, 2), u(1, 5, 3)], axis(2), [(1, 5, 11)])
+    case("split_c", "op_split", [u(2, 6, 4, 4)], struct.pack("<iI", 1, 2), [(2, 2, 4, 4), (2, 4, 4, 4)])
+    case("split_qkv", "op_split", [u(1, 2, 8, 5)], struct.pack("<iI", 2, 3),
+         [(1, 2, 2, 5), (1, 2, 2, 5), (1, 2, 4, 5)])
+
+    def perm_params(perm):
+        return bytes(list(perm) + [0] * (8 - len(perm)) + [len(perm), 0, 0, 0])
+
+    case("transpose_dfl", "op_transpose", [u(2, 4, 6, 5)], perm_params((0, 2, 1, 3)), [(2, 6, 4, 5)])
+    case("transpose_last2", "op_transpose", [u(2, 3, 4, 5)], perm_params((0, 1, 3, 2)), [(2, 3, 5, 4)])
+    case("transpose_rev", "op_transpose", [u(3, 7)], b"", [(7, 3)])
+    case("resize_2x", "op_resize", [u(1, 3, 4, 5)], b"", [(1, 3, 8, 10)])
+    case("resize_odd", "op_resize", [u(2, 2, 5, 3)], b"", [(2, 2, 7, 8)])
+    case("maxpool_sppf", "op_maxpool", [u(1, 3, 7, 7)], pool_params(5, 5, 1, 1, (2, 2, 2, 2)), [(1, 3, 7, 7)])
+    np.savez_compressed(HERE / "tensor_ops.npz", **out)
+
+
 def gemm(L):
     from spinn_amd.ennf import gemm_params
     rng = np.random.default_rng(7)
@@ -225,11 +287,10 @@ def winograd(L):
 
 def main():
     L = ref_lib()
-    planner(L)
-    conv_cases(L)
-    epilogue(L)
-    gemm(L)
-    winograd(L)
+    steps = {"planner": planner, "conv": conv_cases, "epilogue": epilogue, "gemm": gemm, "winograd": winograd,
+             "tensor_ops": tensor_ops}
+    for name in sys.argv[1:] or list(steps):
+        steps[name](L)
     for f in sorted(HERE.glob("*.npz")):
         print(f"{f.name}: {f.stat().st_size} bytes")
 

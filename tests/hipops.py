@@ -70,3 +70,127 @@ def run_gemm(N, torch, a, b, c=None, alpha=1.0, beta=1.0, trans_a=0, trans_b=0, 
     N.check(L.spinn_hip_gemm(C.byref(d), _p(ad), _p(bd), _p(cd), _p(yd), _p(ws), wsz, None), "spinn_hip_gemm")
     torch.cuda.synchronize()
     return yd.cpu().numpy()
+
+
+def _out(torch, shape, offset=0):
+    """A NaN-filled device buffer of `shape`; offset > 0 starts it `offset`
+    floats into a larger allocation (a pointer that is not 16-byte aligned)."""
+    n = int(np.prod(shape))
+    base = torch.full((n + offset,), float("nan"), device="cuda", dtype=torch.float32)
+    return base[offset:].view(*shape) if len(shape) else base[offset:]
+
+
+def _in(torch, a, offset=0):
+    a = np.ascontiguousarray(a, np.float32)
+    t = _out(torch, a.shape, offset)
+    t.copy_(torch.from_numpy(a))
+    return t
+
+
+def _done(torch, t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def run_binary(N, torch, op, a, b, out_shape, offset=0):
+    ad, bd = _in(torch, a, offset), _in(torch, b, offset)
+    yd = _out(torch, out_shape, offset)
+    rc = N.lib().spinn_hip_binary(op, _p(ad), a.size, _p(bd), b.size, _p(yd), int(np.prod(out_shape)), None)
+    N.check(rc, "spinn_hip_binary")
+    return _done(torch, yd)
+
+
+def run_unary(N, torch, op, x, offset=0):
+    xd = _in(torch, x, offset)
+    yd = _out(torch, x.shape, offset)
+    N.check(N.lib().spinn_hip_unary(op, _p(xd), _p(yd), x.size, None), "spinn_hip_unary")
+    return _done(torch, yd)
+
+
+def run_batchnorm(N, torch, x, scale, bias, mean, var, eps, offset=0):
+    xd = _in(torch, x, offset)
+    sd, bd, md, vd = (_in(torch, v) for v in (scale, bias, mean, var))
+    yd = _out(torch, x.shape, offset)
+    spatial = int(np.prod(x.shape[2:])) if x.ndim > 2 else 1
+    rc = N.lib().spinn_hip_batchnorm(x.shape[0], x.shape[1], spatial, _p(xd), _p(sd), _p(bd), _p(md), _p(vd), eps,
+                                     _p(yd), None)
+    N.check(rc, "spinn_hip_batchnorm")
+    return _done(torch, yd)
+
+
+def run_softmax(N, torch, x, axis):
+    axis %= x.ndim
+    xd = _in(torch, x)
+    yd = _out(torch, x.shape)
+    outer, inner = int(np.prod(x.shape[:axis])), int(np.prod(x.shape[axis + 1:]))
+    N.check(N.lib().spinn_hip_softmax(outer, x.shape[axis], inner, _p(xd), _p(yd), None), "spinn_hip_softmax")
+    return _done(torch, yd)
+
+
+def _blocks(N, pieces):
+    arr = (N.BlockCopy * len(pieces))()
+    for i, (src, dst, src_row, src_off, dst_row, dst_off, ln) in enumerate(pieces):
+        arr[i] = N.BlockCopy(src.data_ptr(), dst.data_ptr(), src_row, src_off, dst_row, dst_off, ln)
+    return arr
+
+
+def run_concat(N, torch, xs, axis, offset=0):
+    """Concat as op_concat lays it out: one block copy per input."""
+    axis %= xs[0].ndim
+    outer, inner = int(np.prod(xs[0].shape[:axis])), int(np.prod(xs[0].shape[axis + 1:]))
+    shape = list(xs[0].shape)
+    shape[axis] = sum(x.shape[axis] for x in xs)
+    yd = _out(torch, shape, offset)
+    row = shape[axis] * inner
+    devs, pieces, off = [], [], 0
+    for x in xs:
+        xd = _in(torch, x, offset)
+        devs.append(xd)
+        ln = x.shape[axis] * inner
+        pieces.append((xd, yd, ln, 0, row, off, ln))
+        off += ln
+    N.check(N.lib().spinn_hip_block_copy(_blocks(N, pieces), len(pieces), outer, None), "spinn_hip_block_copy")
+    return _done(torch, yd)
+
+
+def run_split(N, torch, x, sizes, axis):
+    axis %= x.ndim
+    outer, inner = int(np.prod(x.shape[:axis])), int(np.prod(x.shape[axis + 1:]))
+    xd = _in(torch, x)
+    row = x.shape[axis] * inner
+    ys, pieces, off = [], [], 0
+    for s in sizes:
+        shape = list(x.shape)
+        shape[axis] = s
+        yd = _out(torch, shape)
+        ys.append(yd)
+        pieces.append((xd, yd, row, off, s * inner, 0, s * inner))
+        off += s * inner
+    N.check(N.lib().spinn_hip_block_copy(_blocks(N, pieces), len(pieces), outer, None), "spinn_hip_block_copy")
+    return [_done(torch, y) for y in ys]
+
+
+def run_transpose(N, torch, x, perm):
+    xd = _in(torch, x)
+    yd = _out(torch, [x.shape[p] for p in perm] if perm is not None else x.shape[::-1])
+    dims = (C.c_int64 * x.ndim)(*x.shape)
+    pm = (C.c_int32 * x.ndim)(*perm) if perm is not None else None
+    N.check(N.lib().spinn_hip_transpose(x.ndim, dims, pm, _p(xd), _p(yd), None), "spinn_hip_transpose")
+    return _done(torch, yd)
+
+
+def run_resize(N, torch, x, oh, ow):
+    n, c, h, w = x.shape
+    xd = _in(torch, x)
+    yd = _out(torch, (n, c, oh, ow))
+    N.check(N.lib().spinn_hip_resize_nearest(n * c, h, w, oh, ow, _p(xd), _p(yd), None), "spinn_hip_resize_nearest")
+    return _done(torch, yd)
+
+
+def run_maxpool(N, torch, x, oh, ow, kh, kw, sh, sw, ph, pw):
+    n, c, h, w = x.shape
+    xd = _in(torch, x)
+    yd = _out(torch, (n, c, oh, ow))
+    d = N.PoolDesc(n, c, h, w, oh, ow, kh, kw, sh, sw, ph, pw)
+    N.check(N.lib().spinn_hip_maxpool2d(C.byref(d), _p(xd), _p(yd), None), "spinn_hip_maxpool2d")
+    return _done(torch, yd)

@@ -1,0 +1,188 @@
+"""GPU parity of the unfused-node kernels (spinn_hip_binary / unary / batchnorm /
+softmax / block_copy / transpose / resize_nearest, and maxpool 5x5 s1) through
+the C ABI: against the reference's own outputs (tests/golden/tensor_ops.npz),
+against the oracle at detector-head sizes, on both the float4 and the scalar
+paths (16-byte aligned and misaligned buffers), and on the edge cases."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.conftest import assert_parity
+from tests.hipops import (run_batchnorm, run_binary, run_concat, run_maxpool, run_resize, run_softmax, run_split,
+                          run_transpose, run_unary)
+from tests.test_oracle import _ROUNDED, _params_axis, _tensor_op_cases
+
+pytestmark = pytest.mark.gpu
+
+BIN = {"add": 0, "sub": 1, "mul": 2, "div": 3}
+
+
+def _hip_tensor_op(N, torch, name, ins, prm, out_shapes):
+    op = name.split("_")[0]
+    if op in BIN:
+        return [run_binary(N, torch, BIN[op], ins[0], ins[1], out_shapes[0])]
+    if op in ("relu", "sigmoid"):
+        return [run_unary(N, torch, {"relu": 0, "sigmoid": 1}[op], ins[0])]
+    if op == "batch":
+        eps = float(np.frombuffer(prm[:4].tobytes(), np.float32)[0])
+        return [run_batchnorm(N, torch, *ins, eps)]
+    if op == "softmax":
+        return [run_softmax(N, torch, ins[0], _params_axis(prm, -1))]
+    if op == "concat":
+        return [run_concat(N, torch, ins, _params_axis(prm, 0))]
+    if op == "split":
+        ax = _params_axis(prm, 0)
+        return run_split(N, torch, ins[0], [sh[ax] for sh in out_shapes], ax)
+    if op == "transpose":
+        nd = ins[0].ndim
+        return [run_transpose(N, torch, ins[0], list(prm[:nd]) if prm.size else None)]
+    if op == "resize":
+        return [run_resize(N, torch, ins[0], *out_shapes[0][2:])]
+    if op == "maxpool":
+        return [run_maxpool(N, torch, ins[0], *out_shapes[0][2:], 5, 5, 1, 1, 2, 2)]
+    raise AssertionError(name)
+
+
+@pytest.mark.parametrize("case", list(_tensor_op_cases()), ids=lambda c: c[0])
+def test_matches_reference_fixture(hip, torch_gpu, case):
+    name, ins, prm, outs = case
+    print(f"[tensor-op] fixture {name}", flush=True)
+    got = _hip_tensor_op(hip, torch_gpu, name, ins, prm, [o.shape for o in outs])
+    for g, ref in zip(got, outs):
+        if name in _ROUNDED or name.startswith("div"):
+            np.testing.assert_allclose(g, ref, rtol=2e-6, atol=1e-7)
+        else:
+            np.testing.assert_array_equal(g, ref)
+
+
+@pytest.mark.parametrize("offset", [0, 1], ids=["vec4", "scalar"])
+def test_binary_broadcasts(hip, torch_gpu, offset):
+    rng = np.random.default_rng(11 + offset)
+    b16 = rng.uniform(-2, 2, (16, 4, 8400)).astype(np.float32)
+    strides = rng.uniform(8, 32, (1, 8400)).astype(np.float32)
+    anchors = rng.uniform(0, 80, (1, 2, 8400)).astype(np.float32)
+    lt = rng.uniform(0, 9, (16, 2, 8400)).astype(np.float32)
+    cases = [("mul", b16, strides, b16.shape), ("sub", anchors, lt, lt.shape), ("add", lt, anchors, lt.shape),
+             ("mul", np.array([0.1767767], np.float32), b16, b16.shape), ("add", lt, lt, lt.shape),
+             ("div", lt, anchors, lt.shape)]
+    for op, a, b, shape in cases:
+        print(f"[tensor-op] binary {op} {a.shape} {b.shape} offset {offset}", flush=True)
+        y = run_binary(hip, torch_gpu, BIN[op], a, b, shape, offset=offset)
+        ref = O.binary(op, a, b, shape)
+        if op == "div":
+            np.testing.assert_allclose(y, ref, rtol=1e-6)
+        else:
+            np.testing.assert_array_equal(y, ref)
+    # odd element counts (no float4 path even when aligned)
+    a = rng.uniform(-1, 1, 1001).astype(np.float32)
+    b = rng.uniform(-1, 1, 7).astype(np.float32)
+    np.testing.assert_array_equal(run_binary(hip, torch_gpu, 0, a, b, (1001,), offset), O.binary("add", a, b, (1001,)))
+
+
+@pytest.mark.parametrize("offset", [0, 1], ids=["vec4", "scalar"])
+def test_unary_and_batchnorm(hip, torch_gpu, offset):
+    rng = np.random.default_rng(21 + offset)
+    x = rng.uniform(-12, 12, (16, 80, 8400 // 4)).astype(np.float32)
+    for op, name in ((0, "relu"), (1, "sigmoid"), (2, "silu")):
+        print(f"[tensor-op] unary {name} offset {offset}", flush=True)
+        y = run_unary(hip, torch_gpu, op, x, offset)
+        if op == 0:
+            np.testing.assert_array_equal(y, O.unary(name, x))
+        else:
+            np.testing.assert_allclose(y, O.unary(name, x), rtol=2e-6, atol=1e-7)
+    for shape in ((2, 64, 40, 40), (3, 5, 7, 3), (4, 6)):
+        print(f"[tensor-op] batchnorm {shape} offset {offset}", flush=True)
+        xb = rng.uniform(-3, 3, shape).astype(np.float32)
+        c = shape[1]
+        p = [rng.uniform(0.5, 1.5, c).astype(np.float32) for _ in range(4)]
+        y = run_batchnorm(hip, torch_gpu, xb, *p, 1e-3, offset)
+        assert_parity(y, O.batchnorm(xb, *p, eps=1e-3), what=f"batchnorm {shape}")
+
+
+@pytest.mark.parametrize("shape,axis", [
+    ((32, 400, 400), -1),         # attention rows (batch 16 x 2 heads)
+    ((3, 8400), -1),              # one long row per wave
+    ((5, 1), -1),                 # dim 1
+    ((7, 37), -1),                # dim < wave size
+    ((16, 16, 4, 8400), 1),       # DFL: softmax over 16 bins, inner 33600
+    ((2, 3, 5), 0),               # outer 1
+], ids=["attn", "long", "dim1", "short", "dfl", "outer1"])
+def test_softmax(hip, torch_gpu, shape, axis):
+    print(f"[tensor-op] softmax {shape} axis {axis}", flush=True)
+    rng = np.random.default_rng(len(shape) * 100 + shape[-1])
+    x = rng.uniform(-8, 8, shape).astype(np.float32)
+    y = run_softmax(hip, torch_gpu, x, axis)
+    ref = O.softmax(x, axis)
+    np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(y.sum(axis=axis), 1.0, rtol=1e-5)
+
+
+@pytest.mark.parametrize("offset", [0, 1], ids=["vec4", "scalar"])
+def test_concat_split(hip, torch_gpu, offset):
+    rng = np.random.default_rng(31 + offset)
+    head = [rng.uniform(-1, 1, (16, 144, n)).astype(np.float32) for n in (6400, 1600, 400)]
+    print(f"[tensor-op] concat head offset {offset}", flush=True)
+    np.testing.assert_array_equal(run_concat(hip, torch_gpu, head, 2, offset), O.concat(head, 2))
+    c2f = [rng.uniform(-1, 1, (2, 32, 80, 80)).astype(np.float32) for _ in range(4)]
+    np.testing.assert_array_equal(run_concat(hip, torch_gpu, c2f, 1, offset), O.concat(c2f, 1))
+    odd = [rng.uniform(-1, 1, (3, k, 5)).astype(np.float32) for k in (1, 2, 3)]
+    np.testing.assert_array_equal(run_concat(hip, torch_gpu, odd, 1, offset), O.concat(odd, 1))
+    print("[tensor-op] split", flush=True)
+    qkv = rng.uniform(-1, 1, (16, 2, 128, 400)).astype(np.float32)
+    for got, ref in zip(run_split(hip, torch_gpu, qkv, [32, 32, 64], 2), O.split(qkv, [32, 32, 64], 2)):
+        np.testing.assert_array_equal(got, ref)
+    box = rng.uniform(-1, 1, (2, 144, 8400)).astype(np.float32)
+    for got, ref in zip(run_split(hip, torch_gpu, box, [64, 80], 1), O.split(box, [64, 80], 1)):
+        np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("shape,perm", [
+    ((32, 32, 400), (0, 2, 1)),        # q^T: tiled batched 2-D path, ragged 400
+    ((1, 2, 400, 400), (0, 1, 3, 2)),  # attention^T
+    ((16, 4, 16, 8400), (0, 2, 1, 3)),  # DFL: general path, contiguous inner
+    ((1, 84, 8400), (0, 2, 1)),        # head output -> [8400, 84]
+    ((3, 5, 7, 2), (3, 0, 2, 1)),      # general
+    ((33, 65), None),                  # reversed dims (no perm), 2-D tiled
+    ((4, 1, 6), (1, 0, 2)),            # only a size-1 dim moves: a copy
+    ((2, 3, 4), (0, 1, 2)),            # identity
+], ids=["qT", "attnT", "dfl", "head", "general", "rev", "unit", "identity"])
+def test_transpose(hip, torch_gpu, shape, perm):
+    print(f"[tensor-op] transpose {shape} {perm}", flush=True)
+    x = np.random.default_rng(int(np.prod(shape)) % 1000).uniform(-1, 1, shape).astype(np.float32)
+    p = perm if perm is not None else tuple(range(len(shape)))[::-1]
+    np.testing.assert_array_equal(run_transpose(hip, torch_gpu, x, perm), O.transpose(x, p))
+
+
+def test_resize_and_sppf_pool(hip, torch_gpu):
+    rng = np.random.default_rng(41)
+    for shape, oh, ow in (((1, 256, 20, 20), 40, 40), ((16, 128, 40, 40), 80, 80), ((2, 3, 5, 3), 7, 8),
+                          ((1, 2, 6, 6), 3, 4)):
+        print(f"[tensor-op] resize {shape} -> {oh}x{ow}", flush=True)
+        x = rng.uniform(-1, 1, shape).astype(np.float32)
+        np.testing.assert_array_equal(run_resize(hip, torch_gpu, x, oh, ow), O.resize_nearest(x, oh, ow))
+    x = rng.uniform(-1, 1, (16, 128, 20, 20)).astype(np.float32)
+    print("[tensor-op] maxpool 5x5 s1 p2", flush=True)
+    np.testing.assert_array_equal(run_maxpool(hip, torch_gpu, x, 20, 20, 5, 5, 1, 1, 2, 2),
+                                  O.maxpool(x, 20, 20, 5, 5, 1, 1, 2, 2))
+
+
+def test_bad_arguments(hip, torch_gpu):
+    L = hip.lib()
+    buf = torch_gpu.zeros(64, device="cuda")
+    p = C.c_void_p(buf.data_ptr())
+    assert L.spinn_hip_binary(7, p, 4, p, 4, p, 4, None) == hip.SPINN_HIP_EINVAL
+    assert L.spinn_hip_binary(0, p, 0, p, 4, p, 4, None) == hip.SPINN_HIP_EINVAL
+    assert L.spinn_hip_binary(0, p, 4, p, 4, p, 0, None) == 0
+    assert L.spinn_hip_binary(0, p, 4, p, 4, p, 1 << 33, None) == hip.SPINN_HIP_EINVAL
+    assert L.spinn_hip_unary(9, p, p, 4, None) == hip.SPINN_HIP_EINVAL
+    assert L.spinn_hip_softmax(2, 0, 3, p, p, None) == 0
+    dims = (C.c_int64 * 3)(2, 2, 2)
+    assert L.spinn_hip_transpose(3, dims, (C.c_int32 * 3)(0, 0, 1), p, p, None) == hip.SPINN_HIP_EINVAL
+    assert L.spinn_hip_transpose(3, dims, (C.c_int32 * 3)(0, 1, 3), p, p, None) == hip.SPINN_HIP_EINVAL
+    assert L.spinn_hip_transpose(9, dims, None, p, p, None) == hip.SPINN_HIP_EINVAL
+    blocks = (hip.BlockCopy * 17)()
+    assert L.spinn_hip_block_copy(blocks, 17, 1, None) == hip.SPINN_HIP_EINVAL
+    assert L.spinn_hip_resize_nearest(1, 0, 4, 4, 4, p, p, None) == hip.SPINN_HIP_EINVAL
+    torch_gpu.cuda.synchronize()

@@ -182,8 +182,15 @@ def test_dispatch_conventions(native):
     assert L.spinn_dispatch_op(E.OP_CONV, empty, 1, None, 0, empty, 1) == -1
     assert L.spinn_dispatch_op(E.OP_GEMM, empty, 1, None, 0, empty, 1) == -1
     for op in (E.OP_CONV, E.OP_GEMM, E.OP_MATMUL, E.OP_MAXPOOL, E.OP_REDUCEMEAN, E.OP_RESHAPE, E.OP_FLATTEN,
-               E.OP_GAP):
+               E.OP_GAP, E.OP_ADD, E.OP_SUB, E.OP_MUL, E.OP_DIV, E.OP_RELU, E.OP_SIGMOID, E.OP_BN, E.OP_SOFTMAX,
+               E.OP_CONCAT, E.OP_SPLIT, E.OP_TRANSPOSE, E.OP_RESIZE):
         assert L.spinn_op_registered(op) == 1
+    # unfused nodes keep the reference's arity checks
+    for op in (E.OP_ADD, E.OP_SUB, E.OP_MUL, E.OP_DIV):
+        assert L.spinn_dispatch_op(op, empty, 1, None, 0, empty, 1) == -1
+    assert L.spinn_dispatch_op(E.OP_BN, empty, 4, None, 0, empty, 1) == -1
+    for op in (E.OP_RELU, E.OP_SIGMOID, E.OP_SOFTMAX, E.OP_CONCAT, E.OP_SPLIT, E.OP_TRANSPOSE, E.OP_RESIZE):
+        assert L.spinn_dispatch_op(op, empty, 0, None, 0, empty, 1) == -1
 
 
 def test_conv_algo_selection(native):

@@ -194,6 +194,98 @@ def test_bn_fold_closed_form():
     assert_parity(O.conv2d_f64(d, x, w2, b2), bn, max_abs=1e-5, rel_l2=1e-6)
 
 
+# ---------------- unfused graph nodes ----------------
+
+def _params_axis(prm, default):
+    return int(np.frombuffer(prm[:4].tobytes(), np.int32)[0]) if prm.size >= 4 else default
+
+
+def _oracle_tensor_op(name, ins, prm, out_shapes):
+    """Run the oracle's restatement of the fixture's operator."""
+    op = name.split("_")[0]
+    if op in ("add", "sub", "mul", "div"):
+        return [O.binary(op, ins[0], ins[1], out_shapes[0])]
+    if op in ("relu", "sigmoid"):
+        return [O.unary(op, ins[0])]
+    if op == "batch":
+        eps = float(np.frombuffer(prm[:4].tobytes(), np.float32)[0])
+        return [O.batchnorm(*ins, eps=eps)]
+    if op == "softmax":
+        return [O.softmax(ins[0], _params_axis(prm, -1))]
+    if op == "concat":
+        return [O.concat(ins, _params_axis(prm, 0))]
+    if op == "split":
+        ax = _params_axis(prm, 0)
+        return O.split(ins[0], [sh[ax] for sh in out_shapes], ax)
+    if op == "transpose":
+        nd = ins[0].ndim
+        perm = list(prm[:nd]) if prm.size else list(range(nd))[::-1]
+        return [O.transpose(ins[0], perm)]
+    if op == "resize":
+        return [O.resize_nearest(ins[0], *out_shapes[0][2:])]
+    if op == "maxpool":
+        return [O.maxpool(ins[0], *out_shapes[0][2:], 5, 5, 1, 1, 2, 2)]
+    raise AssertionError(name)
+
+
+def _tensor_op_cases():
+    f = _load("tensor_ops.npz")
+    names = sorted({k.rsplit("_", 1)[0] for k in f.files})
+    for name in names:
+        ins = [f[f"{name}_in{i}"] for i in range(8) if f"{name}_in{i}" in f.files]
+        outs = [f[f"{name}_out{i}"] for i in range(8) if f"{name}_out{i}" in f.files]
+        yield name, ins, f[f"{name}_params"], outs
+
+
+# the reference vectorises exp (Cephes polynomial) and BatchNorm's FMA in blocks
+# of 8, so those outputs agree to rounding; every other operator moves or
+# combines values with one IEEE operation each and must agree bit for bit
+_ROUNDED = {"sigmoid", "softmax_last", "softmax_short", "softmax_mid", "batch_norm"}
+
+
+@pytest.mark.parametrize("case", list(_tensor_op_cases()), ids=lambda c: c[0])
+def test_tensor_ops_match_reference(case):
+    name, ins, prm, outs = case
+    got = _oracle_tensor_op(name, ins, prm, [o.shape for o in outs])
+    assert len(got) == len(outs)
+    for g, ref in zip(got, outs):
+        assert g.shape == ref.shape
+        if name in _ROUNDED:
+            np.testing.assert_allclose(g, ref, rtol=2e-6, atol=1e-7)
+        else:
+            np.testing.assert_array_equal(g, ref)
+
+
+def test_tensor_ops_closed_forms():
+    """The same operators against float64 numpy / torch definitions."""
+    import torch
+    import torch.nn.functional as F
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-3, 3, (2, 16, 4, 9)).astype(np.float32)
+    xd = x.astype(np.float64)
+    e = np.exp(xd - xd.max(1, keepdims=True))
+    np.testing.assert_allclose(O.softmax(x, 1), e / e.sum(1, keepdims=True), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(O.unary("sigmoid", x), 1 / (1 + np.exp(-xd)), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(O.unary("silu", x), xd / (1 + np.exp(-xd)), rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(O.unary("relu", x), np.maximum(x, 0))
+    sc, bi, mu, var = (rng.uniform(0.5, 1.5, 16).astype(np.float32) for _ in range(4))
+    bn = F.batch_norm(torch.from_numpy(xd), torch.from_numpy(mu.astype(np.float64)),
+                      torch.from_numpy(var.astype(np.float64)), torch.from_numpy(sc.astype(np.float64)),
+                      torch.from_numpy(bi.astype(np.float64)), False, 0.0, 1e-5).numpy()
+    np.testing.assert_allclose(O.batchnorm(x, sc, bi, mu, var, 1e-5), bn, rtol=1e-5, atol=1e-5)
+    np.testing.assert_array_equal(O.transpose(x, (0, 2, 1, 3)), x.transpose(0, 2, 1, 3))
+    np.testing.assert_array_equal(O.transpose(x, (3, 1, 0, 2)), x.transpose(3, 1, 0, 2))
+    parts = O.split(x, [3, 5, 8], 1)
+    np.testing.assert_array_equal(np.concatenate(parts, 1), x)
+    np.testing.assert_array_equal(O.concat(parts[::-1], 1), np.concatenate(parts[::-1], 1))
+    up = F.interpolate(torch.from_numpy(x), scale_factor=2, mode="nearest").numpy()
+    np.testing.assert_array_equal(O.resize_nearest(x, 8, 18), up)
+    b = rng.uniform(-1, 1, 9).astype(np.float32)
+    np.testing.assert_array_equal(O.binary("sub", x, b, x.shape), x - b)
+    np.testing.assert_array_equal(O.binary("mul", b, x, x.shape), b * x)
+    np.testing.assert_array_equal(O.binary("div", x, b, x.shape), x / np.where(np.abs(b) < 1e-6, 1e-6, b))
+
+
 # ---------------- whole model ----------------
 
 def _torch_graph(g_path, x):
