@@ -428,6 +428,7 @@ int op_div(SpinnTensor **in, int n_in, void *params, uint16_t params_size, Spinn
 
 static int unary_node(int op, SpinnTensor **in, int n_in, SpinnTensor **out, int n_out) {
     if (n_in < 1 || n_out < 1) return -1;
+    if (out[0]->elem_count < in[0]->elem_count) return -1;
     if (g_spinn_exec.preparing) return 0;
     return spinn_hip_unary(op, (const float *)in[0]->data, (float *)out[0]->data, in[0]->elem_count,
                            g_spinn_exec.stream);
@@ -452,7 +453,7 @@ int op_sigmoid(SpinnTensor **in, int n_in, void *params, uint16_t params_size, S
 int op_batch_norm(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
     if (n_in < 5 || n_out < 1) return -1;
     SpinnTensor *X = in[0];
-    if (X->ndim < 2) return -1;
+    if (X->ndim < 2 || out[0]->elem_count < X->elem_count) return -1;
     float eps = 1e-5f;
     if (params && params_size >= sizeof(ENNF_BatchNormParams)) eps = ((const ENNF_BatchNormParams *)params)->epsilon;
     int64_t spatial = 1;
@@ -479,7 +480,7 @@ int op_softmax(SpinnTensor **in, int n_in, void *params, uint16_t params_size, S
     if (params && params_size >= sizeof(ENNF_AxisParams)) axis = ((const ENNF_AxisParams *)params)->axis;
     const int ndim = in[0]->ndim;
     if (axis < 0) axis += ndim;
-    if (axis < 0 || axis >= ndim) return -1;
+    if (axis < 0 || axis >= ndim || out[0]->elem_count < in[0]->elem_count) return -1;
     int64_t outer, inner;
     axis_view(in[0], axis, &outer, &inner);
     if (g_spinn_exec.preparing) return 0;
@@ -558,7 +559,7 @@ int op_split(SpinnTensor **in, int n_in, void *params, uint16_t params_size, Spi
 int op_transpose(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
     if (n_in < 1 || n_out < 1) return -1;
     const int ndim = in[0]->ndim;
-    if (ndim < 1 || ndim > ENNF_MAX_DIMS) return -1;
+    if (ndim < 1 || ndim > ENNF_MAX_DIMS || out[0]->elem_count < in[0]->elem_count) return -1;
     int64_t dims[ENNF_MAX_DIMS];
     int32_t perm[ENNF_MAX_DIMS];
     for (int d = 0; d < ndim; d++) {

@@ -67,6 +67,27 @@ def gemm_params(alpha: float = 1.0, beta: float = 1.0, trans_a: int = 0, trans_b
     return struct.pack("<ffBB2x", alpha, beta, trans_a, trans_b)
 
 
+def axis_params(axis: int) -> bytes:
+    """ENNF_SoftmaxParams / ENNF_ConcatParams / ENNF_FlattenParams (4 B)."""
+    return struct.pack("<i", axis)
+
+
+def split_params(axis: int, num_outputs: int) -> bytes:
+    """ENNF_SplitParams (8 B); the piece sizes travel as the int64 second input."""
+    return struct.pack("<iI", axis, num_outputs)
+
+
+def transpose_params(perm) -> bytes:
+    """ENNF_TransposeParams (12 B): perm[8], num_dims, 3 reserved."""
+    p = list(perm) + [0] * (8 - len(perm))
+    return struct.pack("<8BB3x", *p, len(perm))
+
+
+def batchnorm_params(eps: float = 1e-5, momentum: float = 0.9) -> bytes:
+    """ENNF_BatchNormParams (12 B)."""
+    return struct.pack("<ffB3x", eps, momentum, 0)
+
+
 def reduce_params(axes, keepdims: int = 1) -> bytes:
     """ENNF_ReduceParams (36 B)."""
     a = list(axes) + [0] * (8 - len(axes))
@@ -113,6 +134,8 @@ class Graph:
     def tensor(self, name: str, dims, dtype: int = DT_FLOAT32, data: np.ndarray | None = None) -> int:
         if data is not None:
             data = np.ascontiguousarray(data, dtype=_NP_DTYPE[dtype])
+            if len(dims) == 0 and data.size == 1:
+                data = data.reshape(())  # ONNX scalar initializer: ndim 0, one element
             assert tuple(data.shape) == tuple(dims), (name, data.shape, dims)
         t = Tensor(len(self.tensors), name, tuple(int(d) for d in dims), dtype, data)
         self.tensors.append(t)

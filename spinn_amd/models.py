@@ -177,6 +177,218 @@ def vgg_stack(batch: int = 8, seed: int = 0, in_c: int = 64, schedule=VGG_SCHEDU
     return g, xin
 
 
+def _plain_conv(g: E.Graph, rng, name: str, x: int, oc: int, k: int = 1, bias: bool = True,
+                weight: np.ndarray | None = None) -> int:
+    """A bare nn.Conv2d (no BatchNorm, no activation) with PyTorch's default
+    init: weight and bias ~ U(-1/sqrt(fan_in), 1/sqrt(fan_in))."""
+    n, c, h, w = g.dims(x)
+    bound = 1.0 / np.sqrt(c * k * k)
+    if weight is None:
+        weight = rng.uniform(-bound, bound, (oc, c, k, k)).astype(np.float32)
+    ins = [x, g.weight(f"{name}.weight", weight)]
+    if bias:
+        ins.append(g.weight(f"{name}.bias", rng.uniform(-bound, bound, oc).astype(np.float32)))
+    oh, ow = _out_hw(h, w, k, k, 1, 1, k // 2, k // 2)
+    y = g.tensor(f"{name}.out", (n, oc, oh, ow))
+    g.node(E.OP_CONV, ins, [y], E.conv_params(k, k, 1, 1, (k // 2,) * 4, 1, E.ACT_NONE))
+    return y
+
+
+def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80):
+    """YOLOv10n (width 0.25, depth 0.33; ultralytics yolov10n.yaml) as the
+    converter + graph optimizer would emit the exported detector, up to the
+    one-to-one head's decoded output [B, 4 + nc, anchors] (boxes x1y1x2y2 in
+    pixels, class scores after Sigmoid), i.e. before the TopK post-processing.
+
+    Every Conv-BN-SiLU is one Conv node with act SILU (the export's
+    Conv -> Sigmoid -> Mul pattern, SPINN/graph_opt.c:395-481); convs built
+    with act=False carry no post-op, except where their single consumer is an
+    Add whose other operand already exists - the PSA block's pe, proj and
+    ffn.1 convs - which fuse it as act ADD (SPINN/graph_opt.c:301-374). The
+    Bottleneck / CIB shortcut Adds follow a SiLU conv and stay unfused Add
+    nodes. Node order is the export's execution order.
+    """
+    rng = np.random.default_rng(seed)
+    g = E.Graph()
+    x = g.input("images", (batch, 3, hw, hw))
+    uid = [0]
+
+    def nm(s):
+        uid[0] += 1
+        return f"{s}#{uid[0]}"
+
+    def conv(name, t, oc, k=1, s=1, group=1, act=E.ACT_SILU, residual=None):
+        return add_conv_bn(g, rng, name, t, oc, k, s, k // 2, group, act, residual)
+
+    def split(name, t, sizes, axis=1):
+        dims = g.dims(t)
+        outs = []
+        for i, sz in enumerate(sizes):
+            d = list(dims)
+            d[axis] = sz
+            outs.append(g.tensor(f"{name}.out{i}", tuple(d)))
+        sw = g.weight(nm(f"{name}.split"), np.array(sizes, np.int64), E.DT_INT64)
+        g.node(E.OP_SPLIT, [t, sw], outs, E.split_params(axis, len(sizes)))
+        return outs
+
+    def concat(name, ts, axis=1):
+        d = list(g.dims(ts[0]))
+        d[axis] = sum(g.dims(t)[axis] for t in ts)
+        y = g.tensor(f"{name}.out", tuple(d))
+        g.node(E.OP_CONCAT, ts, [y], E.axis_params(axis))
+        return y
+
+    def binary(op, name, a, b):
+        da, db = g.dims(a), g.dims(b)
+        y = g.tensor(f"{name}.out", da if int(np.prod(da)) >= int(np.prod(db)) else db)
+        g.node(op, [a, b], [y])
+        return y
+
+    def reshape(name, t, dims):
+        sw = g.weight(nm(f"{name}.shape"), np.array(dims, np.int64), E.DT_INT64)
+        y = g.tensor(f"{name}.out", tuple(dims))
+        g.node(E.OP_RESHAPE, [t, sw], [y])
+        return y
+
+    def transpose(name, t, perm):
+        d = g.dims(t)
+        y = g.tensor(f"{name}.out", tuple(d[p] for p in perm))
+        g.node(E.OP_TRANSPOSE, [t], [y], E.transpose_params(perm))
+        return y
+
+    def c2f(name, t, c2, n, shortcut):
+        c = c2 // 2
+        y = split(f"{name}.split", conv(f"{name}.cv1", t, 2 * c), [c, c])
+        for i in range(n):
+            a = conv(f"{name}.m.{i}.cv1", y[-1], c, 3)
+            b = conv(f"{name}.m.{i}.cv2", a, c, 3)
+            y.append(binary(E.OP_ADD, f"{name}.m.{i}.add", y[-1], b) if shortcut else b)
+        return conv(f"{name}.cv2", concat(f"{name}.cat", y), c2)
+
+    def scdown(name, t, c2):
+        return conv(f"{name}.cv2", conv(f"{name}.cv1", t, c2), c2, 3, 2, group=c2, act=E.ACT_NONE)
+
+    def sppf(name, t, c2):
+        n_, c1, h, w = g.dims(t)
+        y = [conv(f"{name}.cv1", t, c1 // 2)]
+        for i in range(3):
+            p = g.tensor(f"{name}.m{i}.out", g.dims(y[-1]))
+            g.node(E.OP_MAXPOOL, [y[-1]], [p], E.pool_params(5, 5, 1, 1, (2, 2, 2, 2)))
+            y.append(p)
+        return conv(f"{name}.cv2", concat(f"{name}.cat", y), c2)
+
+    def psa(name, t):
+        n_, c1, h, w = g.dims(t)
+        c = c1 // 2
+        heads, key_dim, head_dim = c // 64, 32, 64
+        a, b = split(f"{name}.split", conv(f"{name}.cv1", t, 2 * c), [c, c])
+        qkv = conv(f"{name}.attn.qkv", b, c + 2 * heads * key_dim, act=E.ACT_NONE)
+        qkv = reshape(f"{name}.attn.view", qkv, (n_, heads, 2 * key_dim + head_dim, h * w))
+        q, k, v = split(f"{name}.attn.split", qkv, [key_dim, key_dim, head_dim], axis=2)
+        qt = transpose(f"{name}.attn.qT", q, (0, 1, 3, 2))
+        s = g.tensor(f"{name}.attn.scores", (n_, heads, h * w, h * w))
+        g.node(E.OP_MATMUL, [qt, k], [s])
+        scale = g.weight(nm(f"{name}.attn.scale"), np.array(key_dim ** -0.5, np.float32))
+        s = binary(E.OP_MUL, f"{name}.attn.scaled", s, scale)
+        p = g.tensor(f"{name}.attn.softmax", g.dims(s))
+        g.node(E.OP_SOFTMAX, [s], [p], E.axis_params(-1))
+        pt = transpose(f"{name}.attn.pT", p, (0, 1, 3, 2))
+        o = g.tensor(f"{name}.attn.av", (n_, heads, head_dim, h * w))
+        g.node(E.OP_MATMUL, [v, pt], [o])
+        o = reshape(f"{name}.attn.view2", o, (n_, c, h, w))
+        vv = reshape(f"{name}.attn.v", v, (n_, c, h, w))
+        x2 = conv(f"{name}.attn.pe", vv, c, 3, group=c, act=E.ACT_ADD, residual=o)
+        b = conv(f"{name}.attn.proj", x2, c, act=E.ACT_ADD, residual=b)
+        f = conv(f"{name}.ffn.0", b, 2 * c)
+        b = conv(f"{name}.ffn.1", f, c, act=E.ACT_ADD, residual=b)
+        return conv(f"{name}.cv2", concat(f"{name}.cat", [a, b]), c1)
+
+    def c2fcib(name, t, c2):
+        c = c2 // 2
+        y = split(f"{name}.split", conv(f"{name}.cv1", t, 2 * c), [c, c])
+        m = conv(f"{name}.m.0.cv1.0", y[-1], c, 3, group=c)
+        m = conv(f"{name}.m.0.cv1.1", m, 2 * c)
+        m = conv(f"{name}.m.0.cv1.2", m, 2 * c, 7, group=2 * c)  # RepVGGDW, 3x3 branch merged at export
+        m = conv(f"{name}.m.0.cv1.3", m, c)
+        m = conv(f"{name}.m.0.cv1.4", m, c, 3, group=c)
+        y.append(binary(E.OP_ADD, f"{name}.m.0.add", y[-1], m))
+        return conv(f"{name}.cv2", concat(f"{name}.cat", y), c2)
+
+    def upsample(name, t):
+        n_, c, h, w = g.dims(t)
+        sc = g.weight(nm(f"{name}.scales"), np.array([1, 1, 2, 2], np.float32))
+        y = g.tensor(f"{name}.out", (n_, c, 2 * h, 2 * w))
+        g.node(E.OP_RESIZE, [t, sc], [y])
+        return y
+
+    # backbone
+    t = conv("model.0", x, 16, 3, 2)
+    t = conv("model.1", t, 32, 3, 2)
+    t = c2f("model.2", t, 32, 1, True)
+    t = conv("model.3", t, 64, 3, 2)
+    p3 = c2f("model.4", t, 64, 2, True)
+    t = scdown("model.5", p3, 128)
+    p4 = c2f("model.6", t, 128, 2, True)
+    t = scdown("model.7", p4, 256)
+    t = c2f("model.8", t, 256, 1, True)
+    t = sppf("model.9", t, 256)
+    p5 = psa("model.10", t)
+    # neck
+    t = concat("model.12", [upsample("model.11", p5), p4])
+    h13 = c2f("model.13", t, 128, 1, False)
+    t = concat("model.15", [upsample("model.14", h13), p3])
+    o3 = c2f("model.16", t, 64, 1, False)
+    t = concat("model.18", [conv("model.17", o3, 64, 3, 2), h13])
+    o4 = c2f("model.19", t, 128, 1, False)
+    t = concat("model.21", [scdown("model.20", o4, 128), p5])
+    o5 = c2fcib("model.22", t, 256)
+    # one-to-one v10Detect head
+    reg_max, c2h, c3h = 16, 64, max(64, min(nc, 100))
+    levels = []
+    for i, (f, stride) in enumerate(zip((o3, o4, o5), (8, 16, 32))):
+        pre = f"model.23.one2one_cv"
+        n_, ch, h, w = g.dims(f)
+        bx = conv(f"{pre}2.{i}.0", f, c2h, 3)
+        bx = conv(f"{pre}2.{i}.1", bx, c2h, 3)
+        bx = _plain_conv(g, rng, f"{pre}2.{i}.2", bx, 4 * reg_max)
+        cl = conv(f"{pre}3.{i}.0.0", f, ch, 3, group=ch)
+        cl = conv(f"{pre}3.{i}.0.1", cl, c3h)
+        cl = conv(f"{pre}3.{i}.1.0", cl, c3h, 3, group=c3h)
+        cl = conv(f"{pre}3.{i}.1.1", cl, c3h)
+        cl = _plain_conv(g, rng, f"{pre}3.{i}.2", cl, nc)
+        lv = concat(f"model.23.cat{i}", [bx, cl])
+        levels.append((reshape(f"model.23.view{i}", lv, (n_, 4 * reg_max + nc, h * w)), h, w, stride))
+    xcat = concat("model.23.cat", [lv for lv, _, _, _ in levels], axis=2)
+    na = g.dims(xcat)[2]
+    box, cls = split("model.23.split", xcat, [4 * reg_max, nc])
+    sig = g.tensor("model.23.sigmoid.out", g.dims(cls))
+    g.node(E.OP_SIGMOID, [cls], [sig])
+    d = reshape("model.23.dfl.view", box, (batch, 4, reg_max, na))
+    d = transpose("model.23.dfl.t", d, (0, 2, 1, 3))
+    sm = g.tensor("model.23.dfl.softmax", g.dims(d))
+    g.node(E.OP_SOFTMAX, [d], [sm], E.axis_params(1))
+    dist = _plain_conv(g, rng, "model.23.dfl.conv", sm, 1, bias=False,
+                       weight=np.arange(reg_max, dtype=np.float32).reshape(1, reg_max, 1, 1))
+    dist = reshape("model.23.dfl.view2", dist, (batch, 4, na))
+    lt, rb = split("model.23.chunk", dist, [2, 2])
+    ax, ay, st = [], [], []
+    for _, h, w, stride in levels:
+        gy, gx = np.meshgrid(np.arange(h, dtype=np.float32) + 0.5, np.arange(w, dtype=np.float32) + 0.5,
+                             indexing="ij")
+        ax.append(gx.ravel())
+        ay.append(gy.ravel())
+        st.append(np.full(h * w, stride, np.float32))
+    anchors = g.weight("model.23.anchors", np.stack([np.concatenate(ax), np.concatenate(ay)])[None].astype(np.float32))
+    strides = g.weight("model.23.strides", np.concatenate(st)[None].astype(np.float32))
+    x1y1 = binary(E.OP_SUB, "model.23.x1y1", anchors, lt)
+    x2y2 = binary(E.OP_ADD, "model.23.x2y2", anchors, rb)
+    dbox = binary(E.OP_MUL, "model.23.dbox", concat("model.23.xyxy", [x1y1, x2y2]), strides)
+    y = concat("model.23.out", [dbox, sig])
+    g.output(y)
+    xin = np.random.default_rng(seed + 1).uniform(0.0, 1.0, (batch, 3, hw, hw)).astype(np.float32)
+    return g, xin
+
+
 def conv_flops(g: E.Graph) -> list:
     """Per-Conv-node direct-convolution FLOPs 2*N*OC*OH*OW*(C/g)*KH*KW (node index, flops)."""
     out = []

@@ -5,7 +5,7 @@ with oracle/Makefile (the reference's run_time C sources compiled in place) and
 calls the reference functions on small seeded inputs. Each fixture is an .npz
 of inputs and the reference's outputs (no code), loaded with allow_pickle=False.
 
-    python tests/golden/make_golden.py [planner conv epilogue gemm winograd tensor_ops]
+    python tests/golden/make_golden.py [planner conv epilogue gemm winograd tensor_ops models]
 
 Fixtures:
   planner_offsets.npz   spinn_load + spinn_plan_memory offsets and peak for
@@ -21,6 +21,8 @@ Fixtures:
   tensor_ops.npz        op_add / op_sub / op_mul / op_div (modulo broadcast), op_relu, op_sigmoid,
                         op_batch_norm, op_softmax, op_concat, op_split, op_transpose, op_resize and
                         op_maxpool 5x5 s1 p2 on small seeded inputs (the unfused nodes of a detector)
+  models_as_shipped.npz spinn_load + spinn_plan + spinn_run of generated models (YOLOv10n at
+                        64x64, a 4-block ResNet at 64x64, batch 2): the reference's output and an input fingerprint
 """
 from __future__ import annotations
 
@@ -101,6 +103,8 @@ def planner(L):
         "resnet101_b4": models.resnet101(batch=4, seed=0)[0],
         "vgg_b2": models.vgg_stack(batch=2, seed=3, in_c=16, schedule=[(16, 32), (16, 32), (32, 16), (32, 16)])[0],
         "gemm_32": models.gemm_model(32, 1000, 2048, seed=1)[0],
+        "yolov10n_b1": models.yolov10n(batch=1, seed=0)[0],
+        "yolov10n_b2_320": models.yolov10n(batch=2, seed=0, hw=320)[0],
     }
     out = {}
     tmp = HERE / "_tmp_planner.ennf"
@@ -237,6 +241,36 @@ def tensor_ops(L):
     np.savez_compressed(HERE / "tensor_ops.npz", **out)
 
 
+MODEL_CASES = {
+    # name: (generator, kwargs) - small enough that input and output stay a few KB
+    "yolov10n_64": ("yolov10n", dict(batch=1, seed=5, hw=64)),
+    "resnet_64": ("resnet", dict(batch=2, seed=6, blocks=(1, 1, 1, 1), hw=64, num_classes=10)),
+}
+
+
+def models_as_shipped(L):
+    """Whole ENNF models through the reference's spinn_load / spinn_plan /
+    spinn_run: its output is the as-shipped one (group==1 convs drop the
+    epilogue), which the oracle reproduces with oracle_set_as_shipped(1)."""
+    L.spinn_plan.argtypes = [C.c_void_p, C.c_uint32]
+    L.spinn_run.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p]
+    out = {}
+    tmp = HERE / "_tmp_model.ennf"
+    for name, (gen, kw) in MODEL_CASES.items():
+        g, x = getattr(models, gen)(**kw)
+        g.write(tmp)
+        ctx = L.spinn_load(str(tmp).encode())
+        assert ctx and L.spinn_plan(ctx, 0) == 0
+        y = np.zeros(g.dims(g.outputs[0]), np.float32)
+        assert L.spinn_run(ctx, x.ctypes.data, y.ctypes.data) == 0
+        L.spinn_free(ctx)
+        # the generator recreates the input from the seed; keep a fingerprint to catch drift
+        out[f"{name}_x_sum"] = np.array([x.astype(np.float64).sum(), x.ravel()[0], x.ravel()[-1]])
+        out[f"{name}_y"] = y
+    tmp.unlink()
+    np.savez_compressed(HERE / "models_as_shipped.npz", **out)
+
+
 def gemm(L):
     from spinn_amd.ennf import gemm_params
     rng = np.random.default_rng(7)
@@ -288,7 +322,7 @@ def winograd(L):
 def main():
     L = ref_lib()
     steps = {"planner": planner, "conv": conv_cases, "epilogue": epilogue, "gemm": gemm, "winograd": winograd,
-             "tensor_ops": tensor_ops}
+             "tensor_ops": tensor_ops, "models": models_as_shipped}
     for name in sys.argv[1:] or list(steps):
         steps[name](L)
     for f in sorted(HERE.glob("*.npz")):

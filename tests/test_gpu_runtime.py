@@ -74,3 +74,31 @@ def test_resnet101_b1_graph_replay(hip, tmp_path):
         outs = [s.run(x) for _ in range(3)]
     for o in outs:
         assert np.array_equal(o, y_eager)
+
+
+@pytest.mark.parametrize("batch,hw", [(1, 640), (2, 320)], ids=["b1_640", "b2_320"])
+def test_yolov10n(hip, tmp_path, batch, hw):
+    """The detector: fused Conv+SiLU / Conv+Add, depthwise, unfused Add / Split /
+    Concat / MaxPool 5x5 / Resize / attention (Reshape, Transpose, MatMul,
+    Softmax) and the decoded head (DFL Softmax + conv, Sub / Add / Mul with
+    broadcast anchors and strides, Sigmoid), output [B, 84, anchors]."""
+    g, x = models.yolov10n(batch=batch, seed=7, hw=hw)
+    print(f"[yolov10n] b{batch} {hw}x{hw}", flush=True)
+    y, y2, ref = _run_both(tmp_path, g, x, f"y10_b{batch}")
+    assert_parity(y, ref, what=f"yolov10n b{batch}@{hw}")
+    assert np.array_equal(y, y2)
+    assert_parity(y[:, 4:], ref[:, 4:], what="class scores")
+
+
+def test_yolov10n_b16_graph_replay(hip, tmp_path):
+    g, x = models.yolov10n(batch=16, seed=8)
+    path = g.write(tmp_path / "y10_b16.ennf")
+    print("[yolov10n] b16 640 eager + graph", flush=True)
+    with Session(path) as s:
+        y_eager = s.run(x)
+    with Session(path, graph=True) as s:
+        outs = [s.run(x) for _ in range(3)]
+    for o in outs:
+        assert np.array_equal(o, y_eager)
+    ref = O.Model(path).run(x, g.dims(g.outputs[0]))
+    assert_parity(y_eager, ref, what="yolov10n b16")

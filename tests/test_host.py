@@ -99,6 +99,8 @@ def test_native_loader_parses_model(native, tmp_path):
     ("resnet101_b4", lambda: models.resnet101(batch=4, seed=0)[0]),
     ("vgg_b2", lambda: models.vgg_stack(batch=2, seed=3, in_c=16, schedule=[(16, 32), (16, 32), (32, 16), (32, 16)])[0]),
     ("gemm_32", lambda: models.gemm_model(32, 1000, 2048, seed=1)[0]),
+    ("yolov10n_b1", lambda: models.yolov10n(batch=1, seed=0)[0]),
+    ("yolov10n_b2_320", lambda: models.yolov10n(batch=2, seed=0, hw=320)[0]),
 ])
 def test_planner_matches_reference(native, tmp_path, name, maker):
     """Offsets and peak equal the reference planner's (golden, from its compiled code)."""

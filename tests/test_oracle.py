@@ -295,8 +295,14 @@ def _torch_graph(g_path, x):
     m = E.read(g_path)
     vals = {m["inputs"][0]: torch.from_numpy(x).double()}
     W = {k: torch.from_numpy(np.array(v)).double() for k, v in m["weights"].items()}
+
+    def v(t):
+        return vals[t] if t in vals else W[t]
+
     for nd in m["nodes"]:
         ins = nd["inputs"]
+        out_dims = m["tensors"][nd["outputs"][0]]["dims"]
+        axis = int(np.frombuffer(nd["params"][:4], np.int32)[0]) if len(nd["params"]) >= 4 else None
         if nd["op"] == E.OP_CONV:
             p = E.unpack_conv_params(nd["params"])
             act = p["act"]
@@ -318,13 +324,49 @@ def _torch_graph(g_path, x):
         elif nd["op"] == E.OP_REDUCEMEAN:
             y = vals[ins[0]].mean(dim=(2, 3), keepdim=True)
         elif nd["op"] == E.OP_RESHAPE:
-            y = vals[ins[0]].reshape(vals[ins[0]].shape[0], -1)
+            y = vals[ins[0]].reshape(out_dims)
         elif nd["op"] == E.OP_GEMM:
             y = vals[ins[0]] @ W[ins[1]].T + W[ins[2]]
+        elif nd["op"] in (E.OP_ADD, E.OP_SUB, E.OP_MUL):
+            a, b = v(ins[0]), v(ins[1])
+            y = a + b if nd["op"] == E.OP_ADD else a - b if nd["op"] == E.OP_SUB else a * b
+        elif nd["op"] == E.OP_SIGMOID:
+            y = torch.sigmoid(vals[ins[0]])
+        elif nd["op"] == E.OP_SOFTMAX:
+            y = torch.softmax(vals[ins[0]], dim=axis)
+        elif nd["op"] == E.OP_CONCAT:
+            y = torch.cat([v(t) for t in ins], dim=axis)
+        elif nd["op"] == E.OP_SPLIT:
+            sizes = [m["tensors"][o]["dims"][axis] for o in nd["outputs"]]
+            for o, part in zip(nd["outputs"], torch.split(vals[ins[0]], sizes, dim=axis)):
+                vals[o] = part
+            continue
+        elif nd["op"] == E.OP_TRANSPOSE:
+            nd_ = vals[ins[0]].dim()
+            y = vals[ins[0]].permute(*list(nd["params"][:nd_]))
+        elif nd["op"] == E.OP_MATMUL:
+            y = vals[ins[0]] @ vals[ins[1]]
+        elif nd["op"] == E.OP_RESIZE:
+            y = F.interpolate(vals[ins[0]], size=out_dims[2:], mode="nearest")
         else:
             raise AssertionError(nd["op"])
+        assert tuple(y.shape) == tuple(out_dims), (nd["op"], y.shape, out_dims)
         vals[nd["outputs"][0]] = y
     return vals[m["outputs"][0]].numpy()
+
+
+def test_oracle_yolov10n_matches_torch_float64(tmp_path):
+    """The detector graph (unfused Add / Split / Concat / Transpose / MatMul /
+    Softmax / Resize / Sigmoid / Sub / Mul nodes around the fused convs) at
+    256x256, batch 2: every node's output against float64 torch."""
+    g, x = models.yolov10n(batch=2, seed=3, hw=256)
+    path = g.write(tmp_path / "y10_256.ennf")
+    y = O.Model(path).run(x, g.dims(g.outputs[0]))
+    ref = _torch_graph(path, x)
+    assert_parity(y, ref, what="oracle yolov10n vs torch float64")
+    # boxes are pixel coordinates on the 8/16/32 strides grid, scores in (0, 1)
+    assert y.shape == (2, 84, 32 * 32 + 16 * 16 + 8 * 8)
+    assert np.all((y[:, 4:] > 0) & (y[:, 4:] < 1))
 
 
 def test_oracle_model_matches_torch_float64(tmp_path):
@@ -332,3 +374,30 @@ def test_oracle_model_matches_torch_float64(tmp_path):
     path = g.write(tmp_path / "tiny_resnet.ennf")
     y = O.Model(path).run(x, g.dims(g.outputs[0]))
     assert_parity(y, _torch_graph(path, x), what="oracle model vs torch float64")
+
+
+@pytest.mark.parametrize("name", ["yolov10n_64", "resnet_64"])
+def test_oracle_model_as_shipped_matches_reference_runtime(name):
+    """Whole models through the reference's own spinn_load / spinn_plan /
+    spinn_run (tests/golden/models_as_shipped.npz): the oracle's model runner
+    with the as-shipped switch (group==1 convs drop bias/act/residual, as
+    SPINN/run_time/ops/mm/gemm_kernel.c:497-590 does) reproduces the
+    reference's output, so node order, operand wiring and every unfused
+    operator of the runner are pinned end to end."""
+    import tempfile
+    gen, kw = {"yolov10n_64": ("yolov10n", dict(batch=1, seed=5, hw=64)),
+               "resnet_64": ("resnet", dict(batch=2, seed=6, blocks=(1, 1, 1, 1), hw=64, num_classes=10))}[name]
+    f = _load("models_as_shipped.npz")
+    g, x = getattr(models, gen)(**kw)
+    fp = f[f"{name}_x_sum"]
+    assert np.isclose(x.astype(np.float64).sum(), fp[0]) and x.ravel()[0] == fp[1] and x.ravel()[-1] == fp[2]
+    with tempfile.TemporaryDirectory() as td:
+        m = O.Model(g.write(Path(td) / "m.ennf"))
+        O.lib().oracle_set_as_shipped(1)
+        try:
+            y = m.run(x, g.dims(g.outputs[0]))
+        finally:
+            O.lib().oracle_set_as_shipped(0)
+        m.close()
+    ref = f[f"{name}_y"]
+    assert_parity(y, ref, max_abs=1e-5, rel_l2=1e-6, what=f"{name} as-shipped vs reference spinn_run")
