@@ -51,7 +51,7 @@ def host_threads() -> int:
     return n
 
 
-def cpu_baseline(model_b1: Path, in_shape, out_shape, seconds: float) -> dict | None:
+def cpu_baseline(model_b1: Path, in_shape, out_shape, seconds: float, label: str = "ResNet-101") -> dict | None:
     kind = "reference" if (ROOT / "oracle" / "_ref" / "libspinn_ref.so").exists() else "port"
     threads = host_threads()
     env = dict(os.environ, OMP_NUM_THREADS=str(threads))
@@ -68,7 +68,7 @@ def cpu_baseline(model_b1: Path, in_shape, out_shape, seconds: float) -> dict | 
     res = json.loads(r.stdout.strip().splitlines()[-1])
     ips = res["batch"] / (res["avg_ms"] / 1e3)
     return {"value": round(ips, 3), "unit": "images/s", "cores": threads, "kind": kind,
-            "sample": (f"ResNet-101 batch {res['batch']} forward, {res['runs']} runs after 3 warm-up "
+            "sample": (f"{label} batch {res['batch']} forward, {res['runs']} runs after 3 warm-up "
                        f"(reference CLI protocol), ~{seconds:.0f} s budget, OpenMP {threads} threads; "
                        f"best {res['best_ms']:.1f} ms, mean {res['avg_ms']:.1f} ms per image")}
 
@@ -122,7 +122,7 @@ def profiled_node_ms(N, Session, path, x, policy, steps: int, warmup: int):
     return acc / steps
 
 
-def suite(N, Session, models, reps: int = 100) -> dict:
+def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> dict:
     """The other benchmark configurations, each on its own:
     cfg0   single fused Conv3x3+BN+ReLU 1x64x56x56 through spinn_hip_conv
            (launch-bound: 2*reps back-to-back launches timed with events) and
@@ -132,7 +132,8 @@ def suite(N, Session, models, reps: int = 100) -> dict:
            19.7 flop/B ridge, the HBM roofline;
     vgg    the 8-layer 3x3 stack at batch 8 under the implicit-GEMM and the
            Winograd policy: images/s, direct-conv-equivalent TFLOP/s and how far
-           the two outputs are apart (relative L2)."""
+           the two outputs are apart (relative L2);
+    yolo   YOLOv10n 640x640 at batch 1 and 16 (see yolo_bench)."""
     import ctypes as C
     from spinn_amd.devbuf import DeviceBuffer, time_launches
     L = N.lib()
@@ -204,7 +205,54 @@ def suite(N, Session, models, reps: int = 100) -> dict:
     res["winograd_vs_igemm_max_abs"] = float(np.abs(dv).max())
     res["gflop_direct_equiv"] = round(vgg_flops / 1e9, 2)
     out["vgg3x3_stack_b8"] = res
+    out["yolov10n"] = yolo_bench(N, Session, models, tmp, reps)
+    out["yolov10n"]["cpu_baseline_b1"] = yolo_cpu
     return out
+
+
+def _op_family(N, nd, g, policy) -> str:
+    from spinn_amd import ennf as E
+    if nd.op == E.OP_CONV:
+        p = E.unpack_conv_params(nd.params)
+        n, c, h, w = g.dims(nd.inputs[0])
+        oc, cg, kh, kw = g.dims(nd.inputs[1])
+        _, _, oh, ow = g.dims(nd.outputs[0])
+        r = dict(n=n, c=c, h=h, w=w, oc=oc, oh=oh, ow=ow, kh=kh, kw=kw, sh=p["strides"][0], sw=p["strides"][1],
+                 ph=p["pads"][0], pw=p["pads"][1], group=p["group"] or 1, act=p["act"])
+        return "conv_" + ALGO_NAMES.get(algo_of(N, r, policy), "?")
+    return {E.OP_ADD: "add", E.OP_SUB: "sub", E.OP_MUL: "mul", E.OP_CONCAT: "concat", E.OP_SPLIT: "split",
+            E.OP_MAXPOOL: "maxpool", E.OP_RESIZE: "resize", E.OP_RESHAPE: "reshape", E.OP_TRANSPOSE: "transpose",
+            E.OP_MATMUL: "matmul", E.OP_SOFTMAX: "softmax", E.OP_SIGMOID: "sigmoid"}.get(nd.op, f"op{nd.op}")
+
+
+def yolo_bench(N, Session, models, tmp: Path, reps: int) -> dict:
+    """YOLOv10n 640x640 at batch 1 and 16: images/s (graph replay, input
+    resident), direct-conv-equivalent conv TFLOP/s, and at batch 16 the device
+    time per operator family from HIP events around every node."""
+    res = {}
+    for b in (1, 16):
+        g, x = models.yolov10n(batch=b, seed=0)
+        path = g.write(tmp / f"y10_b{b}.ennf")
+        with Session(path, graph=True) as s:
+            s.upload_input(x)
+            ms = time_steps(s, max(20, reps // 2) if b == 1 else max(10, reps // 10), 3)
+        gf = sum(f for _, f in models.conv_flops(g))
+        ent = {"ms": round(ms, 4), "images_per_s": round(b / (ms * 1e-3), 1),
+               "conv_tflops_direct_equiv": round(gf / (ms * 1e-3) / 1e12, 2), "conv_gflop": round(gf / 1e9, 3)}
+        if b == 16:
+            node_ms = profiled_node_ms(N, Session, path, x, N.POLICY_AUTO, 5, 2)
+            fam = {}
+            for i, nd in enumerate(g.nodes):
+                k = _op_family(N, nd, g, N.POLICY_AUTO)
+                f = fam.setdefault(k, [0, 0.0])
+                f[0] += 1
+                f[1] += float(node_ms[i])
+            ent["node_ms_total"] = round(float(node_ms.sum()), 4)
+            ent["families_ms"] = {k: {"nodes": v[0], "ms": round(v[1], 4)}
+                                  for k, v in sorted(fam.items(), key=lambda kv: -kv[1][1])}
+        res[f"b{b}"] = ent
+        print(f"[bench] yolov10n b{b}: {ms:.3f} ms", file=sys.stderr, flush=True)
+    return res
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "conv_igemm_traffic_resnet101_b32.json"
@@ -364,11 +412,17 @@ def main() -> int:
     pB = gB.write(tmp / f"r101_b{a.batch}.ennf")
     print(f"[bench] models written in {time.perf_counter() - t_gen:.1f}s", file=sys.stderr, flush=True)
 
-    # CPU baseline first, before this process touches the GPU.
-    cpu = None
+    # CPU baselines first, before this process touches the GPU.
+    cpu = cpu_y10 = None
     if not a.no_cpu:
         cpu = cpu_baseline(p1, g1.dims(g1.inputs[0]), g1.dims(g1.outputs[0]), a.cpu_seconds)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+        if not a.no_suite:
+            gy, _ = models.yolov10n(batch=1, seed=0)
+            py = gy.write(tmp / "y10_cpu_b1.ennf")
+            cpu_y10 = cpu_baseline(py, gy.dims(gy.inputs[0]), gy.dims(gy.outputs[0]), a.cpu_seconds / 2,
+                                   label="YOLOv10n 640x640")
+            print(f"[bench] yolov10n cpu baseline: {cpu_y10}", file=sys.stderr, flush=True)
 
     L = N.lib()
     N.check(L.spinn_hip_init(0), "spinn_hip_init")
@@ -411,7 +465,7 @@ def main() -> int:
     s1.close()
     print(f"[bench] b1: {ms_1:.3f} ms/step", file=sys.stderr, flush=True)
 
-    other = None if a.no_suite else suite(N, Session, models)
+    other = None if a.no_suite else suite(N, Session, models, yolo_cpu=cpu_y10)
     if other is not None:
         print(f"[bench] suite: {json.dumps(other)}", file=sys.stderr, flush=True)
 

@@ -205,7 +205,16 @@ template <int BN> using Gen77BL = Im2colLoader<BN, kBK, 7, 7>;
 template <int BN> using Gen11BL = Im2colLoader<BN, kBK, 1, 1>;
 template <int BN> using GenBL = Im2colLoader<BN, kBK, 0, 0>;
 
+template <int BN> using PwBL = Pointwise1x1Loader<BN, kBK>;
+
 bool conv_tap_order(const SpinnHipConvDesc *d) { return ((d->c / d->group) % kBK) == 0; }
+
+// 1x1 / stride 1 / no padding over planes of a multiple of 4 pixels, 16-byte
+// aligned input: the B operand is read as float4 runs of the input itself.
+bool conv_pointwise_vec(const SpinnHipConvDesc *d, const float *x) {
+    return d->kh == 1 && d->kw == 1 && d->sh == 1 && d->sw == 1 && d->ph == 0 && d->pw == 0 && d->oh == d->h &&
+           d->ow == d->w && (d->oh * d->ow) % 4 == 0 && ((uintptr_t)x & 15u) == 0;
+}
 
 } // namespace
 
@@ -267,7 +276,8 @@ int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, c
         a.k_chunk = tc.k_chunk;
     }
     int rc;
-    if (conv_tap_order(d)) rc = launch_conv_bl<TapBL>(a, tc, d->group, st);
+    if (conv_pointwise_vec(d, x)) rc = launch_conv_bl<PwBL>(a, tc, d->group, st);
+    else if (conv_tap_order(d)) rc = launch_conv_bl<TapBL>(a, tc, d->group, st);
     else if (d->kh == 3 && d->kw == 3) rc = launch_conv_bl<Gen33BL>(a, tc, d->group, st);
     else if (d->kh == 7 && d->kw == 7) rc = launch_conv_bl<Gen77BL>(a, tc, d->group, st);
     else if (d->kh == 1 && d->kw == 1) rc = launch_conv_bl<Gen11BL>(a, tc, d->group, st);

@@ -310,6 +310,53 @@ struct Im2colTapLoader {
     }
 };
 
+// 1x1 stride-1 unpadded convolution: im2col is the input itself, column j =
+// (img, p) reads x[img][group*Cg + k][p]. With OH*OW a multiple of 4, four
+// consecutive columns starting at a multiple of 4 lie in one image and one
+// 16-byte aligned run, so each thread moves float4s exactly like KMajorLoader,
+// with the image stride folded into a per-thread base computed once.
+template <int BN, int BK>
+struct Pointwise1x1Loader {
+    static constexpr int S = LdsPad<BN>::stride;
+    static constexpr int NV = (BK * BN / 4) / kThreads;
+    static_assert(NV >= 1, "tile too small for 256 threads");
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t hw;
+    uint32_t base[NV]; // element offset of (img, group*Cg, p) of this thread's columns; kOOB past ntot
+    int k_end;
+    f32x4 rv[NV];
+
+    __device__ __forceinline__ void init(const ConvGeom &g, int n0, int group, int tid, int kend) {
+        rsrc = make_rsrc(g.x, g.x_bytes);
+        hw = (uint32_t)(g.OH * g.OW);
+        k_end = kend;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = tid + i * kThreads;
+            const int j = n0 + (c % (BN / 4)) * 4;
+            const int img = j / (int)hw;
+            const uint32_t p = (uint32_t)(j - img * (int)hw);
+            base[i] = j < g.ntot ? ((uint32_t)img * g.C + (uint32_t)group * g.Cg) * hw + p : kOOB;
+        }
+    }
+    __device__ __forceinline__ void fetch(int k0, int tid) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = tid + i * kThreads;
+            const int k = k0 + c / (BN / 4);
+            const bool ok = base[i] != kOOB && k < k_end;
+            rv[i] = buf_f32x4(rsrc, ok ? (base[i] + (uint32_t)k * hw) * 4u : kOOB);
+        }
+    }
+    __device__ __forceinline__ void commit(float *lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = tid + i * kThreads;
+            *reinterpret_cast<f32x4 *>(lds + (c / (BN / 4)) * S + (c % (BN / 4)) * 4) = rv[i];
+        }
+    }
+};
+
 // Output tile of this workgroup. Workgroups are dispatched round-robin over
 // the 8 XCDs (each with its own L2), so consecutive block ids land on
 // different XCDs. Remap so that each XCD walks a contiguous run of the tile

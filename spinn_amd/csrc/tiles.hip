@@ -41,9 +41,11 @@ TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
     // what hides the load latency of a short K loop (measured faster than
     // 128-wide tiles on every ResNet-101 layer shape at batch 32).
     const int64_t tiles = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * reps;
-    if (allow_split && K >= 512 && tiles < 2 * cus) {
+    if (allow_split && ((K >= 512 && tiles < 2 * cus) || (K >= 256 && 2 * tiles < cus))) {
         // Split K only when each split still runs >= 128 deep: the partial
-        // sums cost a write and a read of the output per split.
+        // sums cost a write and a read of the output per split. A 256-deep
+        // K splits only when the grid covers less than half the CUs
+        // (batch-1 1x1 convs).
         int split = (int)std::min<int64_t>((4 * cus + tiles - 1) / tiles, K / 128);
         split = std::max(1, std::min(split, 8));
         if (split > 1) {

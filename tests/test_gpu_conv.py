@@ -23,6 +23,10 @@ CASES = [
     ("stem7x7_s2", 2, 3, 64, 64, 64, 7, 2, 3, 1, 1, 0),
     ("pw1x1_add_relu", 2, 256, 14, 14, 1024, 1, 1, 0, 1, 5, 0),
     ("pw1x1_s2_none", 2, 256, 28, 28, 512, 1, 2, 0, 1, 0, 0),
+    ("pw1x1_ragged_k", 3, 20, 6, 10, 37, 1, 1, 0, 1, 3, 0),     # float4 pixel runs, K tail, images inside a tile
+    ("pw1x1_grouped", 2, 64, 8, 8, 64, 1, 1, 0, 2, 1, 0),
+    ("pw1x1_splitk", 1, 1024, 7, 8, 256, 1, 1, 0, 1, 5, 0),
+    ("pw1x1_odd_plane", 2, 64, 7, 7, 96, 1, 1, 0, 1, 1, 0),     # 49-pixel planes: gather loader
     ("conv3x3_s2", 2, 128, 28, 28, 128, 3, 2, 1, 1, 1, 0),
     ("ragged_silu_c3", 1, 3, 17, 19, 83, 3, 1, 1, 1, 3, 0),
     ("add_only", 1, 32, 9, 11, 48, 3, 1, 1, 1, 4, 0),
