@@ -34,8 +34,11 @@ static int env_winograd() {
 
 static bool winograd_pays(const SpinnHipConvDesc *d) {
     // Winograd cuts GEMM flops 2.25x but moves V (4x the input) and M (4x the
-    // output) through memory; it wins once the GEMM is deep enough.
-    return d->c >= 256 && d->oc >= 256;
+    // output) through memory in three launches; measured on MI355X it wins
+    // from 128 channels in and out once there are >= 256 2x2 output tiles
+    // (1.6x at 128@28x28 batch 32), and loses at 64 channels or at batch 1.
+    const int64_t tiles = (int64_t)d->n * ((d->oh + 1) / 2) * ((d->ow + 1) / 2);
+    return d->c >= 128 && d->oc >= 128 && tiles >= 256;
 }
 
 static int select_algo(const SpinnHipConvDesc *d) {

@@ -205,7 +205,10 @@ def test_conv_algo_selection(native):
         return L.spinn_hip_conv_select_algo(C.byref(d))
 
     assert algo(1, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM
-    assert algo(1, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_WINOGRAD
+    assert algo(32, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_WINOGRAD
+    assert algo(32, 128, 28, 28, 128, 3, 1, 1, 1) == native.ALGO_WINOGRAD
+    assert algo(1, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM  # 49 output tiles: too few
+    assert algo(32, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM   # 64 channels
     assert algo(1, 256, 14, 14, 256, 3, 2, 1, 1) == native.ALGO_IMPLICIT_GEMM
     assert algo(1, 128, 20, 20, 128, 3, 2, 1, 128) == native.ALGO_DIRECT
     assert algo(1, 6, 8, 8, 4, 3, 1, 1, 4) == native.SPINN_HIP_EINVAL  # C % group != 0
