@@ -46,6 +46,7 @@ static int select_algo(const SpinnHipConvDesc *d) {
     const int Cg = d->c / d->group;
     const int OCg = d->oc / d->group;
     if (d->group > 1 && (Cg < 8 || OCg < 8)) return SPINN_CONV_ALGO_DIRECT;
+    if (stem_conv_pays(d)) return SPINN_CONV_ALGO_DIRECT;
     if (winograd_eligible(d)) {
         const int w = env_winograd();
         if (w == 1 || (w < 0 && winograd_pays(d))) return SPINN_CONV_ALGO_WINOGRAD;

@@ -45,8 +45,8 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm0 = (wave >> 1) * WT::WM;
-    const int wn0 = (wave & 1) * WT::WN;
+    const int wm0 = WT::origin_m(wave);
+    const int wn0 = WT::origin_n(wave);
     int tile_m, tile_n;
     xcd_tile(gridDim.y, gridDim.x, tile_m, tile_n);
     const int n0 = tile_n * BN;
@@ -196,6 +196,7 @@ int launch_conv_bl(const ConvKArgs &a, const TileChoice &tc, int groups, hipStre
     if (tc.bm == 128 && tc.bn == 128) return launch_conv_tile<128, 128, BLT<128>>(a, groups, tc.split, st);
     if (tc.bm == 128 && tc.bn == 64) return launch_conv_tile<128, 64, BLT<64>>(a, groups, tc.split, st);
     if (tc.bm == 64 && tc.bn == 128) return launch_conv_tile<64, 128, BLT<128>>(a, groups, tc.split, st);
+    if (tc.bm == 32 && tc.bn == 128) return launch_conv_tile<32, 128, BLT<128>>(a, groups, tc.split, st);
     return launch_conv_tile<64, 64, BLT<64>>(a, groups, tc.split, st);
 }
 

@@ -53,9 +53,180 @@ __global__ __launch_bounds__(256) void direct_conv_kernel(const float *__restric
     y[idx] = apply_act(v, d.act);
 }
 
+// Depthwise (one input and one output channel per group): a 32 x 32 tile of
+// output pixels per block, its input window (with halo, zero-filled outside the
+// image) staged once in LDS, so each input element is read from HBM once per
+// tile instead of KH*KW times through the cache. Each thread computes a
+// column strip of 4 outputs, reusing every LDS value it reads for all the
+// outputs whose window covers it.
+constexpr int kDwTH = 32, kDwTW = 32, kDwRows = 4;
+
+template <int K, int S>
+__global__ __launch_bounds__(256) void dw_tiled_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                       const float *__restrict__ bias, const float *__restrict__ res,
+                                                       float *__restrict__ y, SpinnHipConvDesc d, int tiles_w,
+                                                       int64_t planes) {
+    constexpr int IH = (kDwTH - 1) * S + K; // input rows of a tile
+    constexpr int IW = (kDwTW - 1) * S + K; // input cols of a tile
+    constexpr int LW = IW + 1;
+    constexpr int RIN = (kDwRows - 1) * S + K; // input rows one strip reads
+    __shared__ float tile[IH * LW];
+    const int tx = threadIdx.x & (kDwTW - 1), ty = threadIdx.x / kDwTW; // ty in [0, 8)
+    const int th = blockIdx.x / tiles_w, tw = blockIdx.x - th * tiles_w;
+    const int oh0 = th * kDwTH + ty * kDwRows, ow = tw * kDwTW + tx;
+    const int ih0 = th * kDwTH * S - d.ph, iw0 = tw * kDwTW * S - d.pw;
+    const int64_t hw = (int64_t)d.h * d.w, ohw = (int64_t)d.oh * d.ow;
+    for (int64_t plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        const int c = (int)(plane % d.c);
+        const float *xp = x + plane * hw;
+        for (int e = threadIdx.x; e < IH * IW; e += 256) {
+            const int r = e / IW, q = e - r * IW;
+            const int ih = ih0 + r, iw = iw0 + q;
+            tile[r * LW + q] = ((unsigned)ih < (unsigned)d.h && (unsigned)iw < (unsigned)d.w) ? xp[(int64_t)ih * d.w + iw]
+                                                                                               : 0.f;
+        }
+        float wk[K * K];
+#pragma unroll
+        for (int i = 0; i < K * K; ++i) wk[i] = w[(int64_t)c * K * K + i];
+        __syncthreads();
+        float acc[kDwRows];
+#pragma unroll
+        for (int r = 0; r < kDwRows; ++r) acc[r] = 0.f;
+        const float *trow = tile + (ty * kDwRows * S) * LW + tx * S;
+#pragma unroll
+        for (int ir = 0; ir < RIN; ++ir) {
+#pragma unroll
+            for (int kw = 0; kw < K; ++kw) {
+                const float v = trow[ir * LW + kw];
+#pragma unroll
+                for (int r = 0; r < kDwRows; ++r) {
+                    const int kh = ir - r * S;
+                    if (kh >= 0 && kh < K) acc[r] = fmaf(wk[kh * K + kw], v, acc[r]);
+                }
+            }
+        }
+        if (ow < d.ow) {
+            const float b = bias ? bias[c] : 0.f;
+#pragma unroll
+            for (int r = 0; r < kDwRows; ++r) {
+                const int oh = oh0 + r;
+                if (oh < d.oh) {
+                    const int64_t idx = plane * ohw + (int64_t)oh * d.ow + ow;
+                    float v = acc[r] + b;
+                    if (res) v += res[idx];
+                    y[idx] = apply_act(v, d.act);
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Stem convolutions with few input channels (RGB images): one thread per
+// output pixel computes a chunk of 16 output channels, reading each input
+// channel's KH x KW window into registers once and the chunk's weights from
+// LDS (every lane reads the same word: a broadcast). The implicit GEMM would
+// run these with K = C*KH*KW of 27..147 and mostly padded tiles.
+constexpr int kStemOcb = 16;
+
+template <int KH, int KW>
+__global__ __launch_bounds__(256) void stem_conv_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                        const float *__restrict__ bias, const float *__restrict__ res,
+                                                        float *__restrict__ y, SpinnHipConvDesc d) {
+    __shared__ __attribute__((aligned(16))) float ws[kStemOcb * 4 * KH * KW];
+    const int taps = d.c * KH * KW;
+    const int oc0 = blockIdx.y * kStemOcb;
+    const int ocn = min(kStemOcb, d.oc - oc0);
+    for (int e = threadIdx.x; e < kStemOcb * taps; e += 256) {
+        const int o = e / taps, t = e - o * taps;
+        ws[t * kStemOcb + o] = o < ocn ? w[(int64_t)(oc0 + o) * taps + t] : 0.f;
+    }
+    __syncthreads();
+    const int64_t ohw = (int64_t)d.oh * d.ow;
+    const int64_t total = (int64_t)d.n * ohw;
+    for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+        const int64_t n = e / ohw;
+        const int p = (int)(e - n * ohw);
+        const int oh = p / d.ow, ow = p - oh * d.ow;
+        const int ih0 = oh * d.sh - d.ph, iw0 = ow * d.sw - d.pw;
+        float acc[kStemOcb];
+#pragma unroll
+        for (int o = 0; o < kStemOcb; ++o) acc[o] = 0.f;
+        for (int c = 0; c < d.c; ++c) {
+            const float *xc = x + (n * d.c + c) * (int64_t)d.h * d.w;
+            float win[KH * KW];
+#pragma unroll
+            for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+                for (int kw = 0; kw < KW; ++kw) {
+                    const int ih = ih0 + kh, iw = iw0 + kw;
+                    win[kh * KW + kw] =
+                        ((unsigned)ih < (unsigned)d.h && (unsigned)iw < (unsigned)d.w) ? xc[(int64_t)ih * d.w + iw] : 0.f;
+                }
+            const float *wc = ws + c * KH * KW * kStemOcb;
+#pragma unroll
+            for (int t = 0; t < KH * KW; ++t) {
+#pragma unroll
+                for (int o = 0; o < kStemOcb; o += 4) {
+                    const float4 wv = *reinterpret_cast<const float4 *>(wc + t * kStemOcb + o);
+                    acc[o + 0] = fmaf(wv.x, win[t], acc[o + 0]);
+                    acc[o + 1] = fmaf(wv.y, win[t], acc[o + 1]);
+                    acc[o + 2] = fmaf(wv.z, win[t], acc[o + 2]);
+                    acc[o + 3] = fmaf(wv.w, win[t], acc[o + 3]);
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 0; o < kStemOcb; ++o) {
+            if (o < ocn) {
+                const int64_t idx = (n * d.oc + oc0 + o) * ohw + p;
+                float v = acc[o];
+                if (bias) v += bias[oc0 + o];
+                if (res) v += res[idx];
+                y[idx] = apply_act(v, d.act);
+            }
+        }
+    }
+}
+
+bool stem_conv_eligible(const SpinnHipConvDesc *d) {
+    return d->group == 1 && d->c <= 4 && ((d->kh == 3 && d->kw == 3) || (d->kh == 7 && d->kw == 7));
+}
+
+// Measured on MI355X: 2.6x the implicit GEMM for a 3x3 stem into 16 channels
+// (YOLO, 640x640), while a 7x7 stem into 64 channels (ResNet) has enough K
+// and M for the matrix cores to win.
+bool stem_conv_pays(const SpinnHipConvDesc *d) { return stem_conv_eligible(d) && d->kh == 3 && d->oc <= 32; }
+
+template <int K, int S>
+static int launch_dw(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias, const float *res,
+                     float *y, hipStream_t st) {
+    const int tiles_h = (d->oh + kDwTH - 1) / kDwTH, tiles_w = (d->ow + kDwTW - 1) / kDwTW;
+    const int64_t planes = (int64_t)d->n * d->c;
+    dim3 grid((unsigned)(tiles_h * tiles_w), (unsigned)std::min<int64_t>(planes, 65535));
+    hipLaunchKernelGGL((dw_tiled_kernel<K, S>), grid, dim3(256), 0, st, x, w, bias, res, y, *d, tiles_w, planes);
+    return check_launch();
+}
+
 int direct_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias, const float *res,
                 float *y, hipStream_t st) {
     const int ohw = d->oh * d->ow;
+    const bool depthwise = d->group == d->c && d->group == d->oc && d->kh == d->kw && d->sh == d->sw;
+    if (depthwise && (int64_t)((d->oh + kDwTH - 1) / kDwTH) * ((d->ow + kDwTW - 1) / kDwTW) <= 65535) {
+        if (d->kh == 3 && d->sh == 1) return launch_dw<3, 1>(d, x, w, bias, res, y, st);
+        if (d->kh == 3 && d->sh == 2) return launch_dw<3, 2>(d, x, w, bias, res, y, st);
+        if (d->kh == 5 && d->sh == 1) return launch_dw<5, 1>(d, x, w, bias, res, y, st);
+        if (d->kh == 7 && d->sh == 1) return launch_dw<7, 1>(d, x, w, bias, res, y, st);
+    }
+    if (stem_conv_eligible(d)) {
+        const int64_t total = (int64_t)d->n * ohw;
+        dim3 grid((unsigned)std::min<int64_t>((total + 255) / 256, 1 << 16), (unsigned)((d->oc + kStemOcb - 1) / kStemOcb));
+        if (d->kh == 3)
+            hipLaunchKernelGGL((stem_conv_kernel<3, 3>), grid, dim3(256), 0, st, x, w, bias, res, y, *d);
+        else
+            hipLaunchKernelGGL((stem_conv_kernel<7, 7>), grid, dim3(256), 0, st, x, w, bias, res, y, *d);
+        return check_launch();
+    }
     const int64_t planes = (int64_t)d->n * d->oc;
     if (planes > 2147483647LL) return SPINN_HIP_EUNSUPPORTED;
     dim3 grid((ohw + 255) / 256, (unsigned)planes);

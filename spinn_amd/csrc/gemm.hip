@@ -40,8 +40,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmKArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm0 = (wave >> 1) * WT::WM;
-    const int wn0 = (wave & 1) * WT::WN;
+    const int wm0 = WT::origin_m(wave);
+    const int wn0 = WT::origin_n(wave);
     int tile_m, tile_n;
     xcd_tile(gridDim.y, gridDim.x, tile_m, tile_n);
     const int n0 = tile_n * BN;
@@ -240,6 +240,7 @@ int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const fl
     if (tc.bm == 128 && tc.bn == 128) rc = launch_gemm_loaders<128, 128>(a, ta, tb, va, vb, batch, tc.split, st);
     else if (tc.bm == 128 && tc.bn == 64) rc = launch_gemm_loaders<128, 64>(a, ta, tb, va, vb, batch, tc.split, st);
     else if (tc.bm == 64 && tc.bn == 128) rc = launch_gemm_loaders<64, 128>(a, ta, tb, va, vb, batch, tc.split, st);
+    else if (tc.bm == 32 && tc.bn == 128) rc = launch_gemm_loaders<32, 128>(a, ta, tb, va, vb, batch, tc.split, st);
     else rc = launch_gemm_loaders<64, 64>(a, ta, tb, va, vb, batch, tc.split, st);
     if (rc) return rc;
     if (tc.split > 1) {

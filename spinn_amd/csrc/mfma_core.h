@@ -1,7 +1,7 @@
 // mfma_core.h - fp32 MFMA tile engine for gfx950 (CDNA4, wave64).
 //
-// One workgroup = 256 threads = 4 waves arranged 2x2 over a BM x BN output
-// tile. Each wave owns a (BM/2) x (BN/2) sub-tile made of 32x32 blocks computed
+// One workgroup = 256 threads = 4 waves arranged 2x2 (1x4 for 32-row tiles)
+// over a BM x BN output tile. Each wave owns a sub-tile made of 32x32 blocks computed
 // with v_mfma_f32_32x32x2f32 (4096 flop per instruction, 64 cycles, the full
 // fp32 matrix rate of a SIMD). The K loop stages BK-deep slices of both
 // operands through two LDS buffers and two register stages (gemm_mainloop).
@@ -34,13 +34,19 @@ struct LdsPad {
     static constexpr int stride = BT + value;
 };
 
+// The 4 waves of a workgroup sit 2x2 over the tile, or 1x4 when the tile is
+// only 32 rows tall (small-OC convs); wave w starts at (origin_m, origin_n).
 template <int BM, int BN>
 struct WaveTiling {
-    static constexpr int WM = BM / 2;  // rows per wave
-    static constexpr int WN = BN / 2;  // cols per wave
-    static constexpr int TM = WM / 32; // 32x32 blocks per wave along M
+    static constexpr int WAVES_M = BM >= 64 ? 2 : 1;
+    static constexpr int WAVES_N = 4 / WAVES_M;
+    static constexpr int WM = BM / WAVES_M; // rows per wave
+    static constexpr int WN = BN / WAVES_N; // cols per wave
+    static constexpr int TM = WM / 32;      // 32x32 blocks per wave along M
     static constexpr int TN = WN / 32;
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be a multiple of 32x32");
+    __device__ static int origin_m(int wave) { return (wave / WAVES_N) * WM; }
+    __device__ static int origin_n(int wave) { return (wave % WAVES_N) * WN; }
 };
 
 // ---------------------------------------------------------------------------
@@ -72,12 +78,17 @@ __device__ __forceinline__ f32x4 buf_f32x4(__amdgpu_buffer_rsrc_t r, uint32_t of
 // W^T, a transposed Gemm A, a plain Gemm B); `bytes` covers rows [0, K).
 // VEC: float4 along T, which needs ld % 4 == 0, a 16-byte aligned base and a
 // tile width T that is a multiple of 4 (or zero-padded to one).
+// A tile of fewer elements than threads (VEC: fewer float4s) has the spare
+// threads repeat the first ones: they load and store the same values to the
+// same LDS words, which keeps every load unconditional.
 template <int BT, int BK, bool VEC>
 struct KMajorLoader {
     static constexpr bool kIsKMajor = true;
     static constexpr int S = LdsPad<BT>::stride;
-    static constexpr int NV = VEC ? (BK * BT / 4) / kThreads : (BK * BT) / kThreads;
-    static_assert(NV >= 1, "tile too small for 256 threads");
+    static constexpr int ITEMS = VEC ? BK * BT / 4 : BK * BT; // float4s (VEC) or floats per slice
+    static constexpr int NV = ITEMS >= kThreads ? ITEMS / kThreads : 1;
+    static_assert(ITEMS % kThreads == 0 || kThreads % ITEMS == 0, "tile does not map onto 256 threads");
+    __device__ static int item(int tid, int i) { return ITEMS >= kThreads ? tid + i * kThreads : tid % ITEMS; }
     __amdgpu_buffer_rsrc_t rsrc;
     uint32_t ld;
     uint32_t t0;  // first tile index (m0 or n0)
@@ -95,7 +106,7 @@ struct KMajorLoader {
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                const int c = tid + i * kThreads;
+                const int c = item(tid, i);
                 const int k = c / (BT / 4);
                 const int t = (c % (BT / 4)) * 4;
                 const uint32_t off = t < t_valid ? ((uint32_t)(k0 + k) * ld + t0 + t) * 4u : kOOB;
@@ -104,7 +115,7 @@ struct KMajorLoader {
         } else {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                const int e = tid + i * kThreads;
+                const int e = item(tid, i);
                 const int k = e / BT;
                 const int t = e % BT;
                 const uint32_t off = t < t_valid ? ((uint32_t)(k0 + k) * ld + t0 + t) * 4u : kOOB;
@@ -116,13 +127,13 @@ struct KMajorLoader {
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                const int c = tid + i * kThreads;
+                const int c = item(tid, i);
                 *reinterpret_cast<f32x4 *>(lds + (c / (BT / 4)) * S + (c % (BT / 4)) * 4) = rv[i];
             }
         } else {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
-                const int e = tid + i * kThreads;
+                const int e = item(tid, i);
                 lds[(e / BT) * S + (e % BT)] = rs[i];
             }
         }
@@ -138,8 +149,11 @@ template <int BT, int BK, bool VEC>
 struct RowKLoader {
     static constexpr bool kIsKMajor = false;
     static constexpr int S = LdsPad<BT>::stride;
-    static constexpr int NQ = (BK / 4) * BT / kThreads;
-    static_assert(NQ >= 1 && BK % 4 == 0, "tile too small");
+    static constexpr int ITEMS = (BK / 4) * BT; // float4 row pieces per slice
+    static constexpr int NQ = ITEMS >= kThreads ? ITEMS / kThreads : 1;
+    static_assert(BK % 4 == 0 && (ITEMS % kThreads == 0 || kThreads % ITEMS == 0), "tile does not map onto 256 threads");
+    // spare threads of a small tile repeat the first ones (same loads, same LDS words)
+    __device__ static int item(int tid, int i) { return ITEMS >= kThreads ? tid + i * kThreads : tid % ITEMS; }
     __amdgpu_buffer_rsrc_t rsrc;
     uint32_t ld;
     uint32_t t0;
@@ -158,7 +172,7 @@ struct RowKLoader {
     __device__ __forceinline__ void fetch(int k0, int tid) {
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
-            const int c = tid + i * kThreads;
+            const int c = item(tid, i);
             const int t = c % BT;
             const int kk = k0 + (c / BT) * 4;
             const uint32_t row = (t0 + t) * ld;
@@ -178,7 +192,7 @@ struct RowKLoader {
     __device__ __forceinline__ void commit(float *lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
-            const int c = tid + i * kThreads;
+            const int c = item(tid, i);
             const int t = c % BT;
             const int kq = (c / BT) * 4;
             lds[(kq + 0) * S + t] = r[i][0];

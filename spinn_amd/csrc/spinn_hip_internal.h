@@ -55,6 +55,10 @@ int winograd_conv(const SpinnHipConvDesc *d, const float *x, const float *packed
 // grouped / depthwise direct convolution (direct_conv.hip)
 int direct_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias, const float *res,
                 float *y, hipStream_t st);
+// group 1, <= 4 input channels, 3x3 or 7x7: the stem kernel of direct_conv;
+// stem_conv_pays: the shapes where AUTO prefers it
+bool stem_conv_eligible(const SpinnHipConvDesc *d);
+bool stem_conv_pays(const SpinnHipConvDesc *d);
 
 // glue (glue.hip)
 int maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, hipStream_t st);

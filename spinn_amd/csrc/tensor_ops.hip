@@ -271,18 +271,32 @@ __global__ __launch_bounds__(kThreads) void transpose2d_kernel(const float *__re
     }
 }
 
-// blockIdx.y strides the output rows (plane * oh + i), x-lanes run along a row.
+// One thread per 4 consecutive outputs of a row (ow % 4 == 0: a float4 store,
+// 4 source loads that hit the same one or two input words for upsampling);
+// otherwise one output per thread. Rows are flattened over all planes.
+template <bool VEC>
 __global__ __launch_bounds__(kThreads) void resize_nearest_kernel(const float *__restrict__ x,
                                                                   float *__restrict__ y, int64_t nc, int h, int w,
                                                                   int oh, int ow) {
-    for (int64_t row = blockIdx.y; row < nc * oh; row += gridDim.y) {
+    constexpr int V = VEC ? 4 : 1;
+    const int64_t per_row = ow / V;
+    const int64_t total = nc * oh * per_row;
+    for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < total; e += (int64_t)gridDim.x * kThreads) {
+        const int64_t row = e / per_row;
+        const int j0 = (int)(e - row * per_row) * V;
         const int64_t p = row / oh;
         const int i = (int)(row - p * oh);
-        const int hi = (int)((int64_t)i * h / oh);
-        const float *xr = x + (p * h + hi) * (int64_t)w;
-        float *yr = y + row * (int64_t)ow;
-        for (int j = blockIdx.x * kThreads + threadIdx.x; j < ow; j += gridDim.x * kThreads)
-            yr[j] = xr[(int64_t)j * w / ow];
+        const float *xr = x + (p * h + (int64_t)i * h / oh) * (int64_t)w;
+        if constexpr (VEC) {
+            float4 v;
+            v.x = xr[(int64_t)(j0 + 0) * w / ow];
+            v.y = xr[(int64_t)(j0 + 1) * w / ow];
+            v.z = xr[(int64_t)(j0 + 2) * w / ow];
+            v.w = xr[(int64_t)(j0 + 3) * w / ow];
+            *reinterpret_cast<float4 *>(y + row * ow + j0) = v;
+        } else {
+            y[row * ow + j0] = xr[(int64_t)j0 * w / ow];
+        }
     }
 }
 
@@ -428,9 +442,14 @@ int transpose(int ndim, const int64_t *dims, const int32_t *perm, const float *x
 }
 
 int resize_nearest(int64_t nc, int h, int w, int oh, int ow, const float *x, float *y, hipStream_t st) {
-    if (nc * oh * ow == 0) return 0;
-    const dim3 grid((unsigned)((ow + kThreads - 1) / kThreads), (unsigned)std::min<int64_t>(nc * oh, 65535));
-    hipLaunchKernelGGL(resize_nearest_kernel, grid, dim3(kThreads), 0, st, x, y, nc, h, w, oh, ow);
+    const int64_t total = nc * oh * ow;
+    if (total == 0) return 0;
+    if (ow % 4 == 0 && aligned16(y))
+        hipLaunchKernelGGL(resize_nearest_kernel<true>, dim3(grid_1d(total / 4)), dim3(kThreads), 0, st, x, y, nc, h,
+                           w, oh, ow);
+    else
+        hipLaunchKernelGGL(resize_nearest_kernel<false>, dim3(grid_1d(total)), dim3(kThreads), 0, st, x, y, nc, h, w,
+                           oh, ow);
     return check_launch();
 }
 

@@ -14,7 +14,9 @@ void force_tiles(int bm, int bn, int split) {
     g_force_split = split;
 }
 
-static bool valid_tile(int bm, int bn) { return (bm == 64 || bm == 128) && (bn == 64 || bn == 128); }
+static bool valid_tile(int bm, int bn) {
+    return ((bm == 64 || bm == 128) && (bn == 64 || bn == 128)) || (bm == 32 && bn == 128);
+}
 
 TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
     if (g_force_bm && valid_tile(g_force_bm, g_force_bn)) {
@@ -37,10 +39,16 @@ TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
         tc.bm = tc.bn = 128;
         return tc;
     }
-    // Conv-sized problems: 64x64 tiles run up to six blocks per CU, which is
-    // what hides the load latency of a short K loop (measured faster than
-    // 128-wide tiles on every ResNet-101 layer shape at batch 32).
-    const int64_t tiles = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * reps;
+    // At most 32 rows (output channels): a 32 x 128 tile, waves side by side,
+    // instead of a 64-row tile that would compute on zero-padded rows.
+    // Otherwise 64x64 tiles run up to six blocks per CU, which is what hides
+    // the load latency of a short K loop (measured faster than 128-wide tiles
+    // on every ResNet-101 layer shape at batch 32).
+    if (M <= 32) {
+        tc.bm = 32;
+        tc.bn = 128;
+    }
+    const int64_t tiles = (int64_t)((M + tc.bm - 1) / tc.bm) * ((N + tc.bn - 1) / tc.bn) * reps;
     if (allow_split && ((K >= 512 && tiles < 2 * cus) || (K >= 256 && 2 * tiles < cus))) {
         // Split K only when each split still runs >= 128 deep: the partial
         // sums cost a write and a read of the output per split. A 256-deep

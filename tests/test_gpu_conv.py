@@ -27,6 +27,14 @@ CASES = [
     ("pw1x1_grouped", 2, 64, 8, 8, 64, 1, 1, 0, 2, 1, 0),
     ("pw1x1_splitk", 1, 1024, 7, 8, 256, 1, 1, 0, 1, 5, 0),
     ("pw1x1_odd_plane", 2, 64, 7, 7, 96, 1, 1, 0, 1, 1, 0),     # 49-pixel planes: gather loader
+    ("oc16_3x3_32row_tile", 2, 16, 40, 40, 16, 3, 1, 1, 1, 3, 0),   # <= 32 output channels: 32 x 128 tiles
+    ("oc32_pw_add_relu", 2, 48, 20, 20, 32, 1, 1, 0, 1, 5, 0),
+    ("stem_c3_oc16_s2", 2, 3, 64, 64, 16, 3, 2, 1, 1, 3, 0),
+    ("oc24_splitk", 1, 512, 7, 7, 24, 3, 1, 1, 1, 1, 0),
+    ("stem3x3_direct", 2, 3, 64, 64, 16, 3, 2, 1, 1, 3, 3),        # few-input-channel stem kernel
+    ("stem7x7_direct", 1, 3, 40, 40, 64, 7, 2, 3, 1, 1, 3),
+    ("stem_c1_direct_oc20_res", 1, 1, 33, 35, 20, 3, 1, 1, 1, 5, 3),  # partial 16-channel chunk, residual
+    ("direct_group1_general", 1, 6, 10, 12, 5, 3, 1, 1, 1, 1, 3),      # C > 4: general direct kernel
     ("conv3x3_s2", 2, 128, 28, 28, 128, 3, 2, 1, 1, 1, 0),
     ("ragged_silu_c3", 1, 3, 17, 19, 83, 3, 1, 1, 1, 3, 0),
     ("add_only", 1, 32, 9, 11, 48, 3, 1, 1, 1, 4, 0),
@@ -34,6 +42,11 @@ CASES = [
     ("gemm_grouped", 2, 64, 14, 14, 64, 3, 1, 1, 4, 1, 0),
     ("depthwise_s2_silu", 2, 32, 20, 20, 32, 3, 2, 1, 32, 3, 0),
     ("depthwise7x7", 1, 24, 20, 20, 24, 7, 1, 3, 24, 3, 0),
+    ("depthwise_add_pe", 2, 128, 20, 20, 128, 3, 1, 1, 128, 4, 0),   # PSA pe conv: residual fused
+    ("depthwise_ragged_s1", 3, 16, 37, 45, 16, 3, 1, 1, 16, 1, 0),   # tiles past the plane edge
+    ("depthwise5x5_s1", 1, 8, 19, 70, 8, 5, 1, 2, 8, 0, 0),
+    ("depthwise_s2_ragged", 2, 12, 41, 67, 12, 3, 2, 1, 12, 3, 0),
+    ("grouped_direct_cg2", 1, 16, 12, 12, 8, 3, 1, 1, 8, 1, 0),      # two input channels per group: general kernel
     ("winograd_add_relu", 2, 64, 28, 28, 64, 3, 1, 1, 1, 5, 2),
     ("winograd_odd", 1, 16, 15, 13, 8, 3, 1, 1, 1, 1, 2),
     ("winograd_c256", 1, 256, 14, 14, 256, 3, 1, 1, 1, 1, 2),

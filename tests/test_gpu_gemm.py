@@ -24,12 +24,13 @@ def test_gemm_sweep(hip, torch_gpu, mnk):
     assert_parity(y, O.gemm_f64(a, b, c, trans_b=1), what="vs float64")
 
 
+@pytest.mark.parametrize("m", [37, 19], ids=["m37", "m19_32row_tile"])
 @pytest.mark.parametrize("ta", [0, 1])
 @pytest.mark.parametrize("tb", [0, 1])
 @pytest.mark.parametrize("cmode", [0, 1, 2])
-def test_gemm_transposes_ragged(hip, torch_gpu, ta, tb, cmode):
-    m, n, k = 37, 45, 29
-    rng = np.random.default_rng(100 + 4 * ta + 2 * tb + cmode)
+def test_gemm_transposes_ragged(hip, torch_gpu, ta, tb, cmode, m):
+    n, k = 45, 29
+    rng = np.random.default_rng(100 + 4 * ta + 2 * tb + cmode + m)
     a = rng.uniform(-1, 1, (k, m) if ta else (m, k)).astype(np.float32)
     b = rng.uniform(-1, 1, (n, k) if tb else (k, n)).astype(np.float32)
     c = None if cmode == 0 else rng.uniform(-1, 1, n if cmode == 1 else (m, n)).astype(np.float32)

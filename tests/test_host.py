@@ -211,6 +211,8 @@ def test_conv_algo_selection(native):
     assert algo(32, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM   # 64 channels
     assert algo(1, 256, 14, 14, 256, 3, 2, 1, 1) == native.ALGO_IMPLICIT_GEMM
     assert algo(1, 128, 20, 20, 128, 3, 2, 1, 128) == native.ALGO_DIRECT
+    assert algo(16, 3, 640, 640, 16, 3, 2, 1, 1) == native.ALGO_DIRECT          # RGB stem into 16 channels
+    assert algo(32, 3, 224, 224, 64, 7, 2, 3, 1) == native.ALGO_IMPLICIT_GEMM   # ResNet stem: matrix cores
     assert algo(1, 6, 8, 8, 4, 3, 1, 1, 4) == native.SPINN_HIP_EINVAL  # C % group != 0
 
 
