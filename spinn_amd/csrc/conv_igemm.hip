@@ -60,8 +60,6 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
     al.init(a.wpk + group * a.wpk_group_stride, (uint32_t)a.K * (uint32_t)a.ldw * 4u, (uint32_t)a.ldw, m0, a.ldw);
     BLoader bl;
     bl.init(a.geom, n0, group, tid, k_end);
-    KMajorLoader<BM, BK, true> al1 = al;
-    BLoader bl1 = bl;
 
     f32x16 acc[WT::TM][WT::TN];
 #pragma unroll
@@ -72,7 +70,7 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int nslices = (k_end - k_begin + BK - 1) / BK;
-    gemm_mainloop<BM, BN, BK>(al, bl, al1, bl1, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0);
+    gemm_mainloop<BM, BN, BK, kStages>(al, bl, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0);
 
     // Epilogue: lane owns column jcol = n0 + wn0 + j*32 + lane%32 and rows
     // m0 + wm0 + i*32 + 8*(r/4) + 4*(lane/32) + r%4. All bias and residual

@@ -66,8 +66,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmKArgs a) {
     } else {
         bl.init(bbase, (uint32_t)(a.N * a.ldb * 4), (uint32_t)a.ldb, n0, a.N, k_end);
     }
-    ALoader al1 = al;
-    BLoader bl1 = bl;
 
     f32x16 acc[WT::TM][WT::TN];
 #pragma unroll
@@ -78,7 +76,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmKArgs a) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     const int nslices = (k_end - k_begin + BK - 1) / BK;
-    gemm_mainloop<BM, BN, BK>(al, bl, al1, bl1, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0);
+    gemm_mainloop<BM, BN, BK, kStages>(al, bl, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0);
 
     // Epilogue: C values of a column block are loaded before any store.
     const int h = lane >> 5;

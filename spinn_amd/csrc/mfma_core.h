@@ -4,7 +4,7 @@
 // over a BM x BN output tile. Each wave owns a sub-tile made of 32x32 blocks computed
 // with v_mfma_f32_32x32x2f32 (4096 flop per instruction, 64 cycles, the full
 // fp32 matrix rate of a SIMD). The K loop stages BK-deep slices of both
-// operands through two LDS buffers and two register stages (gemm_mainloop).
+// operands through two LDS buffers and NS register stages (gemm_mainloop).
 //
 // LDS layout of both operands is k-major, [BK][BT + PAD] with T (the M or N
 // index) contiguous, so the operand fetch of an MFMA (lane l reads element
@@ -450,44 +450,63 @@ __device__ __forceinline__ void pipelined_slice(AL &al, BL &bl, const float *As_
 }
 
 // The K loop shared by every MFMA GEMM kernel: BK slices through two LDS
-// buffers and two register stages. Slice j is fetched from global memory into
-// register stage j%2 during slice j-3, written to LDS buffer j%2 during slice
-// j-1 and consumed in slice j, so a global load has two full slices of MFMA
-// work to arrive, and the LDS writes, address math and loads all overlap the
-// matrix pipe. One barrier per slice. The loop is unrolled by two so both
-// register stages are addressed statically. `al0/bl0` and `al1/bl1` are the
-// two register stages of the A and B loaders (same geometry).
-template <int BM, int BN, int BK, class AL, class BL>
-__device__ __forceinline__ void gemm_mainloop(AL &al0, BL &bl0, AL &al1, BL &bl1,
+// buffers and NS register stages (NS even). Slice j is fetched from global
+// memory into register stage j % NS during slice j-1-NS, written to LDS buffer
+// j % 2 during slice j-1 and consumed in slice j, so a global load has NS full
+// slices of MFMA work to arrive. That distance is what keeps a lone workgroup
+// per CU (small grids, split K, batch 1) from stalling on every slice: under
+// load, HBM latency is several slices of 64x64 MFMA work. The LDS writes,
+// address math and loads all overlap the matrix pipe; one barrier per slice.
+// The steady-state loop is unrolled by NS so every stage is addressed
+// statically. `al_init/bl_init` are loaders initialised for this tile; each
+// stage is a copy of them.
+template <int BM, int BN, int BK, int NS, class AL, class BL>
+__device__ __forceinline__ void gemm_mainloop(const AL &al_init, const BL &bl_init,
                                               float (*As)[BK * LdsPad<BM>::stride],
                                               float (*Bs)[BK * LdsPad<BN>::stride],
                                               f32x16 (&acc)[WaveTiling<BM, BN>::TM][WaveTiling<BM, BN>::TN],
                                               int k_begin, int nslices, int tid, int lane, int wm0, int wn0) {
+    static_assert(NS >= 2 && NS % 2 == 0, "the LDS buffer of a slice is its parity: NS must be even");
     if (nslices <= 0) return;
-    // prologue: slice 0 -> LDS 0; slice 1 -> regs 1; slice 2 -> regs 0
-    al0.fetch(k_begin, tid);
-    bl0.fetch(k_begin, tid);
-    al0.commit(As[0], tid);
-    bl0.commit(Bs[0], tid);
-    al1.fetch(k_begin + BK, tid);
-    bl1.fetch(k_begin + BK, tid);
-    al0.fetch(k_begin + 2 * BK, tid);
-    bl0.fetch(k_begin + 2 * BK, tid);
+    AL al[NS];
+    BL bl[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        al[i] = al_init;
+        bl[i] = bl_init;
+    }
+    // prologue: slice 0 -> LDS 0; slices 1..NS -> register stage j % NS
+    al[0].fetch(k_begin, tid);
+    bl[0].fetch(k_begin, tid);
+    al[0].commit(As[0], tid);
+    bl[0].commit(Bs[0], tid);
+#pragma unroll
+    for (int j = 1; j <= NS; ++j) {
+        al[j % NS].fetch(k_begin + j * BK, tid);
+        bl[j % NS].fetch(k_begin + j * BK, tid);
+    }
     __syncthreads();
     int s = 0;
-    for (; s + 1 < nslices; s += 2) {
-        // even slice s: LDS 0; commit s+1 from regs 1; fetch s+3 into regs 1
-        pipelined_slice<BM, BN, BK>(al1, bl1, As[0], Bs[0], As[1], Bs[1], acc, k_begin + (s + 3) * BK, tid, lane,
-                                    wm0, wn0);
-        // odd slice s+1: LDS 1; commit s+2 from regs 0; fetch s+4 into regs 0
-        pipelined_slice<BM, BN, BK>(al0, bl0, As[1], Bs[1], As[0], Bs[0], acc, k_begin + (s + 4) * BK, tid, lane,
-                                    wm0, wn0);
+    for (; s + NS < nslices; s += NS) {
+        // slice s+u reads LDS (s+u)%2 = u%2, commits slice s+u+1 from stage
+        // (u+1)%NS and refills that stage with slice s+u+1+NS
+#pragma unroll
+        for (int u = 0; u < NS; ++u)
+            pipelined_slice<BM, BN, BK>(al[(u + 1) % NS], bl[(u + 1) % NS], As[u % 2], Bs[u % 2], As[(u + 1) % 2],
+                                        Bs[(u + 1) % 2], acc, k_begin + (s + u + 1 + NS) * BK, tid, lane, wm0, wn0);
     }
-    if (s < nslices) {
-        // last (even) slice: nothing left to stage
-        float a[BK / 2][WaveTiling<BM, BN>::TM], b[BK / 2][WaveTiling<BM, BN>::TN];
-        load_fragments<BM, BN, BK>(As[0], Bs[0], a, b, wm0, wn0, lane);
-        mfma_steps<BM, BN, BK, 0, BK / 2>(a, b, acc);
+    // tail: r = nslices - s slices left, 1 <= r <= NS; the last one only computes
+    const int r = nslices - s;
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+        if (u < r - 1) {
+            pipelined_slice<BM, BN, BK>(al[(u + 1) % NS], bl[(u + 1) % NS], As[u % 2], Bs[u % 2], As[(u + 1) % 2],
+                                        Bs[(u + 1) % 2], acc, k_begin + (s + u + 1 + NS) * BK, tid, lane, wm0, wn0);
+        } else if (u == r - 1) {
+            float a[BK / 2][WaveTiling<BM, BN>::TM], b[BK / 2][WaveTiling<BM, BN>::TN];
+            load_fragments<BM, BN, BK>(As[u % 2], Bs[u % 2], a, b, wm0, wn0, lane);
+            mfma_steps<BM, BN, BK, 0, BK / 2>(a, b, acc);
+        }
     }
 }
 

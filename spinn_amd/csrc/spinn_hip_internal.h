@@ -22,7 +22,12 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     return v;
 }
 
-constexpr int kBK = 16; // K depth of one LDS slice of the MFMA GEMMs
+constexpr int kBK = 16;    // K depth of one LDS slice of the MFMA GEMMs
+// Register stages of the K loop (global loads run that many slices ahead of
+// their LDS write). Measured on the ResNet-101 batch-32 and batch-1 conv
+// shapes: 4 stages were no faster than 2 (the loads are not the stall), and
+// cost registers, so 2.
+constexpr int kStages = 2;
 
 // Output tile (bm x bn) and K split of one MFMA GEMM launch.
 struct TileChoice {
