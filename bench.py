@@ -222,16 +222,20 @@ def _op_family(N, nd, g, policy) -> str:
         return "conv_" + ALGO_NAMES.get(algo_of(N, r, policy), "?")
     return {E.OP_ADD: "add", E.OP_SUB: "sub", E.OP_MUL: "mul", E.OP_CONCAT: "concat", E.OP_SPLIT: "split",
             E.OP_MAXPOOL: "maxpool", E.OP_RESIZE: "resize", E.OP_RESHAPE: "reshape", E.OP_TRANSPOSE: "transpose",
-            E.OP_MATMUL: "matmul", E.OP_SOFTMAX: "softmax", E.OP_SIGMOID: "sigmoid"}.get(nd.op, f"op{nd.op}")
+            E.OP_MATMUL: "matmul", E.OP_SOFTMAX: "softmax", E.OP_SIGMOID: "sigmoid", E.OP_TOPK: "topk",
+            E.OP_REDUCEMAX: "reducemax", E.OP_GATHER_ELEMENTS: "gather_elements", E.OP_TILE: "tile",
+            E.OP_UNSQUEEZE: "unsqueeze", E.OP_FLATTEN: "flatten", E.OP_MOD: "mod", E.OP_DIV: "div",
+            E.OP_CAST: "cast"}.get(nd.op, f"op{nd.op}")
 
 
 def yolo_bench(N, Session, models, tmp: Path, reps: int) -> dict:
-    """YOLOv10n 640x640 at batch 1 and 16: images/s (graph replay, input
+    """YOLOv10n 640x640 at batch 1 and 16, the whole exported graph including the
+    TopK post-processing tail (output [B, 300, 6]): images/s (graph replay, input
     resident), direct-conv-equivalent conv TFLOP/s, and at batch 16 the device
     time per operator family from HIP events around every node."""
     res = {}
     for b in (1, 16):
-        g, x = models.yolov10n(batch=b, seed=0)
+        g, x = models.yolov10n(batch=b, seed=0, postprocess=True)
         path = g.write(tmp / f"y10_b{b}.ennf")
         with Session(path, graph=True) as s:
             s.upload_input(x)
@@ -418,7 +422,7 @@ def main() -> int:
         cpu = cpu_baseline(p1, g1.dims(g1.inputs[0]), g1.dims(g1.outputs[0]), a.cpu_seconds)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
         if not a.no_suite:
-            gy, _ = models.yolov10n(batch=1, seed=0)
+            gy, _ = models.yolov10n(batch=1, seed=0, postprocess=True)
             py = gy.write(tmp / "y10_cpu_b1.ennf")
             cpu_y10 = cpu_baseline(py, gy.dims(gy.inputs[0]), gy.dims(gy.outputs[0]), a.cpu_seconds / 2,
                                    label="YOLOv10n 640x640")

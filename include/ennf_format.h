@@ -85,6 +85,7 @@ enum {
     ENNF_OP_Add = 4,
     ENNF_OP_Clip = 18,
     ENNF_OP_Div = 23,
+    ENNF_OP_Mod = 38,
     ENNF_OP_Mul = 39,
     ENNF_OP_Sub = 50,
     ENNF_OP_Conv = 60,
@@ -97,13 +98,19 @@ enum {
     ENNF_OP_Softmax = 134,
     ENNF_OP_Gemm = 160,
     ENNF_OP_MatMul = 161,
+    ENNF_OP_Cast = 180,
     ENNF_OP_Concat = 183,
     ENNF_OP_Flatten = 189,
+    ENNF_OP_GatherElements = 191,
     ENNF_OP_Identity = 193,
     ENNF_OP_Reshape = 197,
     ENNF_OP_Resize = 198,
     ENNF_OP_Split = 206,
+    ENNF_OP_Tile = 209,
+    ENNF_OP_TopK = 210,
     ENNF_OP_Transpose = 211,
+    ENNF_OP_Unsqueeze = 214,
+    ENNF_OP_ReduceMax = 234,
     ENNF_OP_ReduceMean = 235,
     ENNF_OP_REGISTRY_SIZE = 512
 };
@@ -219,6 +226,18 @@ typedef struct {
     uint8_t reserved[3];
 } ENNF_TransposeParams; /* SPINN/ennf_op_params.h:147-151 */
 
+typedef struct {
+    int32_t axis;
+    int32_t batch_dims;
+} ENNF_GatherParams; /* Gather, GatherElements (SPINN/ennf_op_params.h:205-209) */
+
+typedef struct {
+    int32_t axis;
+    uint8_t largest;
+    uint8_t sorted;
+    uint8_t reserved[2];
+} ENNF_TopKParams; /* SPINN/ennf_op_params.h:218-224 */
+
 #if defined(__cplusplus)
 #define ENNF_STATIC_ASSERT(c, m) static_assert(c, m)
 #else
@@ -235,6 +254,8 @@ ENNF_STATIC_ASSERT(sizeof(ENNF_ReduceParams) == 36, "ENNF_ReduceParams must be 3
 ENNF_STATIC_ASSERT(sizeof(ENNF_SplitParams) == 8, "ENNF_SplitParams must be 8 bytes");
 ENNF_STATIC_ASSERT(sizeof(ENNF_TransposeParams) == 12, "ENNF_TransposeParams must be 12 bytes");
 ENNF_STATIC_ASSERT(sizeof(ENNF_BatchNormParams) == 12, "ENNF_BatchNormParams must be 12 bytes");
+ENNF_STATIC_ASSERT(sizeof(ENNF_GatherParams) == 8, "ENNF_GatherParams must be 8 bytes");
+ENNF_STATIC_ASSERT(sizeof(ENNF_TopKParams) == 8, "ENNF_TopKParams must be 8 bytes");
 
 static inline size_t ennf_dtype_bytes(int dtype) {
     switch (dtype) {

@@ -177,6 +177,57 @@ int spinn_hip_transpose(int ndim, const int64_t *dims, const int32_t *perm, cons
 int spinn_hip_resize_nearest(int64_t nc, int32_t h, int32_t w, int32_t oh, int32_t ow, const float *x, float *y,
                              void *stream);
 
+/* ---- detector post-processing: ReduceMax, TopK, GatherElements, Tile, Cast, integer Div/Mod ---- */
+
+/* y[i] = max over x[i * block .. i * block + block) for i < rows, taken in index
+ * order from the first element with `>` (SPINN/run_time/ops/reduce/reduce_max.c:4-28:
+ * block = |x| / |y|). Rows containing NaN are outside the parity contract. */
+int spinn_hip_reduce_max(int64_t rows, int64_t block, const float *x, float *y, void *stream);
+
+/* TopK over the last axis of rows x n (SPINN/run_time/ops/tensor/topk.c:20-89): the k
+ * largest values of each row, sorted descending, ties in ascending index order (the
+ * reference sorts (value, index) pairs with glibc qsort, a stable merge sort, under
+ * `a > b`; -0.0 and +0.0 compare equal). values [rows, k] fp32, indices [rows, k] int64.
+ * 1 <= k <= min(n, SPINN_HIP_TOPK_MAX_K). NaN inputs are outside the parity contract. */
+#define SPINN_HIP_TOPK_MAX_K 1024
+int spinn_hip_topk(int64_t rows, int64_t n, int64_t k, const float *x, float *values, int64_t *indices,
+                   void *stream);
+
+/* GatherElements (SPINN/run_time/ops/tensor/gather_elements.c:5-76): for every output
+ * coordinate c, y[c] = data[c with c[axis] replaced by idx[c]]; idx < 0 wraps once by
+ * in_dims[axis], an index still outside [0, in_dims[axis]) reads position 0, as in the
+ * reference. index_dtype is ENNF_TYPE_INT64 (7) or ENNF_TYPE_INT32 (6). */
+typedef struct {
+    int32_t ndim;        /* 1..8 */
+    int32_t axis;        /* normalised, 0 <= axis < ndim */
+    int32_t index_dtype; /* 6 = int32, 7 = int64 */
+    int32_t reserved;
+    int64_t in_dims[8];  /* data */
+    int64_t out_dims[8]; /* indices and y */
+} SpinnHipGatherDesc;
+int spinn_hip_gather_elements(const SpinnHipGatherDesc *d, const float *data, const void *indices, float *y,
+                              void *stream);
+
+/* Tile (SPINN/run_time/ops/tensor/tile.c:6-65): y[c] = x[c mod in_dims] per axis for
+ * every output coordinate c; elements of elem_bytes in {1, 2, 4, 8}. */
+int spinn_hip_tile(int ndim, const int64_t *in_dims, const int64_t *out_dims, int elem_bytes, const void *x,
+                   void *y, void *stream);
+
+/* Cast between ENNF_TYPE_FLOAT32 / INT32 / INT64 (SPINN/run_time/ops/tensor/cast.c:13-73):
+ * int -> float rounds to nearest, float -> int truncates toward zero, int64 -> int32
+ * keeps the low 32 bits; equal types copy. Other pairs: SPINN_HIP_EUNSUPPORTED. */
+int spinn_hip_cast(int src_dtype, int dst_dtype, int64_t n, const void *x, void *y, void *stream);
+
+/* Integer / remainder forms of Div and Mod with the modulo broadcast of
+ * spinn_hip_binary, y[i] = a[i % na] (op) b[i % nb]:
+ *   SPINN_BINARY_DIV on int32 / int64: C division truncating toward zero, 0 where b == 0
+ *     (SPINN/run_time/ops/math/div.c:33-48);
+ *   SPINN_BINARY_MOD on int32 / int64: C remainder (sign of a), 0 where b == 0;
+ *     on fp32: fmodf (SPINN/run_time/ops/math/mod.c:18-45). */
+enum { SPINN_BINARY_MOD = 4 };
+int spinn_hip_binary_typed(int op, int dtype, const void *a, int64_t na, const void *b, int64_t nb, void *y,
+                           int64_t n, void *stream);
+
 /* ---- device, memory, stream, event and graph plumbing for the host runtime ---- */
 
 int spinn_hip_init(int device);

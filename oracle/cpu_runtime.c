@@ -232,6 +232,8 @@ static int run_node(OracleModel *m, ON *n) {
     case ENNF_OP_Div: {
         OT *B = &m->t[n->in[1]];
         if (n->nin < 2 || X->elems == 0 || B->elems == 0) return n->nin < 2 ? -1 : 0;
+        if (n->op == ENNF_OP_Div && X->dtype != ENNF_TYPE_FLOAT32)
+            return oracle_binary_typed(3, X->dtype, X->data, X->elems, B->data, B->elems, Y->data, Y->elems);
         const int op = n->op == ENNF_OP_Add ? 0 : n->op == ENNF_OP_Sub ? 1 : n->op == ENNF_OP_Mul ? 2 : 3;
         oracle_binary(op, (const float *)X->data, X->elems, (const float *)B->data, B->elems, (float *)Y->data,
                       Y->elems);
@@ -297,6 +299,43 @@ static int run_node(OracleModel *m, ON *n) {
         oracle_transpose(X->ndim, dims, perm, (const float *)X->data, (float *)Y->data);
         return 0;
     }
+    case ENNF_OP_Mod: {
+        OT *B = &m->t[n->in[1]];
+        if (n->nin < 2) return -1;
+        return oracle_binary_typed(4, X->dtype, X->data, X->elems, B->data, B->elems, Y->data, Y->elems);
+    }
+    case ENNF_OP_Unsqueeze:
+        memcpy(Y->data, X->data, X->bytes < Y->bytes ? X->bytes : Y->bytes);
+        return 0;
+    case ENNF_OP_ReduceMax:
+        if (Y->elems == 0) return 0;
+        oracle_reduce_max(Y->elems, X->elems / Y->elems, (const float *)X->data, (float *)Y->data);
+        return 0;
+    case ENNF_OP_TopK: {
+        /* K from the second input, rows over the last axis (topk.c:28-56) */
+        if (n->nin < 2 || n->nout < 2) return -1;
+        const int64_t kv = *(const int64_t *)m->t[n->in[1]].data;
+        const long last = X->dims[X->ndim - 1];
+        const long rows = last ? (long)X->elems / last : 0;
+        return oracle_topk(rows, last, kv, (const float *)X->data, (float *)Y->data,
+                           (int64_t *)m->t[n->out[1]].data);
+    }
+    case ENNF_OP_GatherElements: {
+        int axis = 0;
+        if (n->psize >= sizeof(ENNF_GatherParams)) axis = ((const ENNF_GatherParams *)n->params)->axis;
+        if (axis < 0) axis += X->ndim;
+        OT *I = &m->t[n->in[1]];
+        oracle_gather_elements(X->ndim, X->dims, Y->dims, axis, (const float *)X->data, I->data, I->dtype,
+                               (float *)Y->data, Y->elems);
+        return 0;
+    }
+    case ENNF_OP_Tile: {
+        const int es = X->dtype == ENNF_TYPE_INT64 ? 8 : (X->dtype == ENNF_TYPE_UINT8 || X->dtype == ENNF_TYPE_INT8) ? 1 : 4;
+        oracle_tile(X->ndim, X->dims, Y->dims, es, X->data, Y->data);
+        return 0;
+    }
+    case ENNF_OP_Cast:
+        return oracle_cast(X->dtype, Y->dtype, Y->elems, X->data, Y->data);
     case ENNF_OP_Resize:
         if (X->ndim != 4 || Y->ndim != 4) return -1;
         oracle_resize_nearest((long)X->dims[0] * X->dims[1], X->dims[2], X->dims[3], Y->dims[2], Y->dims[3],

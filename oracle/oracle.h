@@ -40,6 +40,15 @@ void oracle_concat(int n_in, const float *const *xs, const long *sizes, long out
 void oracle_split(int n_out, float *const *ys, const long *sizes, long outer, long inner, const float *X);
 void oracle_transpose(int ndim, const long *dims, const int *perm, const float *X, float *Y);
 void oracle_resize_nearest(long planes, int H, int W, int OH, int OW, const float *X, float *Y);
+void oracle_reduce_max(uint32_t out_n, uint32_t block, const float *X, float *Y);
+int oracle_topk(long rows, long n, long k, const float *X, float *vals, int64_t *idx);
+void oracle_gather_elements(int ndim, const uint32_t *in_dims, const uint32_t *out_dims, int axis,
+                            const float *data, const void *indices, int index_dtype, float *Y, uint32_t n);
+void oracle_tile(int ndim, const uint32_t *in_dims, const uint32_t *out_dims, int elem_size, const void *X,
+                 void *Y);
+int oracle_cast(int src, int dst, uint32_t n, const void *X, void *Y);
+int oracle_binary_typed(int op, int dtype, const void *a, uint32_t na, const void *b, uint32_t nb, void *y,
+                        uint32_t n);
 int oracle_num_threads(void);
 void oracle_set_num_threads(int n);
 

@@ -248,6 +248,76 @@ def resize_nearest(x, oh, ow) -> np.ndarray:
     return y
 
 
+# ---- detector post-processing ----
+_VP = C.c_void_p
+_DT = {np.dtype(np.float32): 1, np.dtype(np.int32): 6, np.dtype(np.int64): 7}
+
+
+def _vp(a):
+    return C.c_void_p(a.ctypes.data)
+
+
+def reduce_max(x, out_n) -> np.ndarray:
+    """Max of each of out_n consecutive blocks of x (reduce_max.c)."""
+    x = _c(x)
+    y = np.zeros(out_n, np.float32)
+    lib().oracle_reduce_max(C.c_uint32(out_n), C.c_uint32(x.size // out_n), _f(x), _f(y))
+    return y
+
+
+def topk(x, k):
+    """Top-k along the last axis, sorted descending: (values fp32, indices int64)."""
+    x = _c(x)
+    n = x.shape[-1]
+    rows = x.size // n if n else 0
+    k = min(k, n)
+    v = np.zeros(x.shape[:-1] + (k,), np.float32)
+    i = np.zeros(x.shape[:-1] + (k,), np.int64)
+    rc = lib().oracle_topk(C.c_long(rows), C.c_long(n), C.c_long(k), _f(x), _f(v), _vp(i))
+    if rc:
+        raise RuntimeError(rc)
+    return v, i
+
+
+def gather_elements(data, idx, axis) -> np.ndarray:
+    data = _c(data)
+    idx = np.ascontiguousarray(idx)
+    axis %= data.ndim
+    y = np.zeros(idx.shape, np.float32)
+    u32 = C.c_uint32 * data.ndim
+    lib().oracle_gather_elements(data.ndim, u32(*data.shape), u32(*idx.shape), axis, _f(data), _vp(idx),
+                                 _DT[idx.dtype], _f(y), C.c_uint32(y.size))
+    return y
+
+
+def tile(x, out_shape) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    y = np.zeros(out_shape, x.dtype)
+    u32 = C.c_uint32 * x.ndim
+    lib().oracle_tile(x.ndim, u32(*x.shape), u32(*out_shape), x.dtype.itemsize, _vp(x), _vp(y))
+    return y
+
+
+def cast(x, dtype) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    y = np.zeros(x.shape, dtype)
+    rc = lib().oracle_cast(_DT[x.dtype], _DT[y.dtype], C.c_uint32(x.size), _vp(x), _vp(y))
+    if rc:
+        raise RuntimeError(rc)
+    return y
+
+
+def binary_typed(op: str, a, b, out_shape) -> np.ndarray:
+    """Integer Div / Mod (and float Mod) with the modulo broadcast."""
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    y = np.zeros(out_shape, a.dtype)
+    rc = lib().oracle_binary_typed({"div": 3, "mod": 4}[op], _DT[a.dtype], _vp(a), C.c_uint32(a.size), _vp(b),
+                                   C.c_uint32(b.size), _vp(y), C.c_uint32(y.size))
+    if rc:
+        raise RuntimeError(rc)
+    return y
+
+
 def set_threads(n: int) -> None:
     lib().oracle_set_num_threads(int(n))
 
@@ -261,9 +331,9 @@ class Model:
             raise RuntimeError(f"oracle could not load {path}")
         lib().oracle_model_set_winograd(self._m, 1 if winograd else 0)
 
-    def run(self, x: np.ndarray, out_shape) -> np.ndarray:
-        y = np.zeros(out_shape, np.float32)
-        rc = lib().oracle_model_run(self._m, _f(np.ascontiguousarray(x, np.float32)), _f(y))
+    def run(self, x: np.ndarray, out_shape, dtype=np.float32) -> np.ndarray:
+        y = np.zeros(out_shape, dtype)
+        rc = lib().oracle_model_run(self._m, _f(np.ascontiguousarray(x, np.float32)), C.cast(y.ctypes.data, _FP))
         if rc != 0:
             raise RuntimeError(f"oracle model run failed: {rc}")
         return y

@@ -649,6 +649,170 @@ void oracle_resize_nearest(long planes, int H, int W, int OH, int OW, const floa
                 Y[(p * OH + h) * OW + w] = X[(p * H + (long)h * H / OH) * W + (long)w * W / OW];
 }
 
+/* ---- detector post-processing ---- */
+
+/* ReduceMax: in-order scan of each block of |X|/|Y| elements from its first
+ * element with `>` (SPINN/run_time/ops/reduce/reduce_max.c:16-26). */
+void oracle_reduce_max(uint32_t out_n, uint32_t block, const float *X, float *Y) {
+    for (uint32_t i = 0; i < out_n; i++) {
+        float m = X[(size_t)i * block];
+        for (uint32_t j = 1; j < block; j++) {
+            const float v = X[(size_t)i * block + j];
+            if (v > m) m = v;
+        }
+        Y[i] = m;
+    }
+}
+
+/* TopK (SPINN/run_time/ops/tensor/topk.c:49-85): each row's (value, index) pairs
+ * sorted with qsort under compare_topk_desc (:11-17), the first k kept. The sort
+ * is glibc's: qsort in glibc 2.35 (this image; the reference builds against the
+ * host's glibc) runs a top-down merge sort, stdlib/msort.c - split n1 = n/2,
+ * n2 = n - n1, sort both halves, merge taking the left element while
+ * cmp(left, right) <= 0. Restated here with the same split and merge rule, so
+ * ties keep index order and a NaN (compares "equal" to everything) lands where
+ * that merge sort puts it. */
+typedef struct {
+    float value;
+    int64_t index;
+} OracleTopkEntry;
+
+static int topk_cmp(const OracleTopkEntry *a, const OracleTopkEntry *b) {
+    if (a->value > b->value) return -1;
+    if (a->value < b->value) return 1;
+    return 0;
+}
+
+static void topk_msort(OracleTopkEntry *b, size_t n, OracleTopkEntry *tmp) {
+    if (n <= 1) return;
+    const size_t n1 = n / 2, n2 = n - n1;
+    OracleTopkEntry *b1 = b, *b2 = b + n1;
+    topk_msort(b1, n1, tmp);
+    topk_msort(b2, n2, tmp);
+    size_t i1 = 0, i2 = 0, o = 0;
+    while (i1 < n1 && i2 < n2) {
+        if (topk_cmp(&b1[i1], &b2[i2]) <= 0) tmp[o++] = b1[i1++];
+        else tmp[o++] = b2[i2++];
+    }
+    while (i1 < n1) tmp[o++] = b1[i1++];
+    memcpy(b, tmp, o * sizeof(*b)); /* the tail of b2 is already in place */
+}
+
+int oracle_topk(long rows, long n, long k, const float *X, float *vals, int64_t *idx) {
+    if (k > n) k = n;
+    OracleTopkEntry *e = (OracleTopkEntry *)malloc(sizeof(*e) * (size_t)(n > 0 ? n : 1));
+    OracleTopkEntry *tmp = (OracleTopkEntry *)malloc(sizeof(*tmp) * (size_t)(n > 0 ? n : 1));
+    if (!e || !tmp) {
+        free(e);
+        free(tmp);
+        return -2;
+    }
+    for (long r = 0; r < rows; r++) {
+        for (long i = 0; i < n; i++) {
+            e[i].value = X[r * n + i];
+            e[i].index = i;
+        }
+        topk_msort(e, (size_t)n, tmp);
+        for (long i = 0; i < k; i++) {
+            vals[r * k + i] = e[i].value;
+            idx[r * k + i] = e[i].index;
+        }
+    }
+    free(e);
+    free(tmp);
+    return 0;
+}
+
+/* GatherElements (SPINN/run_time/ops/tensor/gather_elements.c:19-73): output
+ * coordinates from the output strides, the axis coordinate replaced by the
+ * index (wrapped once if negative, 0 if still outside), input strides. */
+void oracle_gather_elements(int ndim, const uint32_t *in_dims, const uint32_t *out_dims, int axis,
+                            const float *data, const void *indices, int index_dtype, float *Y, uint32_t n) {
+    uint32_t os[8], is[8];
+    os[ndim - 1] = 1;
+    is[ndim - 1] = 1;
+    for (int i = ndim - 2; i >= 0; i--) {
+        os[i] = os[i + 1] * out_dims[i + 1];
+        is[i] = is[i + 1] * in_dims[i + 1];
+    }
+    for (uint32_t e = 0; e < n; e++) {
+        uint32_t c[8], t = e;
+        for (int d = 0; d < ndim; d++) {
+            c[d] = t / os[d];
+            t %= os[d];
+        }
+        int64_t g = index_dtype == 7 ? ((const int64_t *)indices)[e] : ((const int32_t *)indices)[e];
+        if (g < 0) g += in_dims[axis];
+        if (g < 0 || g >= in_dims[axis]) g = 0;
+        c[axis] = (uint32_t)g;
+        uint32_t off = 0;
+        for (int d = 0; d < ndim; d++) off += c[d] * is[d];
+        Y[e] = data[off];
+    }
+}
+
+/* Tile: output coordinate c reads input coordinate c mod in_dims
+ * (SPINN/run_time/ops/tensor/tile.c:32-62). */
+void oracle_tile(int ndim, const uint32_t *in_dims, const uint32_t *out_dims, int elem_size, const void *X,
+                 void *Y) {
+    uint32_t os[8], is[8], n = 1;
+    os[ndim - 1] = 1;
+    is[ndim - 1] = 1;
+    for (int i = ndim - 2; i >= 0; i--) {
+        os[i] = os[i + 1] * out_dims[i + 1];
+        is[i] = is[i + 1] * in_dims[i + 1];
+    }
+    for (int i = 0; i < ndim; i++) n *= out_dims[i];
+    for (uint32_t e = 0; e < n; e++) {
+        uint32_t t = e, off = 0;
+        for (int d = 0; d < ndim; d++) {
+            const uint32_t c = t / os[d];
+            t %= os[d];
+            off += (c % in_dims[d]) * is[d];
+        }
+        memcpy((uint8_t *)Y + (size_t)e * elem_size, (const uint8_t *)X + (size_t)off * elem_size, elem_size);
+    }
+}
+
+/* Cast among float32 (1), int32 (6), int64 (7) (SPINN/run_time/ops/tensor/cast.c:26-72). */
+int oracle_cast(int src, int dst, uint32_t n, const void *X, void *Y) {
+    if (src == dst) {
+        memcpy(Y, X, (size_t)n * (src == 7 ? 8 : 4));
+        return 0;
+    }
+    for (uint32_t i = 0; i < n; i++) {
+        if (src == 7 && dst == 1) ((float *)Y)[i] = (float)((const int64_t *)X)[i];
+        else if (src == 6 && dst == 1) ((float *)Y)[i] = (float)((const int32_t *)X)[i];
+        else if (src == 1 && dst == 7) ((int64_t *)Y)[i] = (int64_t)((const float *)X)[i];
+        else if (src == 1 && dst == 6) ((int32_t *)Y)[i] = (int32_t)((const float *)X)[i];
+        else if (src == 7 && dst == 6) ((int32_t *)Y)[i] = (int32_t)((const int64_t *)X)[i];
+        else if (src == 6 && dst == 7) ((int64_t *)Y)[i] = (int64_t)((const int32_t *)X)[i];
+        else return -2;
+    }
+    return 0;
+}
+
+/* Div (op 3) and Mod (op 4) on int32 / int64 with the modulo broadcast, 0 where
+ * the divisor is 0 (SPINN/run_time/ops/math/div.c:33-48, mod.c:28-45); Mod on
+ * float is fmodf (mod.c:18-27). */
+int oracle_binary_typed(int op, int dtype, const void *a, uint32_t na, const void *b, uint32_t nb, void *y,
+                        uint32_t n) {
+    for (uint32_t i = 0; i < n; i++) {
+        if (dtype == 7) {
+            const int64_t va = ((const int64_t *)a)[i % na], vb = ((const int64_t *)b)[i % nb];
+            ((int64_t *)y)[i] = vb != 0 ? (op == 3 ? va / vb : va % vb) : 0;
+        } else if (dtype == 6) {
+            const int32_t va = ((const int32_t *)a)[i % na], vb = ((const int32_t *)b)[i % nb];
+            ((int32_t *)y)[i] = vb != 0 ? (op == 3 ? va / vb : va % vb) : 0;
+        } else if (dtype == 1 && op == 4) {
+            ((float *)y)[i] = fmodf(((const float *)a)[i % na], ((const float *)b)[i % nb]);
+        } else {
+            return -2;
+        }
+    }
+    return 0;
+}
+
 int oracle_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

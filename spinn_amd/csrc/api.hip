@@ -237,6 +237,75 @@ int spinn_hip_resize_nearest(int64_t nc, int32_t h, int32_t w, int32_t oh, int32
     return resize_nearest(nc, h, w, oh, ow, x, y, (hipStream_t)stream);
 }
 
+int spinn_hip_reduce_max(int64_t rows, int64_t block, const float *x, float *y, void *stream) {
+    if (rows < 0 || block < 0) return SPINN_HIP_EINVAL;
+    if (rows == 0) return SPINN_HIP_OK;
+    if (!x || !y || block == 0 || rows > (int64_t)UINT32_MAX * 4) return SPINN_HIP_EINVAL;
+    return reduce_max_rows(rows, block, x, y, (hipStream_t)stream);
+}
+
+int spinn_hip_topk(int64_t rows, int64_t n, int64_t k, const float *x, float *values, int64_t *indices,
+                   void *stream) {
+    if (rows < 0 || n < 0 || k < 0) return SPINN_HIP_EINVAL;
+    if (rows == 0 || k == 0) return SPINN_HIP_OK;
+    if (k > n || n >= (int64_t)INT32_MAX || rows > (int64_t)UINT32_MAX) return SPINN_HIP_EINVAL;
+    if (k > SPINN_HIP_TOPK_MAX_K) return SPINN_HIP_EUNSUPPORTED;
+    if (!x || !values || !indices) return SPINN_HIP_EINVAL;
+    return topk_rows(rows, n, (int)k, x, values, indices, (hipStream_t)stream);
+}
+
+int spinn_hip_gather_elements(const SpinnHipGatherDesc *d, const float *data, const void *indices, float *y,
+                              void *stream) {
+    if (!d || d->ndim < 1 || d->ndim > 8 || d->axis < 0 || d->axis >= d->ndim) return SPINN_HIP_EINVAL;
+    if (d->index_dtype != ENNF_TYPE_INT64 && d->index_dtype != ENNF_TYPE_INT32) return SPINN_HIP_EINVAL;
+    int64_t total = 1;
+    for (int i = 0; i < d->ndim; ++i) {
+        if (d->in_dims[i] < 0 || d->out_dims[i] < 0) return SPINN_HIP_EINVAL;
+        // outside the gathered axis the indices may not reach past the data (ONNX rule)
+        if (i != d->axis && d->out_dims[i] > d->in_dims[i]) return SPINN_HIP_EINVAL;
+        total *= d->out_dims[i];
+    }
+    if (total == 0) return SPINN_HIP_OK;
+    if (d->in_dims[d->axis] == 0 || !data || !indices || !y) return SPINN_HIP_EINVAL;
+    return gather_elements(d, data, indices, y, (hipStream_t)stream);
+}
+
+int spinn_hip_tile(int ndim, const int64_t *in_dims, const int64_t *out_dims, int elem_bytes, const void *x,
+                   void *y, void *stream) {
+    if (ndim < 1 || ndim > 8 || !in_dims || !out_dims) return SPINN_HIP_EINVAL;
+    if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return SPINN_HIP_EINVAL;
+    int64_t total = 1;
+    for (int i = 0; i < ndim; ++i) {
+        if (in_dims[i] < 0 || out_dims[i] < 0) return SPINN_HIP_EINVAL;
+        if (out_dims[i] > 0 && in_dims[i] == 0) return SPINN_HIP_EINVAL;
+        total *= out_dims[i];
+    }
+    if (total == 0) return SPINN_HIP_OK;
+    if (!x || !y) return SPINN_HIP_EINVAL;
+    return tile(ndim, in_dims, out_dims, elem_bytes, x, y, (hipStream_t)stream);
+}
+
+int spinn_hip_cast(int src_dtype, int dst_dtype, int64_t n, const void *x, void *y, void *stream) {
+    auto known = [](int t) { return t == ENNF_TYPE_FLOAT32 || t == ENNF_TYPE_INT32 || t == ENNF_TYPE_INT64; };
+    if (n < 0) return SPINN_HIP_EINVAL;
+    if (!known(src_dtype) || !known(dst_dtype)) return SPINN_HIP_EUNSUPPORTED;
+    if (n == 0) return SPINN_HIP_OK;
+    if (!x || !y) return SPINN_HIP_EINVAL;
+    return cast(src_dtype, dst_dtype, n, x, y, (hipStream_t)stream);
+}
+
+int spinn_hip_binary_typed(int op, int dtype, const void *a, int64_t na, const void *b, int64_t nb, void *y,
+                           int64_t n, void *stream) {
+    constexpr int64_t kMax = (int64_t)UINT32_MAX;
+    if (op < SPINN_BINARY_ADD || op > SPINN_BINARY_MOD || n < 0 || n > kMax || na > kMax || nb > kMax)
+        return SPINN_HIP_EINVAL;
+    if (dtype != ENNF_TYPE_FLOAT32 && dtype != ENNF_TYPE_INT32 && dtype != ENNF_TYPE_INT64)
+        return SPINN_HIP_EUNSUPPORTED;
+    if (n == 0) return SPINN_HIP_OK;
+    if (!a || !b || !y || na <= 0 || nb <= 0) return SPINN_HIP_EINVAL;
+    return binary_typed(op, dtype, a, na, b, nb, y, n, (hipStream_t)stream);
+}
+
 int spinn_hip_init(int device) { return hip_code(hipSetDevice(device)); }
 
 int spinn_hip_device_count(int *count) {

@@ -370,8 +370,9 @@ int op_reduce_mean(SpinnTensor **in, int n_in, void *params, uint16_t params_siz
     return spinn_hip_reduce_mean(outer, dim, inner, (const float *)X->data, (float *)Y->data, g_spinn_exec.stream);
 }
 
-/* Reshape / Flatten / Identity: a copy unless the tensors alias
- * (SPINN/run_time/ops/shape/reshape.c:6-14, ops/tensor/flatten.c:3-8). */
+/* Reshape / Flatten / Identity / Unsqueeze: a copy unless the tensors alias
+ * (SPINN/run_time/ops/shape/reshape.c:6-14, ops/tensor/flatten.c:3-8,
+ * ops/tensor/unsqueeze.c:3-8). */
 int op_copy_alias(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
     (void)params;
     (void)params_size;
@@ -415,15 +416,30 @@ int op_mul(SpinnTensor **in, int n_in, void *params, uint16_t params_size, Spinn
     return binary_node(SPINN_BINARY_MUL, in, n_in, out, n_out);
 }
 
-/* Div: fp32 only here (the reference also divides int32/int64 tensors,
- * div.c:31-48, which the conv path never produces); an empty operand is a no-op. */
+/* Div / Mod on the dtype of the first input: fp32, int32 or int64, with the
+ * reference's modulo broadcast; an empty operand is a no-op
+ * (SPINN/run_time/ops/math/div.c:5-52, mod.c:5-50). */
+static int typed_binary_node(int op, SpinnTensor **in, int n_in, SpinnTensor **out, int n_out) {
+    if (n_in < 2 || n_out < 1) return -1;
+    if (in[0]->elem_count == 0 || in[1]->elem_count == 0) return 0;
+    const int dt = in[0]->dtype;
+    if (dt != ENNF_TYPE_FLOAT32 && dt != ENNF_TYPE_INT32 && dt != ENNF_TYPE_INT64) return SPINN_HIP_EUNSUPPORTED;
+    if (in[1]->dtype != dt || out[0]->dtype != dt) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_binary_typed(op, dt, in[0]->data, in[0]->elem_count, in[1]->data, in[1]->elem_count,
+                                  out[0]->data, out[0]->elem_count, g_spinn_exec.stream);
+}
+
 int op_div(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
     (void)params;
     (void)params_size;
-    if (n_in < 2 || n_out < 1) return -1;
-    if (in[0]->elem_count == 0 || in[1]->elem_count == 0) return 0;
-    if (in[0]->dtype != ENNF_TYPE_FLOAT32) return SPINN_HIP_EUNSUPPORTED;
-    return binary_node(SPINN_BINARY_DIV, in, n_in, out, n_out);
+    return typed_binary_node(SPINN_BINARY_DIV, in, n_in, out, n_out);
+}
+
+int op_mod(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    return typed_binary_node(SPINN_BINARY_MOD, in, n_in, out, n_out);
 }
 
 static int unary_node(int op, SpinnTensor **in, int n_in, SpinnTensor **out, int n_out) {
@@ -589,6 +605,98 @@ int op_resize(SpinnTensor **in, int n_in, void *params, uint16_t params_size, Sp
 }
 
 /* ------------------------------------------------------------------------
+ * Detector post-processing: the exported YOLOv10 tail after the decoded head
+ * (max class score, TopK anchors, gathers, TopK over anchor x class, label and
+ * anchor from the flat index).
+ * ---------------------------------------------------------------------- */
+
+/* ReduceMax over blocks of |X| / |Y| consecutive elements, whatever the axes
+ * parameter says (SPINN/run_time/ops/reduce/reduce_max.c:12-26). */
+int op_reduce_max(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 1 || n_out < 1) return -1;
+    if (in[0]->dtype != ENNF_TYPE_FLOAT32) return SPINN_HIP_EUNSUPPORTED;
+    const uint32_t out_n = out[0]->elem_count;
+    if (out_n == 0) return 0;
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_reduce_max(out_n, in[0]->elem_count / out_n, (const float *)in[0]->data,
+                                (float *)out[0]->data, g_spinn_exec.stream);
+}
+
+/* TopK along the last axis, largest first, sorted (SPINN/run_time/ops/tensor/topk.c:20-89).
+ * k is the values output's last dimension: the converter's shape inference writes
+ * min(K, N) there, the value the reference computes from the K input (:28-59). */
+int op_topk(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 2 || n_out < 2) return -1;
+    SpinnTensor *X = in[0], *V = out[0], *I = out[1];
+    if (X->ndim < 1 || V->ndim != X->ndim || X->dtype != ENNF_TYPE_FLOAT32 || I->dtype != ENNF_TYPE_INT64) return -1;
+    const int last = X->ndim - 1;
+    const int64_t n = X->dims[last];
+    const int64_t k = V->dims[last];
+    const int64_t rows = n > 0 ? (int64_t)X->elem_count / n : 0;
+    if (k > n || (int64_t)V->elem_count != rows * k || I->elem_count != V->elem_count) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_topk(rows, n, k, (const float *)X->data, (float *)V->data, (int64_t *)I->data,
+                          g_spinn_exec.stream);
+}
+
+/* GatherElements along `axis` (default 0) (SPINN/run_time/ops/tensor/gather_elements.c:5-76). */
+int op_gather_elements(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out,
+                       int n_out) {
+    if (n_in < 2 || n_out < 1) return -1;
+    SpinnTensor *D = in[0], *Ix = in[1], *Y = out[0];
+    if (D->dtype != ENNF_TYPE_FLOAT32) return SPINN_HIP_EUNSUPPORTED;
+    SpinnHipGatherDesc d;
+    memset(&d, 0, sizeof(d));
+    d.ndim = D->ndim;
+    d.axis = 0;
+    if (params && params_size >= sizeof(ENNF_GatherParams)) d.axis = ((const ENNF_GatherParams *)params)->axis;
+    if (d.axis < 0) d.axis += d.ndim;
+    d.index_dtype = Ix->dtype == ENNF_TYPE_INT64 ? ENNF_TYPE_INT64 : ENNF_TYPE_INT32;
+    if (Y->ndim != D->ndim || Ix->elem_count != Y->elem_count) return -1;
+    for (int i = 0; i < d.ndim && i < 8; i++) {
+        d.in_dims[i] = D->dims[i];
+        d.out_dims[i] = Y->dims[i];
+    }
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_gather_elements(&d, (const float *)D->data, Ix->data, (float *)Y->data, g_spinn_exec.stream);
+}
+
+/* Tile: output coordinate c reads input coordinate c mod dims; the repeats
+ * input only shapes the output (SPINN/run_time/ops/tensor/tile.c:6-65). */
+int op_tile(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 2 || n_out < 1) return -1;
+    SpinnTensor *X = in[0], *Y = out[0];
+    if (X->ndim != Y->ndim || X->ndim < 1 || X->ndim > 8) return -1;
+    int es = 4; /* element size by dtype, as tile.c:18-24 */
+    if (X->dtype == ENNF_TYPE_INT64) es = 8;
+    else if (X->dtype == ENNF_TYPE_UINT8 || X->dtype == ENNF_TYPE_INT8) es = 1;
+    int64_t id[8], od[8];
+    for (int i = 0; i < X->ndim; i++) {
+        id[i] = X->dims[i];
+        od[i] = Y->dims[i];
+    }
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_tile(X->ndim, id, od, es, X->data, Y->data, g_spinn_exec.stream);
+}
+
+/* Cast between the tensors' dtypes (SPINN/run_time/ops/tensor/cast.c:13-73). */
+int op_cast(SpinnTensor **in, int n_in, void *params, uint16_t params_size, SpinnTensor **out, int n_out) {
+    (void)params;
+    (void)params_size;
+    if (n_in < 1 || n_out < 1) return -1;
+    if (in[0]->elem_count < out[0]->elem_count) return -1;
+    if (g_spinn_exec.preparing) return 0;
+    return spinn_hip_cast(in[0]->dtype, out[0]->dtype, out[0]->elem_count, in[0]->data, out[0]->data,
+                          g_spinn_exec.stream);
+}
+
+/* ------------------------------------------------------------------------
  * Registry and dispatcher (SPINN/run_time/spinn_ops.c:17-228)
  * ---------------------------------------------------------------------- */
 static SpinnOpKernel g_op_registry[ENNF_OP_REGISTRY_SIZE];
@@ -617,6 +725,13 @@ static void registry_init(void) {
     g_op_registry[ENNF_OP_Split] = op_split;
     g_op_registry[ENNF_OP_Transpose] = op_transpose;
     g_op_registry[ENNF_OP_Resize] = op_resize;
+    g_op_registry[ENNF_OP_Mod] = op_mod;
+    g_op_registry[ENNF_OP_ReduceMax] = op_reduce_max;
+    g_op_registry[ENNF_OP_TopK] = op_topk;
+    g_op_registry[ENNF_OP_GatherElements] = op_gather_elements;
+    g_op_registry[ENNF_OP_Tile] = op_tile;
+    g_op_registry[ENNF_OP_Cast] = op_cast;
+    g_op_registry[ENNF_OP_Unsqueeze] = op_copy_alias;
     g_registry_ready = 1;
 }
 

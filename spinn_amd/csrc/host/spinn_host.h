@@ -55,6 +55,12 @@ SPINN_DECLARE_OP(op_concat);
 SPINN_DECLARE_OP(op_split);
 SPINN_DECLARE_OP(op_transpose);
 SPINN_DECLARE_OP(op_resize);
+SPINN_DECLARE_OP(op_mod);
+SPINN_DECLARE_OP(op_reduce_max);
+SPINN_DECLARE_OP(op_topk);
+SPINN_DECLARE_OP(op_gather_elements);
+SPINN_DECLARE_OP(op_tile);
+SPINN_DECLARE_OP(op_cast);
 
 /* Build the conv descriptor exactly as op_conv2d reads its operands. */
 int spinn_conv_desc_from_tensors(SpinnTensor **in, int n_in, const void *params, uint16_t params_size,

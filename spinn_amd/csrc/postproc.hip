@@ -1,0 +1,361 @@
+// postproc.hip - detector post-processing operators: ReduceMax, TopK,
+// GatherElements, Tile, Cast and the integer forms of Div / Mod.
+//
+// These close the YOLOv10n graph after the decoded head (the exported
+// v10 post-process: max class score per anchor, TopK 300 anchors, gather of
+// their boxes and scores, TopK 300 over anchor x class, label = index mod nc,
+// anchor = index / nc, final gather). All of them are small and latency-bound;
+// each is one launch with coalesced loads where the layout allows.
+#include "spinn_hip_internal.h"
+
+namespace spinn {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// ReduceMax over contiguous blocks (SPINN/run_time/ops/reduce/reduce_max.c:18-26).
+// One wave per row: lanes read consecutive elements, then a shuffle tree keeps
+// (value, index) with "strictly greater wins, equal values keep the lower
+// index", which for NaN-free rows returns exactly the element the reference's
+// in-order scan ends on (the first maximal one, -0.0 and +0.0 being equal).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void reduce_max_rows_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                              int64_t rows, int64_t block) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * block;
+    float best = 0.f;
+    int64_t bi = -1;
+    for (int64_t j = lane; j < block; j += 64) {
+        const float v = xr[j];
+        if (bi < 0 || v > best) {
+            best = v;
+            bi = j;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int64_t oi = __shfl_xor(bi, off);
+        const bool take = oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi));
+        if (take) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) y[row] = xr[bi]; // the element itself (keeps the sign of a zero)
+}
+
+// ---------------------------------------------------------------------------
+// TopK (SPINN/run_time/ops/tensor/topk.c:20-89), one 1024-thread workgroup per row.
+// Order: value descending, ties by ascending index - what the reference's stable
+// qsort of (value, index) pairs under `a > b` produces for NaN-free rows.
+//   1. radix select of the k-th largest order key, 8 bits per pass, LDS histogram;
+//   2. compaction of the k winners: every key above the threshold, and the
+//      lowest-index elements equal to it (block-wide prefix count in index order);
+//   3. bitonic sort of the winners by (key desc, index asc) in LDS.
+// ---------------------------------------------------------------------------
+constexpr int kTopkThreads = 1024;
+
+__device__ __forceinline__ uint32_t order_key(float v) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7fffffffu) == 0u) u = 0u;               // -0.0 == +0.0
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0u;    // NaN: below everything
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u); // larger float -> larger key
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__restrict__ x, int64_t n, int k,
+                                                                 float *__restrict__ values,
+                                                                 int64_t *__restrict__ indices) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_prefix, s_mask, s_need;
+    __shared__ uint32_t s_gt, s_eq_base;
+    __shared__ uint32_t s_wave_eq[kTopkThreads / 64];
+    __shared__ uint64_t cand[SPINN_HIP_TOPK_MAX_K];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const float *xr = x + (int64_t)blockIdx.x * n;
+
+    if (tid == 0) {
+        s_prefix = 0u;
+        s_mask = 0u;
+        s_need = (uint32_t)k;
+    }
+    // 1. radix select, most significant digit first
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = tid; b < 256; b += kTopkThreads) hist[b] = 0u;
+        __syncthreads();
+        const uint32_t prefix = s_prefix, mask = s_mask;
+        for (int64_t i = tid; i < n; i += kTopkThreads) {
+            const uint32_t key = order_key(xr[i]);
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            // walk the digits from the top until the remaining count is covered
+            uint32_t need = s_need, above = 0u;
+            int d = 255;
+            for (; d > 0; --d) {
+                if (above + hist[d] >= need) break;
+                above += hist[d];
+            }
+            s_need = need - above;
+            s_prefix = prefix | ((uint32_t)d << shift);
+            s_mask = mask | (255u << shift);
+        }
+        __syncthreads();
+    }
+    const uint32_t thr = s_prefix;     // key of the k-th largest element
+    const uint32_t take_eq = s_need;   // how many elements equal to it are kept
+    const uint32_t n_gt = (uint32_t)k - take_eq;
+    if (tid == 0) {
+        s_gt = 0u;
+        s_eq_base = 0u;
+    }
+    __syncthreads();
+
+    // 2. compaction in index order
+    for (int64_t base = 0; base < n; base += kTopkThreads) {
+        const int64_t i = base + tid;
+        uint32_t key = 0u;
+        bool gt = false, eq = false;
+        if (i < n) {
+            key = order_key(xr[i]);
+            gt = key > thr;
+            eq = key == thr;
+        }
+        const uint64_t ball = __ballot(eq);
+        const uint32_t below = (uint32_t)__popcll(ball & ((1ull << lane) - 1ull));
+        if (lane == 0) s_wave_eq[wave] = (uint32_t)__popcll(ball);
+        __syncthreads();
+        uint32_t rank = s_eq_base + below;
+        for (int w = 0; w < wave; ++w) rank += s_wave_eq[w];
+        const uint64_t packed = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+        if (gt) {
+            const uint32_t slot = atomicAdd(&s_gt, 1u); // < n_gt by construction of thr
+            if (slot < n_gt) cand[slot] = packed;
+        } else if (eq && rank < take_eq) {
+            cand[n_gt + rank] = packed;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t t = 0u;
+            for (int w = 0; w < kTopkThreads / 64; ++w) t += s_wave_eq[w];
+            s_eq_base += t;
+        }
+        __syncthreads();
+    }
+
+    // 3. bitonic sort, descending, over the next power of two >= k (pads sort last)
+    int p2 = 1;
+    while (p2 < k) p2 <<= 1;
+    for (int i = k + tid; i < p2; i += kTopkThreads) cand[i] = 0ull;
+    __syncthreads();
+    for (int size = 2; size <= p2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < p2; i += kTopkThreads) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;
+                    const uint64_t a = cand[i], b = cand[j];
+                    if (desc ? (a < b) : (a > b)) {
+                        cand[i] = b;
+                        cand[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int j = tid; j < k; j += kTopkThreads) {
+        const uint32_t i = 0xffffffffu - (uint32_t)cand[j];
+        values[(int64_t)blockIdx.x * k + j] = xr[i];
+        indices[(int64_t)blockIdx.x * k + j] = (int64_t)i;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GatherElements (SPINN/run_time/ops/tensor/gather_elements.c:36-73), one thread
+// per output element.
+// ---------------------------------------------------------------------------
+struct GatherGeom {
+    int ndim, axis;
+    int64_t out_dims[8];
+    int64_t in_strides[8];
+    int64_t axis_dim;
+};
+
+template <typename IT>
+__global__ __launch_bounds__(256) void gather_elements_kernel(const float *__restrict__ data,
+                                                              const IT *__restrict__ idx, float *__restrict__ y,
+                                                              int64_t total, GatherGeom g) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        int64_t gi = (int64_t)idx[e];
+        if (gi < 0) gi += g.axis_dim;
+        if (gi < 0 || gi >= g.axis_dim) gi = 0;
+        int64_t rem = e, off = 0;
+        for (int d = g.ndim - 1; d >= 0; --d) {
+            const int64_t c = rem % g.out_dims[d];
+            rem /= g.out_dims[d];
+            off += (d == g.axis ? gi : c) * g.in_strides[d];
+        }
+        y[e] = data[off];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Tile (SPINN/run_time/ops/tensor/tile.c:45-62), one thread per output element.
+// ---------------------------------------------------------------------------
+struct TileGeom {
+    int ndim;
+    int64_t in_dims[8];
+    int64_t out_dims[8];
+    int64_t in_strides[8];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void tile_kernel(const T *__restrict__ x, T *__restrict__ y, int64_t total,
+                                                   TileGeom g) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        int64_t rem = e, off = 0;
+        for (int d = g.ndim - 1; d >= 0; --d) {
+            const int64_t c = rem % g.out_dims[d];
+            rem /= g.out_dims[d];
+            off += (c % g.in_dims[d]) * g.in_strides[d];
+        }
+        y[e] = x[off];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Cast (SPINN/run_time/ops/tensor/cast.c:31-66) and integer Div / Mod
+// (SPINN/run_time/ops/math/div.c:33-48, mod.c:18-45).
+// ---------------------------------------------------------------------------
+template <typename S, typename D>
+__global__ __launch_bounds__(256) void cast_kernel(const S *__restrict__ x, D *__restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = (D)x[i];
+}
+
+template <typename T, int OP>
+__global__ __launch_bounds__(256) void binary_int_kernel(const T *__restrict__ a, int64_t na, const T *__restrict__ b,
+                                                         int64_t nb, T *__restrict__ y, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const T va = a[i % na], vb = b[i % nb];
+        y[i] = vb != 0 ? (OP == SPINN_BINARY_DIV ? (T)(va / vb) : (T)(va % vb)) : (T)0;
+    }
+}
+
+__global__ __launch_bounds__(256) void fmod_kernel(const float *__restrict__ a, int64_t na,
+                                                   const float *__restrict__ b, int64_t nb, float *__restrict__ y,
+                                                   int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = fmodf(a[i % na], b[i % nb]);
+}
+
+int grid_for(int64_t n) { return (int)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 65536)); }
+
+} // namespace
+
+int reduce_max_rows(int64_t rows, int64_t block, const float *x, float *y, hipStream_t st) {
+    hipLaunchKernelGGL(reduce_max_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, y, rows, block);
+    return check_launch();
+}
+
+int topk_rows(int64_t rows, int64_t n, int k, const float *x, float *values, int64_t *indices, hipStream_t st) {
+    hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, x, n, k, values, indices);
+    return check_launch();
+}
+
+int gather_elements(const SpinnHipGatherDesc *d, const float *data, const void *indices, float *y, hipStream_t st) {
+    GatherGeom g{};
+    g.ndim = d->ndim;
+    g.axis = d->axis;
+    g.axis_dim = d->in_dims[d->axis];
+    int64_t total = 1, stride = 1;
+    for (int i = d->ndim - 1; i >= 0; --i) {
+        g.out_dims[i] = d->out_dims[i];
+        g.in_strides[i] = stride;
+        stride *= d->in_dims[i];
+        total *= d->out_dims[i];
+    }
+    if (d->index_dtype == ENNF_TYPE_INT64)
+        hipLaunchKernelGGL(gather_elements_kernel<int64_t>, dim3(grid_for(total)), dim3(256), 0, st, data,
+                           (const int64_t *)indices, y, total, g);
+    else
+        hipLaunchKernelGGL(gather_elements_kernel<int32_t>, dim3(grid_for(total)), dim3(256), 0, st, data,
+                           (const int32_t *)indices, y, total, g);
+    return check_launch();
+}
+
+int tile(int ndim, const int64_t *in_dims, const int64_t *out_dims, int elem_bytes, const void *x, void *y,
+         hipStream_t st) {
+    TileGeom g{};
+    g.ndim = ndim;
+    int64_t total = 1, stride = 1;
+    for (int i = ndim - 1; i >= 0; --i) {
+        g.in_dims[i] = in_dims[i];
+        g.out_dims[i] = out_dims[i];
+        g.in_strides[i] = stride;
+        stride *= in_dims[i];
+        total *= out_dims[i];
+    }
+    const dim3 grid(grid_for(total)), blk(256);
+    switch (elem_bytes) {
+    case 1: hipLaunchKernelGGL(tile_kernel<uint8_t>, grid, blk, 0, st, (const uint8_t *)x, (uint8_t *)y, total, g); break;
+    case 2: hipLaunchKernelGGL(tile_kernel<uint16_t>, grid, blk, 0, st, (const uint16_t *)x, (uint16_t *)y, total, g); break;
+    case 4: hipLaunchKernelGGL(tile_kernel<uint32_t>, grid, blk, 0, st, (const uint32_t *)x, (uint32_t *)y, total, g); break;
+    default: hipLaunchKernelGGL(tile_kernel<uint64_t>, grid, blk, 0, st, (const uint64_t *)x, (uint64_t *)y, total, g); break;
+    }
+    return check_launch();
+}
+
+int cast(int src, int dst, int64_t n, const void *x, void *y, hipStream_t st) {
+    const dim3 grid(grid_for(n)), blk(256);
+    const int F = ENNF_TYPE_FLOAT32, I32 = ENNF_TYPE_INT32, I64 = ENNF_TYPE_INT64;
+    if (src == dst) {
+        const size_t bytes = (size_t)n * (src == I64 ? 8 : 4);
+        return x == y ? 0 : hip_code(hipMemcpyAsync(y, x, bytes, hipMemcpyDeviceToDevice, st));
+    }
+    if (src == I64 && dst == F) hipLaunchKernelGGL((cast_kernel<int64_t, float>), grid, blk, 0, st, (const int64_t *)x, (float *)y, n);
+    else if (src == I32 && dst == F) hipLaunchKernelGGL((cast_kernel<int32_t, float>), grid, blk, 0, st, (const int32_t *)x, (float *)y, n);
+    else if (src == F && dst == I64) hipLaunchKernelGGL((cast_kernel<float, int64_t>), grid, blk, 0, st, (const float *)x, (int64_t *)y, n);
+    else if (src == F && dst == I32) hipLaunchKernelGGL((cast_kernel<float, int32_t>), grid, blk, 0, st, (const float *)x, (int32_t *)y, n);
+    else if (src == I64 && dst == I32) hipLaunchKernelGGL((cast_kernel<int64_t, int32_t>), grid, blk, 0, st, (const int64_t *)x, (int32_t *)y, n);
+    else if (src == I32 && dst == I64) hipLaunchKernelGGL((cast_kernel<int32_t, int64_t>), grid, blk, 0, st, (const int32_t *)x, (int64_t *)y, n);
+    else return SPINN_HIP_EUNSUPPORTED;
+    return check_launch();
+}
+
+int binary_typed(int op, int dtype, const void *a, int64_t na, const void *b, int64_t nb, void *y, int64_t n,
+                 hipStream_t st) {
+    const dim3 grid(grid_for(n)), blk(256);
+    if (dtype == ENNF_TYPE_FLOAT32) {
+        if (op == SPINN_BINARY_MOD) {
+            hipLaunchKernelGGL(fmod_kernel, grid, blk, 0, st, (const float *)a, na, (const float *)b, nb, (float *)y, n);
+            return check_launch();
+        }
+        return binary_op(op, (const float *)a, na, (const float *)b, nb, (float *)y, n, st);
+    }
+    if (op != SPINN_BINARY_DIV && op != SPINN_BINARY_MOD) return SPINN_HIP_EUNSUPPORTED;
+    if (dtype == ENNF_TYPE_INT64) {
+        if (op == SPINN_BINARY_DIV)
+            hipLaunchKernelGGL((binary_int_kernel<int64_t, SPINN_BINARY_DIV>), grid, blk, 0, st, (const int64_t *)a, na, (const int64_t *)b, nb, (int64_t *)y, n);
+        else
+            hipLaunchKernelGGL((binary_int_kernel<int64_t, SPINN_BINARY_MOD>), grid, blk, 0, st, (const int64_t *)a, na, (const int64_t *)b, nb, (int64_t *)y, n);
+    } else if (dtype == ENNF_TYPE_INT32) {
+        if (op == SPINN_BINARY_DIV)
+            hipLaunchKernelGGL((binary_int_kernel<int32_t, SPINN_BINARY_DIV>), grid, blk, 0, st, (const int32_t *)a, na, (const int32_t *)b, nb, (int32_t *)y, n);
+        else
+            hipLaunchKernelGGL((binary_int_kernel<int32_t, SPINN_BINARY_MOD>), grid, blk, 0, st, (const int32_t *)a, na, (const int32_t *)b, nb, (int32_t *)y, n);
+    } else {
+        return SPINN_HIP_EUNSUPPORTED;
+    }
+    return check_launch();
+}
+
+} // namespace spinn

@@ -80,4 +80,14 @@ int block_copy(const SpinnHipBlockCopy *blocks, int n_blocks, int64_t outer, hip
 int transpose(int ndim, const int64_t *dims, const int32_t *perm, const float *x, float *y, hipStream_t st);
 int resize_nearest(int64_t nc, int h, int w, int oh, int ow, const float *x, float *y, hipStream_t st);
 
+// detector post-processing (postproc.hip)
+int reduce_max_rows(int64_t rows, int64_t block, const float *x, float *y, hipStream_t st);
+int topk_rows(int64_t rows, int64_t n, int k, const float *x, float *values, int64_t *indices, hipStream_t st);
+int gather_elements(const SpinnHipGatherDesc *d, const float *data, const void *indices, float *y, hipStream_t st);
+int tile(int ndim, const int64_t *in_dims, const int64_t *out_dims, int elem_bytes, const void *x, void *y,
+         hipStream_t st);
+int cast(int src, int dst, int64_t n, const void *x, void *y, hipStream_t st);
+int binary_typed(int op, int dtype, const void *a, int64_t na, const void *b, int64_t nb, void *y, int64_t n,
+                 hipStream_t st);
+
 } // namespace spinn

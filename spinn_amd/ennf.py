@@ -37,6 +37,7 @@ OP_BN, OP_RELU, OP_SIGMOID, OP_SOFTMAX = 100, 130, 133, 134
 OP_GEMM, OP_MATMUL = 160, 161
 OP_CONCAT, OP_FLATTEN, OP_IDENTITY, OP_RESHAPE = 183, 189, 193, 197
 OP_RESIZE, OP_SPLIT, OP_TRANSPOSE, OP_REDUCEMEAN = 198, 206, 211, 235
+OP_MOD, OP_CAST, OP_GATHER_ELEMENTS, OP_TILE, OP_TOPK, OP_UNSQUEEZE, OP_REDUCEMAX = 38, 180, 191, 209, 210, 214, 234
 
 ACT_NONE, ACT_RELU, ACT_CLIP, ACT_SILU, ACT_ADD, ACT_ADD_RELU = 0, 1, 2, 3, 4, 5
 NODE_FLAG_FUSED = 1
@@ -92,6 +93,21 @@ def reduce_params(axes, keepdims: int = 1) -> bytes:
     """ENNF_ReduceParams (36 B)."""
     a = list(axes) + [0] * (8 - len(axes))
     return struct.pack("<8iBBBB", *a, len(axes), keepdims, 0, 0)
+
+
+def topk_params(axis: int = -1, largest: int = 1, sorted_: int = 1) -> bytes:
+    """ENNF_TopKParams (8 B); K travels as the int64 second input."""
+    return struct.pack("<iBB2x", axis, largest, sorted_)
+
+
+def gather_params(axis: int) -> bytes:
+    """ENNF_GatherParams (8 B): axis, batch_dims."""
+    return struct.pack("<ii", axis, 0)
+
+
+def cast_params(to_type: int) -> bytes:
+    """ENNF_CastParams (4 B)."""
+    return struct.pack("<BB2x", to_type, 0)
 
 
 @dataclass

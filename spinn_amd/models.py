@@ -194,7 +194,8 @@ def _plain_conv(g: E.Graph, rng, name: str, x: int, oc: int, k: int = 1, bias: b
     return y
 
 
-def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80):
+def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postprocess: bool = False,
+             max_det: int = 300):
     """YOLOv10n (width 0.25, depth 0.33; ultralytics yolov10n.yaml) as the
     converter + graph optimizer would emit the exported detector, up to the
     one-to-one head's decoded output [B, 4 + nc, anchors] (boxes x1y1x2y2 in
@@ -384,9 +385,73 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80):
     x2y2 = binary(E.OP_ADD, "model.23.x2y2", anchors, rb)
     dbox = binary(E.OP_MUL, "model.23.dbox", concat("model.23.xyxy", [x1y1, x2y2]), strides)
     y = concat("model.23.out", [dbox, sig])
+    if postprocess:
+        y = _v10_postprocess(g, y, batch, na, nc, max_det, nm, split, transpose, concat)
     g.output(y)
     xin = np.random.default_rng(seed + 1).uniform(0.0, 1.0, (batch, 3, hw, hw)).astype(np.float32)
     return g, xin
+
+
+def _v10_postprocess(g: E.Graph, y: int, batch: int, na: int, nc: int, max_det: int, nm, split, transpose,
+                     concat) -> int:
+    """The exported one-to-one post-process after the decoded head [B, 4 + nc, A]:
+    per-anchor best score, TopK anchors, gather of their boxes and class scores,
+    TopK over anchor x class, label = index mod nc, anchor = index / nc, final
+    box gather; output [B, k, 6] = (x1, y1, x2, y2, score, label). The node
+    sequence is the one the ONNX export carries (Transpose, Split, ReduceMax, TopK,
+    Unsqueeze, Tile, GatherElements, Flatten, TopK, Mod, Div, Cast, Concat)."""
+    i64 = E.DT_INT64
+    pre = "model.23.post"
+    yt = transpose(f"{pre}.t", y, (0, 2, 1))                       # [B, A, 4 + nc]
+    boxes, scores = split(f"{pre}.split", yt, [4, nc], axis=2)
+    best = g.tensor(f"{pre}.max", (batch, na))
+    g.node(E.OP_REDUCEMAX, [scores], [best], E.reduce_params([-1], keepdims=0))
+    k1 = min(max_det, na)
+    kt = g.weight(nm(f"{pre}.k"), np.array([max_det], np.int64), i64)
+
+    def topk(name, t, k):
+        v = g.tensor(f"{name}.values", g.dims(t)[:-1] + (k,))
+        ix = g.tensor(f"{name}.indices", g.dims(t)[:-1] + (k,), i64)
+        g.node(E.OP_TOPK, [t, kt], [v, ix], E.topk_params(-1, 1, 1))
+        return v, ix
+
+    def unsqueeze(name, t):
+        u = g.tensor(f"{name}.out", g.dims(t) + (1,), g.tensors[t].dtype)
+        g.node(E.OP_UNSQUEEZE, [t, g.weight(nm(f"{name}.axes"), np.array([-1], np.int64), i64)], [u])
+        return u
+
+    def tile(name, t, reps):
+        d = g.dims(t)
+        u = g.tensor(f"{name}.out", tuple(a * r for a, r in zip(d, reps)), g.tensors[t].dtype)
+        g.node(E.OP_TILE, [t, g.weight(nm(f"{name}.repeats"), np.array(reps, np.int64), i64)], [u])
+        return u
+
+    def gather(name, data, idx):
+        u = g.tensor(f"{name}.out", g.dims(idx))
+        g.node(E.OP_GATHER_ELEMENTS, [data, idx], [u], E.gather_params(1))
+        return u
+
+    def int_op(op, name, t, divisor):
+        u = g.tensor(f"{name}.out", g.dims(t), i64)
+        g.node(op, [t, divisor], [u])
+        return u
+
+    _, i1 = topk(f"{pre}.topk0", best, k1)
+    i1u = unsqueeze(f"{pre}.unsq0", i1)
+    boxes1 = gather(f"{pre}.gather0", boxes, tile(f"{pre}.tile0", i1u, (1, 1, 4)))
+    scores1 = gather(f"{pre}.gather1", scores, tile(f"{pre}.tile1", i1u, (1, 1, nc)))
+    flat = g.tensor(f"{pre}.flat", (batch, k1 * nc))
+    g.node(E.OP_FLATTEN, [scores1], [flat], E.axis_params(1))
+    k2 = min(max_det, k1 * nc)
+    s2, i2 = topk(f"{pre}.topk1", flat, k2)
+    ncw = g.weight(nm(f"{pre}.nc"), np.array(nc, np.int64), i64)
+    labels = int_op(E.OP_MOD, f"{pre}.mod", i2, ncw)
+    anchor = int_op(E.OP_DIV, f"{pre}.div", i2, ncw)
+    lab = unsqueeze(f"{pre}.unsq1", labels)
+    labf = g.tensor(f"{pre}.cast.out", g.dims(lab))
+    g.node(E.OP_CAST, [lab], [labf], E.cast_params(E.DT_FLOAT32))
+    boxes2 = gather(f"{pre}.gather2", boxes1, tile(f"{pre}.tile2", unsqueeze(f"{pre}.unsq2", anchor), (1, 1, 4)))
+    return concat(f"{pre}.out", [boxes2, unsqueeze(f"{pre}.unsq3", s2), labf], axis=2)
 
 
 def conv_flops(g: E.Graph) -> list:

@@ -29,7 +29,8 @@ ALGO_AUTO, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_DIRECT = 0, 1, 2, 3
 ACT_NONE, ACT_RELU, ACT_CLIP, ACT_SILU, ACT_ADD, ACT_ADD_RELU = 0, 1, 2, 3, 4, 5
 ENNF_MAX_DIMS = 8
 POLICY_AUTO, POLICY_IGEMM, POLICY_WINOGRAD = 0, 1, 2
-BINARY_ADD, BINARY_SUB, BINARY_MUL, BINARY_DIV = 0, 1, 2, 3
+BINARY_ADD, BINARY_SUB, BINARY_MUL, BINARY_DIV, BINARY_MOD = 0, 1, 2, 3, 4
+TOPK_MAX_K = 1024
 UNARY_RELU, UNARY_SIGMOID, UNARY_SILU = 0, 1, 2
 MAX_BLOCKS = 16
 
@@ -53,6 +54,11 @@ class GemmDesc(C.Structure):
 class PoolDesc(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n", "c", "h", "w", "oh", "ow", "kh", "kw", "sh", "sw", "ph", "pw")]
+
+
+class GatherDesc(C.Structure):
+    _fields_ = [("ndim", C.c_int32), ("axis", C.c_int32), ("index_dtype", C.c_int32), ("reserved", C.c_int32),
+                ("in_dims", C.c_int64 * 8), ("out_dims", C.c_int64 * 8)]
 
 
 class BlockCopy(C.Structure):
@@ -140,6 +146,14 @@ _SIGS = {
                                       C.c_void_p, C.c_void_p]),
     "spinn_hip_resize_nearest": (C.c_int, [C.c_int64, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                                            C.c_void_p, C.c_void_p]),
+    "spinn_hip_reduce_max": (C.c_int, [C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "spinn_hip_topk": (C.c_int, [C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "spinn_hip_gather_elements": (C.c_int, [C.POINTER(GatherDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "spinn_hip_tile": (C.c_int, [C.c_int, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.c_int, C.c_void_p,
+                                 C.c_void_p, C.c_void_p]),
+    "spinn_hip_cast": (C.c_int, [C.c_int, C.c_int, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "spinn_hip_binary_typed": (C.c_int, [C.c_int, C.c_int, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p,
+                                         C.c_int64, C.c_void_p]),
     "spinn_hip_init": (C.c_int, [C.c_int]),
     "spinn_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "spinn_hip_malloc": (C.c_int, [C.POINTER(C.c_void_p), C.c_size_t]),

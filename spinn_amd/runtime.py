@@ -77,8 +77,10 @@ class Session:
         x = np.ascontiguousarray(x, np.float32)
         N.check(self.L.spinn_tensor_upload(self.ctx, self.input_id, x.ctypes.data, x.nbytes), "upload")
 
+    _NP = {1: np.float32, 6: np.int32, 7: np.int64}
+
     def download(self, tid: int) -> np.ndarray:
-        y = np.empty(self.dims(tid), np.float32)
+        y = np.empty(self.dims(tid), self._NP.get(self.tensor(tid).dtype, np.float32))
         N.check(self.L.spinn_tensor_download(self.ctx, tid, y.ctypes.data, y.nbytes), "download")
         return y
 

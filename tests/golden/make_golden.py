@@ -5,7 +5,7 @@ with oracle/Makefile (the reference's run_time C sources compiled in place) and
 calls the reference functions on small seeded inputs. Each fixture is an .npz
 of inputs and the reference's outputs (no code), loaded with allow_pickle=False.
 
-    python tests/golden/make_golden.py [planner conv epilogue gemm winograd tensor_ops models]
+    python tests/golden/make_golden.py [planner conv epilogue gemm winograd tensor_ops postproc models]
 
 Fixtures:
   planner_offsets.npz   spinn_load + spinn_plan_memory offsets and peak for
@@ -21,6 +21,9 @@ Fixtures:
   tensor_ops.npz        op_add / op_sub / op_mul / op_div (modulo broadcast), op_relu, op_sigmoid,
                         op_batch_norm, op_softmax, op_concat, op_split, op_transpose, op_resize and
                         op_maxpool 5x5 s1 p2 on small seeded inputs (the unfused nodes of a detector)
+  postproc.npz          op_reduce_max, op_topk (ties, signed zeros), op_gather_elements, op_tile,
+                        op_cast, op_mod / op_div on int64, int32 and fp32, op_unsqueeze: the
+                        detector's post-processing tail on small seeded inputs
   models_as_shipped.npz spinn_load + spinn_plan + spinn_run of generated models (YOLOv10n at
                         64x64, a 4-block ResNet at 64x64, batch 2): the reference's output and an input fingerprint
 """
@@ -43,6 +46,7 @@ from spinn_amd.native import SpinnTensor, SpinnContext  # noqa: E402  (same stru
 REF_LIB = ROOT / "oracle" / "_ref" / "libspinn_ref.so"
 TENSOR_OPS = ("op_add", "op_sub", "op_mul", "op_div", "op_relu", "op_sigmoid", "op_batch_norm", "op_softmax",
               "op_concat", "op_split", "op_transpose", "op_resize", "op_maxpool")
+POSTPROC_OPS = ("op_reduce_max", "op_topk", "op_gather_elements", "op_tile", "op_cast", "op_mod", "op_unsqueeze")
 FP = C.POINTER(C.c_float)
 
 
@@ -55,7 +59,7 @@ def ref_lib() -> C.CDLL:
     L.spinn_free.argtypes = [C.c_void_p]
     sig = [C.POINTER(C.POINTER(SpinnTensor)), C.c_int, C.c_void_p, C.c_uint16, C.POINTER(C.POINTER(SpinnTensor)),
            C.c_int]
-    for f in ("op_conv2d", "op_gemm", "op_matmul") + TENSOR_OPS:
+    for f in ("op_conv2d", "op_gemm", "op_matmul") + TENSOR_OPS + POSTPROC_OPS:
         getattr(L, f).argtypes = sig
         getattr(L, f).restype = C.c_int
     L.sgemm_nn.argtypes = [C.c_int, C.c_int, C.c_int, FP, C.c_int, FP, C.c_int, FP, C.c_int, FP, C.c_int, FP]
@@ -71,9 +75,12 @@ def _fp(a):
     return None if a is None else a.ctypes.data_as(FP)
 
 
+_ENNF_DT = {np.dtype(np.float32): 1, np.dtype(np.int32): 6, np.dtype(np.int64): 7}
+
+
 def tensor(arr: np.ndarray, keep: list) -> SpinnTensor:
     t = SpinnTensor()
-    t.dtype = 1
+    t.dtype = _ENNF_DT[arr.dtype]
     t.ndim = arr.ndim
     for i, d in enumerate(arr.shape):
         t.dims[i] = d
@@ -241,10 +248,91 @@ def tensor_ops(L):
     np.savez_compressed(HERE / "tensor_ops.npz", **out)
 
 
+def postproc(L):
+    """The detector post-processing operators (the exported YOLOv10 tail) on
+    small seeded inputs: ReduceMax, TopK (with ties and signed zeros), GatherElements
+    (negative and out-of-range indices, int64 and int32), Tile (int64 and fp32),
+    Cast, Mod / Div on int64 and fp32 Mod, Unsqueeze."""
+    import struct
+    rng = np.random.default_rng(2025)
+    out = {}
+
+    def case(name, op, ins, params, outs):
+        ys = [np.zeros(sh, dt) for sh, dt in outs]
+        call_op(L, op, ins, params, ys)
+        for i, a in enumerate(ins):
+            out[f"{name}_in{i}"] = a
+        for i, y in enumerate(ys):
+            out[f"{name}_out{i}"] = y
+        out[f"{name}_params"] = np.frombuffer(params, np.uint8).copy() if params else np.zeros(0, np.uint8)
+
+    f32, i64, i32 = np.float32, np.int64, np.int32
+    # ReduceMax: ties, signed zeros, an all-negative row
+    x = np.round(rng.uniform(-1, 1, (1, 37, 80)), 1).astype(f32)
+    x[0, 0, :] = -0.0
+    x[0, 1, :5] = [0.0, -0.0, 0.0, -0.0, 0.0]
+    x[0, 1, 5:] = -1.0
+    x[0, 2, :] = -np.abs(x[0, 2, :]) - 0.5
+    case("reduce_max_scores", "op_reduce_max", [x], struct.pack("<8iBBBB", -1, *([0] * 7), 1, 0, 0, 0),
+         [((1, 37), f32)])
+    case("reduce_max_rows", "op_reduce_max", [rng.uniform(-3, 3, (5, 9)).astype(f32)], b"", [((5,), f32)])
+    # TopK: two rows, values on a coarse grid so many values tie; +0.0 and -0.0 mixed in
+    tk = np.round(rng.uniform(-1, 1, (2, 700)), 2).astype(f32)
+    tk[0, ::7] = 0.0
+    tk[0, 3::7] = -0.0
+    tk[1, 100:400] = 0.5
+    topk_params = struct.pack("<iBB2x", -1, 1, 1)
+    case("topk_ties", "op_topk", [tk, np.array([300], i64)], topk_params, [((2, 300), f32), ((2, 300), i64)])
+    case("topk_all", "op_topk", [rng.uniform(-1, 1, (1, 50)).astype(f32), np.array([50], i64)], topk_params,
+         [((1, 50), f32), ((1, 50), i64)])
+    case("topk_flat", "op_topk", [rng.uniform(0, 1, (1, 6000)).astype(f32), np.array([300], i64)], topk_params,
+         [((1, 300), f32), ((1, 300), i64)])
+    # GatherElements: the detector's two forms, with negative and out-of-range indices
+    data = rng.uniform(-1, 1, (1, 37, 4)).astype(f32)
+    idx = rng.integers(-37, 37, (1, 10, 4)).astype(i64)
+    idx[0, 0, :] = [40, -40, 36, -1]
+    gparams = lambda a: struct.pack("<ii", a, 0)  # noqa: E731
+    case("gather_boxes", "op_gather_elements", [data, idx], gparams(1), [((1, 10, 4), f32)])
+    data = rng.uniform(-1, 1, (2, 5, 6)).astype(f32)
+    idx = rng.integers(0, 6, (2, 5, 3)).astype(i32)
+    case("gather_last_i32", "op_gather_elements", [data, idx], gparams(-1), [((2, 5, 3), f32)])
+    data = rng.uniform(-1, 1, (6, 4)).astype(f32)
+    case("gather_axis0", "op_gather_elements", [data, rng.integers(0, 6, (3, 4)).astype(i64)], gparams(0),
+         [((3, 4), f32)])
+    # Tile: the detector's index broadcast and an fp32 2-D tile
+    case("tile_idx", "op_tile", [rng.integers(0, 8400, (1, 10, 1)).astype(i64), np.array([1, 1, 80], i64)], b"",
+         [((1, 10, 80), i64)])
+    case("tile_f32", "op_tile", [rng.uniform(-1, 1, (2, 3)).astype(f32), np.array([2, 2], i64)], b"",
+         [((4, 6), f32)])
+    # Cast: int64 -> fp32 (one value needs rounding), fp32 -> int64 (truncation), int32 <-> int64
+    ci = np.array([0, 1, -7, 79, 2 ** 40 + 1, -(2 ** 31), 16777217], i64)
+    case("cast_i64_f32", "op_cast", [ci], struct.pack("<BB2x", 1, 0), [((7,), f32)])
+    case("cast_f32_i64", "op_cast", [np.array([0.0, 1.9, -1.9, 79.5, -0.0, 123456.7], f32)],
+         struct.pack("<BB2x", 7, 0), [((6,), i64)])
+    case("cast_i32_i64", "op_cast", [np.array([5, -5, 2 ** 31 - 1], i32)], struct.pack("<BB2x", 7, 0), [((3,), i64)])
+    case("cast_i64_i32", "op_cast", [np.array([5, -5, 2 ** 33 + 7], i64)], struct.pack("<BB2x", 6, 0), [((3,), i32)])
+    # Mod / Div: label = index mod nc, anchor = index / nc (scalar divisor), negatives, a zero divisor
+    flat = rng.integers(0, 24000, (1, 300)).astype(i64)
+    nc = np.array(80, i64)
+    case("mod_labels", "op_mod", [flat, nc.reshape(())], b"", [((1, 300), i64)])
+    case("div_anchor", "op_div", [flat, nc.reshape(())], b"", [((1, 300), i64)])
+    sa = np.array([7, -7, 7, -7, 5, 0], i64)
+    sb = np.array([3, 3, -3, -3, 0, 4], i64)
+    case("mod_signs", "op_mod", [sa, sb], b"", [((6,), i64)])
+    case("div_signs", "op_div", [sa, sb], b"", [((6,), i64)])
+    case("mod_i32", "op_mod", [sa.astype(i32), np.array([4], i32)], b"", [((6,), i32)])
+    case("mod_f32", "op_mod", [np.array([5.5, -5.5, 7.25, 1e-3, -0.0], f32), np.array([2.0, 2.0, -2.5], f32)], b"",
+         [((5,), f32)])
+    case("unsqueeze", "op_unsqueeze", [rng.integers(0, 99, (1, 7)).astype(i64), np.array([-1], i64)], b"",
+         [((1, 7, 1), i64)])
+    np.savez_compressed(HERE / "postproc.npz", **out)
+
+
 MODEL_CASES = {
     # name: (generator, kwargs) - small enough that input and output stay a few KB
     "yolov10n_64": ("yolov10n", dict(batch=1, seed=5, hw=64)),
     "resnet_64": ("resnet", dict(batch=2, seed=6, blocks=(1, 1, 1, 1), hw=64, num_classes=10)),
+    "yolov10n_64_post": ("yolov10n", dict(batch=1, seed=5, hw=64, postprocess=True)),
 }
 
 
@@ -322,7 +410,7 @@ def winograd(L):
 def main():
     L = ref_lib()
     steps = {"planner": planner, "conv": conv_cases, "epilogue": epilogue, "gemm": gemm, "winograd": winograd,
-             "tensor_ops": tensor_ops, "models": models_as_shipped}
+             "tensor_ops": tensor_ops, "postproc": postproc, "models": models_as_shipped}
     for name in sys.argv[1:] or list(steps):
         steps[name](L)
     for f in sorted(HERE.glob("*.npz")):

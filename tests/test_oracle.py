@@ -376,7 +376,7 @@ def test_oracle_model_matches_torch_float64(tmp_path):
     assert_parity(y, _torch_graph(path, x), what="oracle model vs torch float64")
 
 
-@pytest.mark.parametrize("name", ["yolov10n_64", "resnet_64"])
+@pytest.mark.parametrize("name", ["yolov10n_64", "resnet_64", "yolov10n_64_post"])
 def test_oracle_model_as_shipped_matches_reference_runtime(name):
     """Whole models through the reference's own spinn_load / spinn_plan /
     spinn_run (tests/golden/models_as_shipped.npz): the oracle's model runner
@@ -386,7 +386,8 @@ def test_oracle_model_as_shipped_matches_reference_runtime(name):
     operator of the runner are pinned end to end."""
     import tempfile
     gen, kw = {"yolov10n_64": ("yolov10n", dict(batch=1, seed=5, hw=64)),
-               "resnet_64": ("resnet", dict(batch=2, seed=6, blocks=(1, 1, 1, 1), hw=64, num_classes=10))}[name]
+               "resnet_64": ("resnet", dict(batch=2, seed=6, blocks=(1, 1, 1, 1), hw=64, num_classes=10)),
+               "yolov10n_64_post": ("yolov10n", dict(batch=1, seed=5, hw=64, postprocess=True))}[name]
     f = _load("models_as_shipped.npz")
     g, x = getattr(models, gen)(**kw)
     fp = f[f"{name}_x_sum"]
@@ -401,3 +402,77 @@ def test_oracle_model_as_shipped_matches_reference_runtime(name):
         m.close()
     ref = f[f"{name}_y"]
     assert_parity(y, ref, max_abs=1e-5, rel_l2=1e-6, what=f"{name} as-shipped vs reference spinn_run")
+
+
+# ---------------------------------------------------------------------------
+# Detector post-processing (the exported YOLOv10 tail): oracle vs the
+# reference's own operators, bit for bit, and vs numpy closed forms.
+# ---------------------------------------------------------------------------
+def _postproc_cases():
+    f = np.load(GOLD / "postproc.npz", allow_pickle=False)
+    names = sorted({k.rsplit("_", 1)[0] for k in f.files})
+    out = []
+    for n in names:
+        ins = [f[f"{n}_in{i}"] for i in range(8) if f"{n}_in{i}" in f.files]
+        outs = [f[f"{n}_out{i}"] for i in range(8) if f"{n}_out{i}" in f.files]
+        out.append((n, ins, f[f"{n}_params"].tobytes(), outs))
+    return out
+
+
+def oracle_postproc(name, ins, prm, outs):
+    """Run the oracle function a fixture case exercises (shared with the GPU tests)."""
+    import struct
+    if name.startswith("reduce_max"):
+        return [O.reduce_max(ins[0], outs[0].size).reshape(outs[0].shape)]
+    if name.startswith("topk"):
+        return list(O.topk(ins[0], int(ins[1][0])))
+    if name.startswith("gather"):
+        axis = struct.unpack("<i", prm[:4])[0]
+        return [O.gather_elements(ins[0], ins[1], axis)]
+    if name.startswith("tile"):
+        return [O.tile(ins[0], outs[0].shape)]
+    if name.startswith("cast"):
+        return [O.cast(ins[0], outs[0].dtype)]
+    if name.startswith("mod") or name.startswith("div"):
+        op = "mod" if name.startswith("mod") else "div"
+        return [O.binary_typed(op, ins[0], ins[1], outs[0].shape)]
+    if name == "unsqueeze":
+        return [ins[0].reshape(outs[0].shape).copy()]
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("case", _postproc_cases(), ids=lambda c: c[0])
+def test_postproc_oracle_matches_reference(case):
+    name, ins, prm, outs = case
+    got = oracle_postproc(name, ins, prm, outs)
+    assert len(got) == len(outs)
+    for g, ref in zip(got, outs):
+        assert g.shape == ref.shape and g.dtype == ref.dtype, (name, g.shape, ref.shape, g.dtype, ref.dtype)
+        np.testing.assert_array_equal(g.view(np.uint8), ref.view(np.uint8))  # bit for bit, signed zeros included
+
+
+def test_postproc_closed_forms():
+    """TopK = stable descending argsort; GatherElements = take_along_axis; Tile,
+    Cast, C-style integer Div / Mod and fmod against numpy."""
+    rng = np.random.default_rng(11)
+    x = np.round(rng.uniform(-1, 1, (3, 500)), 2).astype(np.float32)  # many ties
+    v, i = O.topk(x, 120)
+    ref_i = np.argsort(-x, axis=1, kind="stable")[:, :120]
+    np.testing.assert_array_equal(i, ref_i)
+    np.testing.assert_array_equal(v, np.take_along_axis(x, ref_i, 1))
+    np.testing.assert_array_equal(O.reduce_max(x, 3), x.max(1))
+    d = rng.uniform(-1, 1, (2, 9, 5)).astype(np.float32)
+    ix = rng.integers(0, 9, (2, 4, 5)).astype(np.int64)
+    np.testing.assert_array_equal(O.gather_elements(d, ix, 1), np.take_along_axis(d, ix, 1))
+    np.testing.assert_array_equal(O.gather_elements(d, ix - 9, 1), np.take_along_axis(d, ix, 1))  # negative wrap
+    t = rng.integers(0, 100, (1, 6, 1)).astype(np.int64)
+    np.testing.assert_array_equal(O.tile(t, (2, 6, 80)), np.tile(t, (2, 1, 80)))
+    a = rng.integers(-24000, 24000, 64).astype(np.int64)
+    b = rng.integers(1, 90, 64).astype(np.int64) * rng.choice([-1, 1], 64)
+    np.testing.assert_array_equal(O.binary_typed("div", a, b, (64,)), np.trunc(a / b).astype(np.int64))
+    np.testing.assert_array_equal(O.binary_typed("mod", a, b, (64,)), np.fmod(a, b))
+    fa = rng.uniform(-9, 9, 40).astype(np.float32)
+    fb = rng.uniform(0.5, 3, 40).astype(np.float32)
+    np.testing.assert_array_equal(O.binary_typed("mod", fa, fb, (40,)), np.fmod(fa, fb))
+    np.testing.assert_array_equal(O.cast(a, np.float32), a.astype(np.float32))
+    np.testing.assert_array_equal(O.cast(fa, np.int64), np.trunc(fa).astype(np.int64))
