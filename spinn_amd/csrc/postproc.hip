@@ -68,85 +68,146 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__restrict__ x, int64_t n, int k,
                                                                  float *__restrict__ values,
                                                                  int64_t *__restrict__ indices) {
+    constexpr int kWaves = kTopkThreads / 64;
+    constexpr int kBins = 257; // per-wave histograms, padded so equal bins of two waves sit in different banks
+    __shared__ uint32_t whist[kWaves * kBins];
     __shared__ uint32_t hist[256];
     __shared__ uint32_t s_prefix, s_mask, s_need;
     __shared__ uint32_t s_gt, s_eq_base;
-    __shared__ uint32_t s_wave_eq[kTopkThreads / 64];
+    __shared__ uint32_t s_wave_eq[kWaves];
     __shared__ uint64_t cand[SPINN_HIP_TOPK_MAX_K];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const float *xr = x + (int64_t)blockIdx.x * n;
+    const int64_t nchunks = (n + kTopkThreads - 1) / kTopkThreads;
+
+    // key of element c * 1024 + tid (chunk c), and whether it exists
+    auto key_at = [&](int64_t c, bool &valid) -> uint32_t {
+        const int64_t i = c * kTopkThreads + tid;
+        valid = i < n;
+        return valid ? order_key(xr[i]) : 0u;
+    };
 
     if (tid == 0) {
         s_prefix = 0u;
         s_mask = 0u;
         s_need = (uint32_t)k;
     }
-    // 1. radix select, most significant digit first
+    // 1. radix select, most significant digit first. Each wave counts into its
+    // own histogram; when every counted lane of a wave falls in one bin (the
+    // usual case for the leading digit of scores in a narrow range) the wave adds
+    // its lane count with one atomic instead of 64 serialised ones.
     for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int b = tid; b < 256; b += kTopkThreads) hist[b] = 0u;
+        for (int b = tid; b < kWaves * kBins; b += kTopkThreads) whist[b] = 0u;
         __syncthreads();
         const uint32_t prefix = s_prefix, mask = s_mask;
-        for (int64_t i = tid; i < n; i += kTopkThreads) {
-            const uint32_t key = order_key(xr[i]);
-            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        uint32_t *wh = whist + wave * kBins;
+        for (int64_t c0 = 0; c0 < nchunks; c0 += 4) {
+            // four chunks' loads in flight before any is counted
+            uint32_t kk[4];
+            bool vv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) kk[u] = key_at(c0 + u, vv[u]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t key = kk[u];
+                const bool match = vv[u] && (key & mask) == prefix;
+                const uint32_t bin = (key >> shift) & 255u;
+                const uint64_t act = __ballot(match);
+                if (act) {
+                    const int lead = __ffsll((unsigned long long)act) - 1;
+                    const uint32_t lead_bin = (uint32_t)__shfl((int)bin, lead);
+                    const uint64_t same = __ballot(match && bin == lead_bin);
+                    if (same == act) {
+                        if (lane == lead) atomicAdd(&wh[lead_bin], (uint32_t)__popcll(act));
+                    } else if (match) {
+                        atomicAdd(&wh[bin], 1u);
+                    }
+                }
+            }
         }
         __syncthreads();
-        if (tid == 0) {
-            // walk the digits from the top until the remaining count is covered
-            uint32_t need = s_need, above = 0u;
-            int d = 255;
-            for (; d > 0; --d) {
-                if (above + hist[d] >= need) break;
-                above += hist[d];
+        for (int b = tid; b < 256; b += kTopkThreads) {
+            uint32_t t = 0u;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) t += whist[w * kBins + b];
+            hist[b] = t;
+        }
+        __syncthreads();
+        // digit selection, in parallel over the 256 bins: with above(b) the
+        // count of elements whose digit exceeds b, the k-th largest has the one
+        // digit b where above(b) < need <= above(b) + hist[b]. Thread t < 256
+        // holds bin 255 - t, so above() is an exclusive prefix sum over t.
+        const uint32_t need = s_need;
+        const int b = 255 - tid;
+        uint32_t v = 0u, incl = 0u;
+        if (tid < 256) {
+            v = hist[b];
+            incl = v;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t o = (uint32_t)__shfl_up((int)incl, off);
+                if (lane >= off) incl += o;
             }
-            s_need = need - above;
-            s_prefix = prefix | ((uint32_t)d << shift);
-            s_mask = mask | (255u << shift);
+            if (lane == 63) s_wave_eq[wave] = incl;
+        }
+        __syncthreads();
+        if (tid < 256) {
+            for (int w = 0; w < wave; ++w) incl += s_wave_eq[w];
+            const uint32_t above = incl - v;
+            if (above < need && above + v >= need) {
+                s_need = need - above;
+                s_prefix = prefix | ((uint32_t)b << shift);
+                s_mask = mask | (255u << shift);
+            }
         }
         __syncthreads();
     }
     const uint32_t thr = s_prefix;     // key of the k-th largest element
     const uint32_t take_eq = s_need;   // how many elements equal to it are kept
     const uint32_t n_gt = (uint32_t)k - take_eq;
-    if (tid == 0) {
-        s_gt = 0u;
-        s_eq_base = 0u;
-    }
-    __syncthreads();
+    if (tid == 0) s_gt = 0u;
 
-    // 2. compaction in index order
-    for (int64_t base = 0; base < n; base += kTopkThreads) {
-        const int64_t i = base + tid;
-        uint32_t key = 0u;
-        bool gt = false, eq = false;
-        if (i < n) {
-            key = order_key(xr[i]);
-            gt = key > thr;
-            eq = key == thr;
-        }
-        const uint64_t ball = __ballot(eq);
-        const uint32_t below = (uint32_t)__popcll(ball & ((1ull << lane) - 1ull));
-        if (lane == 0) s_wave_eq[wave] = (uint32_t)__popcll(ball);
-        __syncthreads();
-        uint32_t rank = s_eq_base + below;
-        for (int w = 0; w < wave; ++w) rank += s_wave_eq[w];
+    // 2. compaction. Slots only need to be distinct (step 3 orders by key and
+    // index), so winners take slots with LDS atomics; what must follow index
+    // order is which elements equal to the threshold are kept: the first
+    // take_eq. A block-wide count per chunk of 1024 elements tells whether a
+    // chunk's equal elements are all in, all out, or (one chunk) split, and
+    // only that chunk ranks its equal elements exactly.
+    if (tid == 0) s_eq_base = 0u;
+    __syncthreads();
+    uint32_t cum = 0u; // equal elements in the chunks before this one (block-uniform)
+    bool vnext;
+    uint32_t knext = key_at(0, vnext);
+    for (int64_t c = 0; c < nchunks; ++c) {
+        const bool valid = vnext;
+        const uint32_t key = knext;
+        knext = key_at(c + 1, vnext); // next chunk's load in flight across this one's barriers
+        const int64_t i = c * kTopkThreads + tid;
+        const bool gt = valid && key > thr;
+        const bool eq = valid && key == thr;
         const uint64_t packed = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+        const uint32_t cnt = (uint32_t)__syncthreads_count(eq);
         if (gt) {
             const uint32_t slot = atomicAdd(&s_gt, 1u); // < n_gt by construction of thr
             if (slot < n_gt) cand[slot] = packed;
-        } else if (eq && rank < take_eq) {
-            cand[n_gt + rank] = packed;
         }
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t t = 0u;
-            for (int w = 0; w < kTopkThreads / 64; ++w) t += s_wave_eq[w];
-            s_eq_base += t;
+        if (cum < take_eq) {
+            if (cum + cnt <= take_eq) {
+                if (eq) cand[n_gt + atomicAdd(&s_eq_base, 1u)] = packed;
+            } else {
+                const uint64_t ball = __ballot(eq);
+                if (lane == 0) s_wave_eq[wave] = (uint32_t)__popcll(ball);
+                __syncthreads();
+                uint32_t rank = cum + (uint32_t)__popcll(ball & ((1ull << lane) - 1ull));
+                for (int w = 0; w < wave; ++w) rank += s_wave_eq[w];
+                if (eq && rank < take_eq) cand[n_gt + rank] = packed;
+            }
         }
-        __syncthreads();
+        cum += cnt;
     }
+    __syncthreads();
 
     // 3. bitonic sort, descending, over the next power of two >= k (pads sort last)
     int p2 = 1;
