@@ -282,6 +282,69 @@ def calibration_kernels() -> None:
     print("[bench] calibration kernels done", flush=True)
 
 
+COMPARE_LAYERS = [  # (n, c, h, w, oc, k, stride, pad, act): ResNet-101 batch-32 layers
+    (32, 256, 14, 14, 1024, 1, 1, 0, 5),
+    (32, 1024, 14, 14, 256, 1, 1, 0, 1),
+    (32, 64, 56, 56, 64, 3, 1, 1, 1),
+]
+
+
+def gemm_compare(reps: int = 5) -> None:
+    """Launches for the PMC comparison of the MFMA engine: three ResNet-101
+    batch-32 conv layers through spinn_hip_conv (implicit GEMM, per-shape tiles),
+    an 8192^3 fp32 Gemm through spinn_hip_gemm, and the same Gemm through torch
+    (hipBLASLt), `reps` launches each; run it under rocprofv3 --pmc."""
+    import ctypes as C
+    import torch
+    from spinn_amd import native as N
+    L = N.lib()
+    N.check(L.spinn_hip_init(0), "spinn_hip_init")
+    P = lambda t: None if t is None else C.c_void_p(t.data_ptr())  # noqa: E731
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for (n, c, h, w, oc, k, s, p, act) in COMPARE_LAYERS:
+        oh, ow = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+        d = N.ConvDesc(n, c, h, w, oc, oh, ow, k, k, s, s, p, p, 1, act, N.ALGO_IMPLICIT_GEMM, 0)
+        x = torch.rand(n, c, h, w, device="cuda", generator=g)
+        wt = torch.randn(oc, c, k, k, device="cuda", generator=g) * (2.0 / (c * k * k)) ** 0.5
+        b = torch.zeros(oc, device="cuda")
+        r = torch.rand(n, oc, oh, ow, device="cuda", generator=g) if act in (4, 5) else None
+        y = torch.empty(n, oc, oh, ow, device="cuda")
+        pk = torch.empty(max(L.spinn_hip_conv_packed_size(C.byref(d)) // 4, 1), device="cuda")
+        N.check(L.spinn_hip_conv_pack_weights(C.byref(d), P(wt), P(pk), None), "pack")
+        wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
+        ws = torch.empty(max(wsz // 4, 1), device="cuda")
+        for _ in range(reps):
+            N.check(L.spinn_hip_conv(C.byref(d), P(x), P(wt), P(pk), P(b), P(r), P(y), P(ws), wsz, None), "conv")
+    m = 8192
+    a = torch.rand(m, m, device="cuda", generator=g)
+    bb = torch.rand(m, m, device="cuda", generator=g)
+    yy = torch.empty(m, m, device="cuda")
+    gd = N.GemmDesc(m, m, m, 0, 0, 0, 1.0, 0.0, 1, 0, 0, 0, 0)
+    for _ in range(reps):
+        N.check(L.spinn_hip_gemm(C.byref(gd), P(a), P(bb), None, P(yy), None, 0, None), "gemm")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    for _ in range(reps):
+        torch.matmul(a, bb, out=yy)
+    torch.cuda.synchronize()
+    # hipBLASLt on the GEMM shapes of the conv layers (M = OC, N = batch*OH*OW, K = C*KH*KW)
+    lib_us = {}
+    for (m_, n_, k_) in [(1024, 6272, 256), (256, 6272, 1024), (64, 100352, 576), (256, 6272, 2304),
+                         (512, 1568, 4608)]:
+        a2 = torch.rand(m_, k_, device="cuda", generator=g)
+        b2 = torch.rand(k_, n_, device="cuda", generator=g)
+        y2 = torch.empty(m_, n_, device="cuda")
+        for _ in range(3):
+            torch.matmul(a2, b2, out=y2)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            torch.matmul(a2, b2, out=y2)
+        e1.record()
+        torch.cuda.synchronize()
+        lib_us[f"{m_}x{n_}x{k_}"] = round(e0.elapsed_time(e1) / 20 * 1e3, 2)
+    print(json.dumps({"gemm_compare": True, "torch_fp32_matmul_us": lib_us}), flush=True)
+
+
 def igemm_algorithmic_bytes(batch: int, policy: str) -> float:
     """Mean algorithmic bytes per implicit-GEMM conv launch of ResNet-101 at
     `batch`: input + weights + bias + output (+ residual for the fused add),
@@ -379,8 +442,13 @@ def main() -> int:
     ap.add_argument("--profile-pass", action="store_true",
                     help="only the per-node-event pass at batch B (warmup + steps, eager launches): the run a "
                          "kernel profiler wraps, so its kernel statistics cover exactly the measured launches")
+    ap.add_argument("--profile-model", choices=["resnet101", "yolov10n"], default="resnet101",
+                    help="model of --profile-pass (yolov10n: the 640x640 detector with its TopK tail)")
     ap.add_argument("--layers-out", default=str(ROOT / "gpurun_out" / "bench_layers.json"))
     ap.add_argument("--no-suite", action="store_true", help="skip the config-0 / Gemm sweep / VGG measurements")
+    ap.add_argument("--gemm-compare", action="store_true",
+                    help="only the launches of the MFMA-engine PMC comparison (three ResNet-101 conv layers, an "
+                         "8192^3 Gemm here and through torch/hipBLASLt)")
     ap.add_argument("--calibration-kernels", action="store_true",
                     help="only run the known-size fill/copy kernels that scale the HBM byte counters")
     ap.add_argument("--traffic-summary", metavar="DIR",
@@ -392,6 +460,9 @@ def main() -> int:
         return 2
     if a.calibration_kernels:
         calibration_kernels()
+        return 0
+    if a.gemm_compare:
+        gemm_compare()
         return 0
     if a.traffic_summary:
         cmds = [f"rocprofv3 --pmc {c} --output-format csv -d {a.traffic_summary} -o {o}_{c} -- python -u bench.py {f}"
@@ -431,6 +502,20 @@ def main() -> int:
     L = N.lib()
     N.check(L.spinn_hip_init(0), "spinn_hip_init")
 
+    if a.profile_pass and a.profile_model == "yolov10n":
+        gy, xy = models.yolov10n(batch=a.batch, seed=0, postprocess=True)
+        py = gy.write(tmp / f"y10_b{a.batch}.ennf")
+        node_ms = profiled_node_ms(N, Session, py, xy, policy, a.steps, a.warmup)
+        fam = {}
+        for i, nd in enumerate(gy.nodes):
+            f = fam.setdefault(_op_family(N, nd, gy, policy), [0, 0.0])
+            f[0] += 1
+            f[1] += float(node_ms[i])
+        print(json.dumps({"profile_pass": True, "model": "yolov10n+tail", "batch": a.batch, "steps": a.steps,
+                          "warmup": a.warmup, "node_ms_total": float(node_ms.sum()),
+                          "families_ms": {k: {"nodes": v[0], "ms": round(v[1], 4)} for k, v in
+                                          sorted(fam.items(), key=lambda kv: -kv[1][1])}}))
+        return 0
     if a.profile_pass:
         node_ms = profiled_node_ms(N, Session, pB, xB, policy, a.steps, a.warmup)
         rows = conv_table(gB)
