@@ -131,12 +131,12 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce_kernel(const float *__
                                                                  float *__restrict__ y) {
     const int64_t total = (int64_t)OC * ntot;
     const int64_t plane = total;
+    const bool narrow = total <= INT32_MAX; // 32-bit index division (uniform branch)
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * blockDim.x) {
-        const int oc = (int)(e / ntot);
+        const int oc = narrow ? (int)((uint32_t)e / (uint32_t)ntot) : (int)(e / ntot);
         const int jcol = (int)(e - (int64_t)oc * ntot);
-        float v = 0.f;
-        for (int s = 0; s < nsplit; ++s) v += ws[s * plane + e];
+        float v = splitk_sum(ws, nsplit, plane, e);
         const int img = jcol / OHW;
         const int p = jcol - img * OHW;
         const int64_t idx = ((int64_t)img * OC + oc) * OHW + p;

@@ -120,8 +120,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *__
     const int64_t total = (int64_t)M * N;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (int64_t)gridDim.x * blockDim.x) {
-        float v = 0.f;
-        for (int s = 0; s < nsplit; ++s) v += ws[s * total + e];
+        float v = splitk_sum(ws, nsplit, total, e);
         v *= alpha;
         if (c_mode == 1) v += beta * c[e % N];
         else if (c_mode == 2) v += beta * c[e];

@@ -22,6 +22,23 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     return v;
 }
 
+// Sum of the split-K partials ws[s * plane + e] for s = 0..nsplit-1, added in
+// split order starting from 0 (the order the partials' K ranges take). The
+// loads of a group of 8 splits are issued before the first add: a plain loop
+// would wait out one memory round trip per split.
+__device__ __forceinline__ float splitk_sum(const float *__restrict__ ws, int nsplit, int64_t plane, int64_t e) {
+    float v = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+        float p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) p[u] = ws[(int64_t)min(s0 + u, nsplit - 1) * plane + e];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (s0 + u < nsplit) v += p[u];
+    }
+    return v;
+}
+
 constexpr int kBK = 16;    // K depth of one LDS slice of the MFMA GEMMs
 // Register stages of the K loop (global loads run that many slices ahead of
 // their LDS write). Measured on the ResNet-101 batch-32 and batch-1 conv

@@ -53,9 +53,11 @@ TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
         // Split K only when each split still runs >= 128 deep: the partial
         // sums cost a write and a read of the output per split. A 256-deep
         // K splits only when the grid covers less than half the CUs
-        // (batch-1 1x1 convs).
+        // (batch-1 1x1 convs). At most 16 splits: measured on the batch-1
+        // ResNet-101 convs, 16 beat 8 (the 14x14 3x3 layers then cover all
+        // CUs), while 64-deep splits or 8 workgroups per CU were slower.
         int split = (int)std::min<int64_t>((4 * cus + tiles - 1) / tiles, K / 128);
-        split = std::max(1, std::min(split, 8));
+        split = std::max(1, std::min(split, 16));
         if (split > 1) {
             int chunk = (K + split - 1) / split;
             chunk = (chunk + kBK - 1) / kBK * kBK;
