@@ -6,10 +6,10 @@
 // fp32 matrix rate of a SIMD). The K loop stages BK-deep slices of both
 // operands through two LDS buffers and NS register stages (gemm_mainloop).
 //
-// LDS layout of both operands is k-major, [BK][BT + PAD] with T (the M or N
+// LDS layout of both operands is k-major, [BK][BT (+ PAD)] with T (the M or N
 // index) contiguous, so the operand fetch of an MFMA (lane l reads element
-// (k = 2s + l/32, t = t0 + l%32)) is 32 consecutive words per half-wave; PAD
-// puts the two half-waves 32 banks apart.
+// (k = 2s + l/32, t = t0 + l%32)) is 32 consecutive words per half-wave; a
+// swizzle of odd rows (or PAD) puts the two half-waves 32 banks apart.
 //
 // MFMA 32x32x2 f32 register layout (CDNA3/CDNA4 ISA, matrix instruction
 // tables): A operand lane l = A[l%32][l/32], B operand lane l = B[l/32][l%32],
@@ -27,11 +27,16 @@ constexpr int kThreads = 256;
 
 template <int BT>
 struct LdsPad {
-    // Row stride of a k-major LDS tile: keep it a multiple of 4 floats (b128
-    // stores) and 32 words off a multiple of 64 so the two half-waves of an
-    // operand fetch land in disjoint banks.
-    static constexpr int value = ((BT % 64) == 0) ? 32 : (((BT + 32) % 64 == 0) ? 0 : 32 - (BT % 32));
+    // Row stride and column placement of a k-major LDS tile. The two
+    // half-waves of an operand fetch read rows k and k+1 and must land in
+    // disjoint halves of the 64 banks. Tiles 64 or 128 wide are unpadded and
+    // store column t of odd rows at t ^ 32 (the swizzle keeps every aligned
+    // float4 contiguous); other widths pad the row to 32 words off a multiple
+    // of 64 (a 32-wide tile needs no pad).
+    static constexpr bool swz = (BT % 64) == 0;
+    static constexpr int value = swz ? 0 : (((BT + 32) % 64 == 0) ? 0 : 32 - (BT % 32));
     static constexpr int stride = BT + value;
+    __device__ static __forceinline__ int col(int k, int t) { return swz ? (t ^ ((k & 1) << 5)) : t; }
 };
 
 // The 4 waves of a workgroup sit 2x2 over the tile, or 1x4 when the tile is
@@ -128,13 +133,14 @@ struct KMajorLoader {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
                 const int c = item(tid, i);
-                *reinterpret_cast<f32x4 *>(lds + (c / (BT / 4)) * S + (c % (BT / 4)) * 4) = rv[i];
+                const int k = c / (BT / 4);
+                *reinterpret_cast<f32x4 *>(lds + k * S + LdsPad<BT>::col(k, (c % (BT / 4)) * 4)) = rv[i];
             }
         } else {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
                 const int e = item(tid, i);
-                lds[(e / BT) * S + (e % BT)] = rs[i];
+                lds[(e / BT) * S + LdsPad<BT>::col(e / BT, e % BT)] = rs[i];
             }
         }
     }
@@ -195,10 +201,10 @@ struct RowKLoader {
             const int c = item(tid, i);
             const int t = c % BT;
             const int kq = (c / BT) * 4;
-            lds[(kq + 0) * S + t] = r[i][0];
-            lds[(kq + 1) * S + t] = r[i][1];
-            lds[(kq + 2) * S + t] = r[i][2];
-            lds[(kq + 3) * S + t] = r[i][3];
+            lds[(kq + 0) * S + LdsPad<BT>::col(kq + 0, t)] = r[i][0];
+            lds[(kq + 1) * S + LdsPad<BT>::col(kq + 1, t)] = r[i][1];
+            lds[(kq + 2) * S + LdsPad<BT>::col(kq + 2, t)] = r[i][2];
+            lds[(kq + 3) * S + LdsPad<BT>::col(kq + 3, t)] = r[i][3];
         }
     }
 };
@@ -279,7 +285,7 @@ struct Im2colLoader {
         const int kt = tid / BN;
         const int n = tid % BN;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) lds[(kt + i * KSTEP) * S + n] = r[i];
+        for (int i = 0; i < NV; ++i) lds[(kt + i * KSTEP) * S + LdsPad<BN>::col(kt + i * KSTEP, n)] = r[i];
     }
 };
 
@@ -320,7 +326,7 @@ struct Im2colTapLoader {
         const int kt = tid / BN;
         const int n = tid % BN;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) lds[(kt + i * KSTEP) * S + n] = r[i];
+        for (int i = 0; i < NV; ++i) lds[(kt + i * KSTEP) * S + LdsPad<BN>::col(kt + i * KSTEP, n)] = r[i];
     }
 };
 
@@ -366,7 +372,8 @@ struct Pointwise1x1Loader {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int c = tid + i * kThreads;
-            *reinterpret_cast<f32x4 *>(lds + (c / (BN / 4)) * S + (c % (BN / 4)) * 4) = rv[i];
+            const int k = c / (BN / 4);
+            *reinterpret_cast<f32x4 *>(lds + k * S + LdsPad<BN>::col(k, (c % (BN / 4)) * 4)) = rv[i];
         }
     }
 };
@@ -399,14 +406,20 @@ __device__ __forceinline__ void load_fragments(const float *__restrict__ As, con
                                                int lane) {
     constexpr int SA = LdsPad<BM>::stride;
     constexpr int SB = LdsPad<BN>::stride;
-    const float *ap = As + (lane >> 5) * SA + wm0 + (lane & 31);
-    const float *bp = Bs + (lane >> 5) * SB + wn0 + (lane & 31);
+    const int h = lane >> 5; // row parity of this half-wave's fetches
+    const float *ap = As + h * SA;
+    const float *bp = Bs + h * SB;
+    int ac[WaveTiling<BM, BN>::TM], bc[WaveTiling<BM, BN>::TN];
+#pragma unroll
+    for (int i = 0; i < WaveTiling<BM, BN>::TM; ++i) ac[i] = LdsPad<BM>::col(h, wm0 + i * 32 + (lane & 31));
+#pragma unroll
+    for (int j = 0; j < WaveTiling<BM, BN>::TN; ++j) bc[j] = LdsPad<BN>::col(h, wn0 + j * 32 + (lane & 31));
 #pragma unroll
     for (int q = 0; q < BK / 2; ++q) {
 #pragma unroll
-        for (int i = 0; i < WaveTiling<BM, BN>::TM; ++i) a[q][i] = ap[(2 * q) * SA + i * 32];
+        for (int i = 0; i < WaveTiling<BM, BN>::TM; ++i) a[q][i] = ap[(2 * q) * SA + ac[i]];
 #pragma unroll
-        for (int j = 0; j < WaveTiling<BM, BN>::TN; ++j) b[q][j] = bp[(2 * q) * SB + j * 32];
+        for (int j = 0; j < WaveTiling<BM, BN>::TN; ++j) b[q][j] = bp[(2 * q) * SB + bc[j]];
     }
 }
 
