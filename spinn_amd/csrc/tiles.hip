@@ -49,11 +49,14 @@ TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
         tc.bn = 128;
     }
     const int64_t tiles = (int64_t)((M + tc.bm - 1) / tc.bm) * ((N + tc.bn - 1) / tc.bn) * reps;
-    if (allow_split && ((K >= 512 && tiles < 2 * cus) || (K >= 256 && 2 * tiles < cus))) {
+    if (allow_split &&
+        ((K >= 512 && tiles < cus) || (K >= 1536 && tiles < 2 * cus) || (K >= 256 && 2 * tiles < cus))) {
         // Split K only when each split still runs >= 128 deep: the partial
-        // sums cost a write and a read of the output per split. A 256-deep
-        // K splits only when the grid covers less than half the CUs
-        // (batch-1 1x1 convs). At most 16 splits: measured on the batch-1
+        // sums cost a write and a read of the output per split. A grid of
+        // 1-2 tiles per CU splits only a long K (>= 1536: the 3x3 convs of
+        // ResNet-101 at batch 32 gain, its 1024-deep 1x1 convs lose); a
+        // 256-deep K splits only when the grid covers less than half the
+        // CUs (batch-1 1x1 convs). At most 16 splits: measured on the batch-1
         // ResNet-101 convs, 16 beat 8 (the 14x14 3x3 layers then cover all
         // CUs), while 64-deep splits or 8 workgroups per CU were slower.
         int split = (int)std::min<int64_t>((4 * cus + tiles - 1) / tiles, K / 128);
