@@ -7,8 +7,9 @@
 // (the plan-time counterpart of sgemm_pack_a_offline, gemm_kernel.c:346-369);
 // the B operand is never materialised: each K slice of im2col is gathered from
 // NCHW input straight into LDS (no column buffer, unlike conv2d.c:172-193).
-// The bias / residual / ReLU / SiLU epilogue (gemm_kernel.c:316-338) is applied
-// to the accumulators before the only store of the output.
+// The bias / residual / ReLU / SiLU epilogue (gemm_kernel.c:316-338) is fused:
+// bias + residual are the accumulators' start value, the activation is applied
+// before the only store of the output.
 //
 // When the tile grid is too small to fill 256 CUs, K is split over blockIdx.z:
 // each split writes raw partial sums to the workspace and a reduction kernel
@@ -28,6 +29,7 @@ struct ConvKArgs {
     float *__restrict__ y;
     const float *__restrict__ bias;
     const float *__restrict__ res;
+    uint32_t res_bytes; // extent of res (the output's size)
     int act;
     int OC, OHW;
     float *__restrict__ ws; // split-K partials [split][OC][ntot]
@@ -61,25 +63,52 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
     BLoader bl;
     bl.init(a.geom, n0, group, tid, k_end);
 
-    f32x16 acc[WT::TM][WT::TN];
-#pragma unroll
-    for (int i = 0; i < WT::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < WT::TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    const int nslices = (k_end - k_begin + BK - 1) / BK;
-    gemm_mainloop<BM, BN, BK, kStages>(al, bl, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0);
-
-    // Epilogue: lane owns column jcol = n0 + wn0 + j*32 + lane%32 and rows
-    // m0 + wm0 + i*32 + 8*(r/4) + 4*(lane/32) + r%4. All bias and residual
-    // values of a column block are loaded before any store so the loads are in
-    // flight together instead of each waiting behind the previous store.
+    // Lane owns columns jcol = n0 + wn0 + j*32 + lane%32 and rows
+    // m0 + wm0 + i*32 + 8*(r/4) + 4*(lane/32) + r%4 of the tile.
     const int h = lane >> 5;
     const int l32 = lane & 31;
     const int ntot = a.geom.ntot;
-    constexpr int NR = WT::TM * 16;
+
+    // Without split K the accumulators start from the epilogue's additive
+    // terms, bias + residual: their loads then overlap the K loop's prologue
+    // instead of arriving as one burst of reads after it, and the epilogue
+    // only applies the activation and stores. (The sum is the reference's
+    // acc + bias + residual in another order, within fp32 rounding.)
+    auto init = [&](f32x16 (&c)[WT::TM][WT::TN]) {
+        if constexpr (SPLIT) {
+            ZeroAcc{}(c);
+        } else {
+            // Unconditional buffer loads: a missing bias or residual is a
+            // zero-sized resource and rows or columns past the edge read at
+            // kOOB, all of which return 0.
+            const __amdgpu_buffer_rsrc_t rb =
+                make_rsrc(a.bias ? a.bias + group * a.M : a.y, a.bias ? (uint32_t)a.M * 4u : 0u);
+            const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res ? a.res : a.y, a.res ? a.res_bytes : 0u);
+#pragma unroll
+            for (int j = 0; j < WT::TN; ++j) {
+                const int jcol = n0 + wn0 + j * 32 + l32;
+                const bool col_ok = jcol < ntot;
+                const int img = jcol / a.OHW;
+                const int p = jcol - img * a.OHW;
+                const uint32_t ybase = ((uint32_t)img * a.OC + (uint32_t)(group * a.M)) * a.OHW + p;
+#pragma unroll
+                for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                        const bool ok = m < a.M;
+                        const float bv = buf_f32(rb, ok ? (uint32_t)m * 4u : kOOB);
+                        const float rv = buf_f32(rr, ok && col_ok ? (ybase + (uint32_t)m * a.OHW) * 4u : kOOB);
+                        c[i][j][r] = bv + rv;
+                    }
+            }
+        }
+    };
+
+    f32x16 acc[WT::TM][WT::TN];
+    const int nslices = (k_end - k_begin + BK - 1) / BK;
+    gemm_mainloop<BM, BN, BK, kStages>(al, bl, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0, init);
+
     if constexpr (SPLIT) {
 #pragma unroll
         for (int j = 0; j < WT::TN; ++j) {
@@ -95,12 +124,6 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
                 }
         }
     } else {
-        float bv[NR];
-#pragma unroll
-        for (int q = 0; q < NR; ++q) {
-            const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
-            bv[q] = (a.bias && m < a.M) ? a.bias[group * a.M + m] : 0.f;
-        }
 #pragma unroll
         for (int j = 0; j < WT::TN; ++j) {
             const int jcol = n0 + wn0 + j * 32 + l32;
@@ -108,17 +131,13 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
             const int img = jcol / a.OHW;
             const int p = jcol - img * a.OHW;
             const int64_t ybase = ((int64_t)img * a.OC + (int64_t)group * a.M) * a.OHW + p;
-            float rv[NR];
 #pragma unroll
-            for (int q = 0; q < NR; ++q) {
-                const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
-                rv[q] = (a.res && m < a.M) ? a.res[ybase + (int64_t)m * a.OHW] : 0.f;
-            }
+            for (int i = 0; i < WT::TM; ++i)
 #pragma unroll
-            for (int q = 0; q < NR; ++q) {
-                const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
-                if (m < a.M) a.y[ybase + (int64_t)m * a.OHW] = apply_act(acc[q >> 4][j][q & 15] + bv[q] + rv[q], a.act);
-            }
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < a.M) a.y[ybase + (int64_t)m * a.OHW] = apply_act(acc[i][j][r], a.act);
+                }
         }
     }
 }
@@ -258,12 +277,15 @@ int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, c
     a.wpk_group_stride = (int64_t)a.K * a.ldw;
     const uint64_t x_bytes = (uint64_t)d->n * d->c * d->h * d->w * sizeof(float);
     const uint64_t w_bytes = (uint64_t)igemm_packed_floats(d) * sizeof(float);
-    if (x_bytes > kMaxOperandBytes || w_bytes > kMaxOperandBytes) return SPINN_HIP_EUNSUPPORTED;
+    const uint64_t y_bytes = (uint64_t)d->n * d->oc * d->oh * d->ow * sizeof(float);
+    if (x_bytes > kMaxOperandBytes || w_bytes > kMaxOperandBytes || y_bytes > kMaxOperandBytes)
+        return SPINN_HIP_EUNSUPPORTED;
     a.geom = ConvGeom{x, (uint32_t)x_bytes, d->c, d->h, d->w, d->c / d->group, d->oh, d->ow, d->kh, d->kw,
                       d->sh, d->sw, d->ph, d->pw, d->n * d->oh * d->ow};
     a.y = y;
     a.bias = bias;
     a.res = res;
+    a.res_bytes = (uint32_t)y_bytes;
     a.act = d->act;
     a.OC = d->oc;
     a.OHW = d->oh * d->ow;

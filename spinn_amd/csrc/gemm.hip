@@ -68,15 +68,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmKArgs a) {
     }
 
     f32x16 acc[WT::TM][WT::TN];
-#pragma unroll
-    for (int i = 0; i < WT::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < WT::TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
     const int nslices = (k_end - k_begin + BK - 1) / BK;
-    gemm_mainloop<BM, BN, BK, kStages>(al, bl, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0);
+    gemm_mainloop<BM, BN, BK, kStages>(al, bl, As, Bs, acc, k_begin, nslices, tid, lane, wm0, wn0, ZeroAcc{});
 
     // Epilogue: C values of a column block are loaded before any store.
     const int h = lane >> 5;

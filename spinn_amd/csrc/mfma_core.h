@@ -54,6 +54,19 @@ struct WaveTiling {
     __device__ static int origin_n(int wave) { return (wave % WAVES_N) * WN; }
 };
 
+// Accumulator start value of the plain GEMM: zero.
+struct ZeroAcc {
+    template <class Acc>
+    __device__ __forceinline__ void operator()(Acc &acc) const {
+        constexpr int N = sizeof(Acc) / sizeof(f32x16);
+        f32x16 *p = reinterpret_cast<f32x16 *>(&acc);
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[i][r] = 0.f;
+    }
+};
+
 // ---------------------------------------------------------------------------
 // Tile loaders. Each stages a BK x BT slice of one operand: fetch() issues the
 // global loads into registers for slice [k0, k0+BK), commit() writes them to
@@ -472,15 +485,21 @@ __device__ __forceinline__ void pipelined_slice(AL &al, BL &bl, const float *As_
 // address math and loads all overlap the matrix pipe; one barrier per slice.
 // The steady-state loop is unrolled by NS so every stage is addressed
 // statically. `al_init/bl_init` are loaders initialised for this tile; each
-// stage is a copy of them.
-template <int BM, int BN, int BK, int NS, class AL, class BL>
+// stage is a copy of them. `init(acc)` sets the accumulators' start values;
+// it runs right after the first slice's loads are issued, so loads it makes
+// (a fused epilogue's bias and residual) overlap the prologue.
+template <int BM, int BN, int BK, int NS, class AL, class BL, class Init>
 __device__ __forceinline__ void gemm_mainloop(const AL &al_init, const BL &bl_init,
                                               float (*As)[BK * LdsPad<BM>::stride],
                                               float (*Bs)[BK * LdsPad<BN>::stride],
                                               f32x16 (&acc)[WaveTiling<BM, BN>::TM][WaveTiling<BM, BN>::TN],
-                                              int k_begin, int nslices, int tid, int lane, int wm0, int wn0) {
+                                              int k_begin, int nslices, int tid, int lane, int wm0, int wn0,
+                                              const Init &init) {
     static_assert(NS >= 2 && NS % 2 == 0, "the LDS buffer of a slice is its parity: NS must be even");
-    if (nslices <= 0) return;
+    if (nslices <= 0) {
+        init(acc);
+        return;
+    }
     AL al[NS];
     BL bl[NS];
 #pragma unroll
@@ -491,6 +510,7 @@ __device__ __forceinline__ void gemm_mainloop(const AL &al_init, const BL &bl_in
     // prologue: slice 0 -> LDS 0; slices 1..NS -> register stage j % NS
     al[0].fetch(k_begin, tid);
     bl[0].fetch(k_begin, tid);
+    init(acc);
     al[0].commit(As[0], tid);
     bl[0].commit(Bs[0], tid);
 #pragma unroll
