@@ -168,6 +168,28 @@ def test_resize_and_sppf_pool(hip, torch_gpu):
                                   O.maxpool(x, 20, 20, 5, 5, 1, 1, 2, 2))
 
 
+@pytest.mark.parametrize("shape,k,s,p", [
+    ((32, 64, 112, 112), 3, 2, 1),  # ResNet stem pool at batch 32
+    ((2, 5, 17, 16), 3, 2, 1),      # odd height: the last window hangs over the pad
+    ((1, 3, 8, 8), 2, 2, 0),        # VGG-style 2x2 (runtime window)
+    ((2, 4, 9, 11), 3, 1, 1),
+    ((1, 2, 10, 9), 7, 3, 3),
+    ((3, 2, 6, 7), 5, 1, 2),
+], ids=["r101-b32", "odd", "2x2", "3x3s1", "7x7s3", "5x5s1"])
+def test_maxpool_shapes(hip, torch_gpu, shape, k, s, p):
+    """Bit-exact against the oracle, including NaN inputs (never selected: the reference keeps
+    the running max unless val > max, SPINN/run_time/ops/pool/maxpool.c:36) and -inf."""
+    n, c, h, w = shape
+    oh, ow = (h + 2 * p - k) // s + 1, (w + 2 * p - k) // s + 1
+    print(f"[tensor-op] maxpool {shape} k{k} s{s} p{p}", flush=True)
+    x = np.random.default_rng(n * c + h).uniform(-1, 1, shape).astype(np.float32)
+    flat = x.reshape(-1)
+    flat[::97] = np.nan
+    flat[5::89] = -np.inf
+    np.testing.assert_array_equal(run_maxpool(hip, torch_gpu, x, oh, ow, k, k, s, s, p, p),
+                                  O.maxpool(x, oh, ow, k, k, s, s, p, p))
+
+
 def test_bad_arguments(hip, torch_gpu):
     L = hip.lib()
     buf = torch_gpu.zeros(64, device="cuda")
