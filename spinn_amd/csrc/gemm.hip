@@ -121,6 +121,60 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *__
     }
 }
 
+// Y = alpha * A B^T (+ beta C) for at most MR rows, A [M][K] and B [N][K] both
+// row-major with K contiguous (the Gemm transB=1 layout of fully-connected
+// layers): one wave per output column streams its row of B once, in float4s
+// when K % 4 == 0 and both bases are 16-byte aligned, against the M rows of A
+// (L2-resident), then sums each row's lane partials with a shuffle tree. The
+// whole launch reads B once from HBM; the MFMA tiles would stage it through
+// LDS for a single row of A.
+template <int MR, bool VEC>
+__global__ __launch_bounds__(256) void gemv_rows_kernel(const float *__restrict__ A, const float *__restrict__ B,
+                                                        const float *__restrict__ Cm, int c_mode, float alpha,
+                                                        float beta, float *__restrict__ Y, int M, int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (n >= N) return; // whole wave
+    const float *bp = B + (int64_t)n * K;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+    if constexpr (VEC) {
+#pragma unroll 4
+        for (int k = lane * 4; k < K; k += 256) {
+            const f32x4 b = *reinterpret_cast<const f32x4 *>(bp + k);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                if (m < M) {
+                    const f32x4 av = *reinterpret_cast<const f32x4 *>(A + (int64_t)m * K + k);
+                    acc[m] += av[0] * b[0] + av[1] * b[1] + av[2] * b[2] + av[3] * b[3];
+                }
+            }
+        }
+    } else {
+        for (int k = lane; k < K; k += 64) {
+            const float b = bp[k];
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+                if (m < M) acc[m] += A[(int64_t)m * K + k] * b;
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+    if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            if (m >= M) break;
+            float v = acc[m] * alpha;
+            if (c_mode == 1) v += beta * Cm[n];
+            else if (c_mode == 2) v += beta * Cm[(int64_t)m * N + n];
+            Y[(int64_t)m * N + n] = v;
+        }
+    }
+}
+
 // Tag the loaders with their source orientation for gemm_kernel.
 template <int BT, int BK, bool VEC>
 struct KMajorG : KMajorLoader<BT, BK, VEC> {
@@ -184,9 +238,15 @@ TileChoice gemm_tiles(const SpinnHipGemmDesc *d) {
     return choose_tiles(d->m, d->n, d->k, d->batch > 0 ? d->batch : 1, d->batch <= 1);
 }
 
+// The shapes gemm_run hands to gemv_rows_kernel (no workspace).
+bool gemm_is_gemv(const SpinnHipGemmDesc *d) {
+    return (d->batch <= 1) && d->m <= 4 && !d->trans_a && d->trans_b;
+}
+
 } // namespace
 
 size_t gemm_workspace_bytes(const SpinnHipGemmDesc *d) {
+    if (gemm_is_gemv(d)) return 0;
     TileChoice tc = gemm_tiles(d);
     if (tc.split <= 1) return 0;
     return (size_t)tc.split * d->m * (size_t)d->n * sizeof(float);
@@ -218,6 +278,17 @@ int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const fl
     // Vector loads need 16-byte aligned rows in every batch entry.
     const bool va = aligned16(A) && (a.lda % 4 == 0) && (batch == 1 || d->stride_a % 4 == 0);
     const bool vb = aligned16(B) && (a.ldb % 4 == 0) && (batch == 1 || d->stride_b % 4 == 0);
+    if (gemm_is_gemv(d)) {
+        // fully-connected shape: B streamed once by waves, no tiles, no workspace
+        const dim3 grid((unsigned)((d->n + 3) / 4));
+        if (va && vb)
+            hipLaunchKernelGGL((gemv_rows_kernel<4, true>), grid, dim3(256), 0, st, A, B, C, a.c_mode, d->alpha,
+                               d->beta, Y, d->m, d->n, d->k);
+        else
+            hipLaunchKernelGGL((gemv_rows_kernel<4, false>), grid, dim3(256), 0, st, A, B, C, a.c_mode, d->alpha,
+                               d->beta, Y, d->m, d->n, d->k);
+        return check_launch();
+    }
     TileChoice tc = gemm_tiles(d);
     if (tc.split > 1) {
         const size_t need = (size_t)tc.split * d->m * (size_t)d->n * sizeof(float);

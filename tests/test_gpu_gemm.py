@@ -38,6 +38,22 @@ def test_gemm_transposes_ragged(hip, torch_gpu, ta, tb, cmode, m):
     assert_parity(y, O.gemm_f64(a, b, c, alpha=0.5, beta=2.0, trans_a=ta, trans_b=tb), what="vs float64")
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("k", [2048, 2047, 5], ids=["k2048", "k2047_scalar", "k5"])
+@pytest.mark.parametrize("cmode", [0, 1, 2])
+def test_gemm_few_rows_fc(hip, torch_gpu, m, k, cmode):
+    """M <= 4 with transB=1 (fully-connected layers) runs one wave per output column over a
+    row of B; float4 loads when K % 4 == 0, scalar otherwise; alpha, beta and both C forms."""
+    n = 1000
+    rng = np.random.default_rng(m * 10 + k + cmode)
+    a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    b = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
+    c = None if cmode == 0 else rng.uniform(-1, 1, n if cmode == 1 else (m, n)).astype(np.float32)
+    print(f"[gemm] fc m={m} k={k} cmode={cmode}", flush=True)
+    y = run_gemm(hip, torch_gpu, a, b, c, alpha=0.75, beta=1.5, trans_b=1)
+    assert_parity(y, O.gemm_f64(a, b, c, alpha=0.75, beta=1.5, trans_b=1), what="vs float64")
+
+
 def test_gemm_aligned_large(hip, torch_gpu):
     m, n, k = 512, 768, 1024
     rng = np.random.default_rng(5)
