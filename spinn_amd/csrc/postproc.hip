@@ -47,6 +47,34 @@ __global__ __launch_bounds__(256) void reduce_max_rows_kernel(const float *__res
     if (lane == 0) y[row] = xr[bi]; // the element itself (keeps the sign of a zero)
 }
 
+// Short rows (a detector's class scores, 80 per anchor): one thread per row,
+// the reference's own scan - start from the first element, replace it by any
+// later one that is strictly greater - in float4 steps when VEC.
+template <bool VEC>
+__global__ __launch_bounds__(256) void reduce_max_short_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                               int64_t rows, int block) {
+    for (int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; row < rows;
+         row += (int64_t)gridDim.x * blockDim.x) {
+        const float *xr = x + row * block;
+        float best = xr[0];
+        if constexpr (VEC) {
+            for (int j = 0; j < block; j += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(xr + j);
+                if (v.x > best) best = v.x;
+                if (v.y > best) best = v.y;
+                if (v.z > best) best = v.z;
+                if (v.w > best) best = v.w;
+            }
+        } else {
+            for (int j = 1; j < block; ++j) {
+                const float v = xr[j];
+                if (v > best) best = v;
+            }
+        }
+        y[row] = best;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // TopK (SPINN/run_time/ops/tensor/topk.c:20-89), one 1024-thread workgroup per row.
 // Order: value descending, ties by ascending index - what the reference's stable
@@ -323,6 +351,14 @@ int grid_for(int64_t n) { return (int)std::max<int64_t>(1, std::min<int64_t>((n 
 } // namespace
 
 int reduce_max_rows(int64_t rows, int64_t block, const float *x, float *y, hipStream_t st) {
+    if (block <= 256) {
+        const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>((rows + 255) / 256, 65536)));
+        if (block % 4 == 0 && ((uintptr_t)x & 15u) == 0)
+            hipLaunchKernelGGL(reduce_max_short_kernel<true>, grid, dim3(256), 0, st, x, y, rows, (int)block);
+        else
+            hipLaunchKernelGGL(reduce_max_short_kernel<false>, grid, dim3(256), 0, st, x, y, rows, (int)block);
+        return check_launch();
+    }
     hipLaunchKernelGGL(reduce_max_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, y, rows, block);
     return check_launch();
 }

@@ -217,7 +217,63 @@ __global__ __launch_bounds__(kThreads) void block_copy_kernel(BlockCopyArgs args
     }
 }
 
+// The same copies for short runs (a Split or Concat along the last axis of a
+// detector head: runs of 4 or 80 floats): one thread per element of the
+// block's outer x len elements, so a workgroup covers many rows.
+__global__ __launch_bounds__(kThreads) void block_copy_flat_kernel(BlockCopyArgs args) {
+    const SpinnHipBlockCopy bk = args.b[blockIdx.y];
+    if (bk.len == 0) return;
+    const int64_t total = args.outer * bk.len;
+    if (total <= INT32_MAX) { // 32-bit index division (uniform branch)
+        const uint32_t len = (uint32_t)bk.len;
+        for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < (uint32_t)total; e += gridDim.x * kThreads) {
+            const uint32_t o = e / len;
+            const uint32_t j = e - o * len;
+            bk.dst[o * bk.dst_row + bk.dst_off + j] = bk.src[o * bk.src_row + bk.src_off + j];
+        }
+        return;
+    }
+    for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < total; e += (int64_t)gridDim.x * kThreads) {
+        const int64_t o = e / bk.len;
+        const int64_t j = e - o * bk.len;
+        bk.dst[o * bk.dst_row + bk.dst_off + j] = bk.src[o * bk.src_row + bk.src_off + j];
+    }
+}
+
 constexpr int kMaxDims = 8;
+
+// A permutation that keeps the innermost dimension innermost: rows of `run`
+// contiguous floats, output row r read from the input at the offset its
+// coordinates give. Workgroups stride the row; float4 when VEC.
+struct RunCopyArgs {
+    int ndim; // outer dims (output order)
+    uint32_t odims[kMaxDims];
+    int64_t step[kMaxDims];
+    int64_t rows, run;
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void run_copy_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                            RunCopyArgs t) {
+    for (int64_t r = blockIdx.y; r < t.rows; r += gridDim.y) {
+        uint64_t rem = (uint64_t)r;
+        int64_t off = 0;
+        for (int d = t.ndim - 1; d >= 0; --d) {
+            const uint64_t q = rem / t.odims[d];
+            off += (int64_t)(rem - q * t.odims[d]) * t.step[d];
+            rem = q;
+        }
+        const float *s = x + off;
+        float *d = y + r * t.run;
+        if constexpr (VEC) {
+            for (int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x; j < t.run / 4; j += (int64_t)gridDim.x * kThreads)
+                reinterpret_cast<float4 *>(d)[j] = reinterpret_cast<const float4 *>(s)[j];
+        } else {
+            for (int64_t j = (int64_t)blockIdx.x * kThreads + threadIdx.x; j < t.run; j += (int64_t)gridDim.x * kThreads)
+                d[j] = s[j];
+        }
+    }
+}
 
 struct TransposeArgs {
     int ndim;
@@ -383,6 +439,11 @@ int block_copy(const SpinnHipBlockCopy *blocks, int n_blocks, int64_t outer, hip
         longest = std::max(longest, b.len);
     }
     if (longest == 0) return 0;
+    if (longest < kThreads) {
+        const dim3 grid((unsigned)grid_1d(outer * longest, 16384), (unsigned)n_blocks);
+        hipLaunchKernelGGL(block_copy_flat_kernel, grid, dim3(kThreads), 0, st, args);
+        return check_launch();
+    }
     const dim3 grid((unsigned)grid_1d(vec ? longest / 4 : longest, 1024), (unsigned)n_blocks,
                     (unsigned)std::min<int64_t>(outer, 65535));
     if (vec)
@@ -428,6 +489,25 @@ int transpose(int ndim, const int64_t *dims, const int32_t *perm, const float *x
         const int64_t tiles = batch * ((rows + 31) / 32) * ((cols + 31) / 32);
         hipLaunchKernelGGL(transpose2d_kernel, dim3((unsigned)std::min<int64_t>(tiles, 1 << 16)), dim3(kThreads), 0,
                            st, x, y, batch, rows, cols);
+        return check_launch();
+    }
+    if (os[m - 1] == 1 && od[m - 1] >= kThreads) {
+        // the innermost dimension stays innermost: copy runs of od[m-1] floats
+        RunCopyArgs r;
+        r.ndim = m - 1;
+        r.run = od[m - 1];
+        r.rows = total / r.run;
+        for (int d = 0; d < m - 1; ++d) {
+            r.odims[d] = (uint32_t)od[d];
+            r.step[d] = os[d];
+        }
+        bool vec = r.run % 4 == 0 && aligned16(x) && aligned16(y);
+        for (int d = 0; d < m - 1; ++d) vec = vec && os[d] % 4 == 0;
+        const dim3 grid((unsigned)grid_1d(vec ? r.run / 4 : r.run, 64), (unsigned)std::min<int64_t>(r.rows, 65535));
+        if (vec)
+            hipLaunchKernelGGL(run_copy_kernel<true>, grid, dim3(kThreads), 0, st, x, y, r);
+        else
+            hipLaunchKernelGGL(run_copy_kernel<false>, grid, dim3(kThreads), 0, st, x, y, r);
         return check_launch();
     }
     TransposeArgs t;

@@ -86,10 +86,12 @@ def test_postproc_matches_reference(hip, torch_gpu, case):
 
 
 @pytest.mark.parametrize("rows,n,k,grid", [(16, 8400, 300, 0.01), (2, 24000, 300, 0.05), (3, 1024, 1024, 0.25),
-                                          (1, 97, 1, 0.0), (4, 5000, 700, 0.0)])
+                                          (1, 97, 1, 0.0), (4, 5000, 700, 0.0), (1, 24000, 300, 0.5),
+                                          (3, 100003, 7, 0.001), (2, 9000, 1, 0.0)])
 def test_topk_detector_sizes(hip, torch_gpu, rows, n, k, grid):
     """Sizes of the detector tail (8400 anchors, 300 x 80 candidates, batch 16),
-    k = n, k = 1 and k > 512, with values on a grid so ties are everywhere."""
+    k = n, k = 1 and k > 512, long rows, with values on a grid so ties are everywhere (a
+    0.5 grid leaves five distinct values)."""
     print(f"[topk] rows={rows} n={n} k={k}", flush=True)
     rng = np.random.default_rng(n + k)
     x = rng.uniform(-1, 1, (rows, n)).astype(np.float32)
