@@ -139,7 +139,8 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
     L = N.lib()
     out = {}
     g, x = models.conv_bn_relu(seed=0)
-    wt, bias = g.tensors[1].data, g.tensors[2].data
+    conv = g.nodes[0]  # the fused Conv: inputs x, folded weight, folded bias
+    wt, bias = g.tensors[conv.inputs[1]].data, g.tensors[conv.inputs[2]].data
     d = N.ConvDesc(1, 64, 56, 56, 64, 56, 56, 3, 3, 1, 1, 1, 1, 1, N.ACT_RELU, 0, 0)
     d.algo = L.spinn_hip_conv_select_algo(C.byref(d))
     bx, bw, bb = DeviceBuffer.from_array(x), DeviceBuffer.from_array(wt), DeviceBuffer.from_array(bias)

@@ -28,7 +28,8 @@ class OracleConv(C.Structure):
 
 
 def build(ref: bool = True) -> None:
-    """Compile liboracle.so and, when the reference sources are present, _ref/libspinn_ref.so."""
+    """Compile liboracle.so and, when the reference sources are present, _ref/libspinn_ref.so and
+    _ref/onnx2ennf."""
     subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
     if ref and REF_SRC.exists():
         subprocess.run(["make", "-s", "-C", str(HERE), "-j8", "ref"], check=True)

@@ -11,12 +11,14 @@ The writer lays a file out the way the reference converter does
     [zero padding to 16 B]
     [weight blob, tensors back to back in id order]                 <- header.weight_data_offset
 
-Graphs are written post-fusion, as graph_opt would leave them
-(SPINN/graph_opt.c:95-559): BN folded into the conv weights and bias, the
-fused post-op code in ENNF_ConvParams.reserved, the residual appended as the
-conv's last input, and ENNF_NODE_FLAG_FUSED on convs that carry an
-activation or residual. Tensor reference counts are the number of node
-inputs naming the tensor (onnx2ennf.c:232-246).
+A `Graph` here is the converted, post-fusion graph (spinn_amd.onnx.convert
+builds it from an exporter-shaped graph as the reference converter does): BN
+folded into the conv weights and bias, the fused post-op code in
+ENNF_ConvParams.reserved, the residual appended as the conv's last input,
+ENNF_NODE_FLAG_FUSED on convs that carry an activation or residual, and the
+reference counts of the graph before fusion (onnx2ennf.c:232-241) in
+`ref_counts`; without them the writer counts the node inputs naming each
+tensor.
 """
 from __future__ import annotations
 
@@ -27,8 +29,8 @@ from pathlib import Path
 import numpy as np
 
 ENNF_MAGIC = 0x454E4E46
-DT_FLOAT32, DT_INT64 = 1, 7
-_NP_DTYPE = {DT_FLOAT32: np.float32, DT_INT64: np.int64}
+DT_FLOAT32, DT_INT32, DT_INT64 = 1, 6, 7
+_NP_DTYPE = {DT_FLOAT32: np.float32, DT_INT32: np.int32, DT_INT64: np.int64}
 
 # op ids (SPINN/ennf_op_types.h numeric values)
 OP_ADD, OP_DIV, OP_MUL, OP_SUB = 4, 23, 39, 50
@@ -146,6 +148,8 @@ class Graph:
     inputs: list = field(default_factory=list)
     outputs: list = field(default_factory=list)
     opset: int = 17
+    ref_counts: list | None = None   # per tensor id; None: count the node inputs naming each tensor
+    flags: int = 0                   # ENNF_Header.flags
 
     def tensor(self, name: str, dims, dtype: int = DT_FLOAT32, data: np.ndarray | None = None) -> int:
         if data is not None:
@@ -176,10 +180,12 @@ class Graph:
 
     # ---- serialisation ----
     def to_bytes(self) -> bytes:
-        ref = [0] * len(self.tensors)
-        for n in self.nodes:
-            for i in n.inputs:
-                ref[i] += 1
+        ref = self.ref_counts
+        if ref is None:
+            ref = [0] * len(self.tensors)
+            for n in self.nodes:
+                for i in n.inputs:
+                    ref[i] += 1
         nt = len(self.tensors)
         entry_off = _HDR.size
         graph_meta_off = entry_off + nt * _ENTRY.size
@@ -196,8 +202,8 @@ class Graph:
         mb = bytearray()
         for t in self.tensors:
             dims = list(t.dims) + [0] * (8 - len(t.dims))
-            mb += _META.pack(t.id, t.dtype, len(t.dims), *dims, t.elem_count, 1 if t.is_weight else 0,
-                             min(ref[t.id], 255))
+            mb += _META.pack(t.id, t.dtype, len(t.dims), *dims, t.elem_count & 0xFFFFFFFF,
+                             1 if t.is_weight else 0, ref[t.id] & 0xFF)
         weight_off = (meta_off + len(mb) + 15) & ~15
         pad = weight_off - (meta_off + len(mb))
         entries = bytearray()
@@ -212,7 +218,7 @@ class Graph:
             else:
                 entries += _ENTRY.pack(t.id, 0, 0, 0, 0)
         hdr = _HDR.pack(ENNF_MAGIC, 2, 0, len(self.nodes), nt, n_weights, len(blob), len(self.inputs),
-                        len(self.outputs), self.opset, 0, graph_meta_off, node_off, meta_off, weight_off, 0,
+                        len(self.outputs), self.opset, self.flags, graph_meta_off, node_off, meta_off, weight_off, 0,
                         entry_off, 0, 0)
         return bytes(hdr) + bytes(entries) + gm + bytes(nb) + bytes(mb) + b"\0" * pad + bytes(blob)
 

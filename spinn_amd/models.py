@@ -1,21 +1,30 @@
-"""Seeded synthetic ENNF models for the benchmark configurations.
+"""Seeded synthetic models for the benchmark configurations.
 
-Every model is written post-fusion, exactly as the reference converter and
-graph optimizer would emit it (see spinn_amd.ennf). Weights are random-init,
-drawn from numpy's PCG64 generator with a fixed seed so that the CPU and GPU
-paths see identical bytes:
+Every model is built the way an exporter leaves it (spinn_amd.onnx.OnnxGraph:
+Conv, BatchNormalization, Relu, Add, Sigmoid, Mul, ... with value_info for
+every intermediate) and converted to ENNF exactly as the reference converter
+and graph optimizer do it (spinn_amd.onnx.convert; SPINN/onnx2ennf.c,
+SPINN/graph_opt.c). The returned ENNF graph keeps its source as `g.onnx`, so
+the same model can be written as an .onnx file and fed to the reference
+converter. Weights are random-init, drawn from numpy's PCG64 generator with a
+fixed seed so that the CPU and GPU paths see identical bytes:
 
   * conv weights: Kaiming normal, std = sqrt(2 / fan_in), fan_in = C/g*KH*KW;
   * BatchNorm: gamma ~ U(0.5,1.5), beta ~ N(0,0.1), mean ~ N(0,0.1),
-    var ~ U(0.5,1.5), eps = 1e-5, folded into the conv in float32 as
-    SPINN/graph_opt.c:181-198 does:
+    var ~ U(0.5,1.5), eps = 1e-5. ResNet and VGG carry BatchNormalization
+    nodes, which the converter folds into the conv in float32
+    (SPINN/graph_opt.c:181-198):
         f = gamma / sqrtf(var + eps);  W'[oc] = W[oc] * f;  b' = f * (b - mean) + beta.
+    YOLOv10n is exported the way its framework exports it, with BN already
+    folded into conv weight and bias by the same float32 formula (`fold_bn`).
 """
 from __future__ import annotations
 
 import numpy as np
 
 from . import ennf as E
+from . import onnx as X
+from .onnx import ONNX_INT64, OnnxGraph
 
 BN_EPS = np.float32(1e-5)
 
@@ -48,39 +57,74 @@ def _out_hw(h, w, kh, kw, sh, sw, ph, pw):
     return (h + 2 * ph - kh) // sh + 1, (w + 2 * pw - kw) // sw + 1
 
 
-def add_conv_bn(g: E.Graph, rng, name: str, x: int, oc: int, k: int, stride: int = 1, pad: int = 0,
-                group: int = 1, act: int = E.ACT_NONE, residual: int | None = None, bn: bool = True,
-                bias: bool = False) -> int:
-    """Append one fused Conv(+BN)(+act)(+residual) node; returns its output tensor."""
+def add_conv_bn(g: OnnxGraph, rng, name: str, x: str, oc: int, k: int, stride: int = 1, pad: int = 0,
+                group: int = 1, act: int = E.ACT_NONE, residual: str | None = None, bn: bool = True,
+                bias: bool = False, fold: bool = False) -> str:
+    """Append Conv [+ BatchNormalization] [+ its activation / residual nodes]; returns the last
+    output. `act` names the post-op the converter will fuse: RELU -> Relu, SILU -> Sigmoid +
+    Mul, ADD -> Add(residual, y), ADD_RELU -> Add(y, residual) + Relu. `fold` folds the BN at
+    build time (an exporter that fuses BN itself) instead of emitting a BatchNormalization node."""
     n, c, h, w = g.dims(x)
     cg = c // group
     wt = kaiming(rng, oc, cg, k, k)
     b = rng.normal(0.0, 0.01, oc).astype(np.float32) if bias else None
-    if bn:
-        wt, b = fold_bn(wt, b, *bn_params(rng, oc))
+    bnp = bn_params(rng, oc) if bn else None
+    if bnp is not None and fold:
+        wt, b = fold_bn(wt, b, *bnp)
+        bnp = None
     oh, ow = _out_hw(h, w, k, k, stride, stride, pad, pad)
-    wid = g.weight(f"{name}.weight", wt)
-    ins = [x, wid]
+    ins = [x, g.weight(f"{name}.weight", wt)]
     if b is not None:
         ins.append(g.weight(f"{name}.bias", b))
-    if residual is not None:
-        assert act in (E.ACT_ADD, E.ACT_ADD_RELU)
-        ins.append(residual)
-    y = g.tensor(f"{name}.out", (n, oc, oh, ow))
-    flags = E.NODE_FLAG_FUSED if act != E.ACT_NONE else 0
-    g.node(E.OP_CONV, ins, [y], E.conv_params(k, k, stride, stride, (pad, pad, pad, pad), group, act), flags)
+    shape = (n, oc, oh, ow)
+    y = g.value(f"{name}.conv", shape)
+    g.node("Conv", ins, [y], dilations=[1, 1], group=group, kernel_shape=[k, k], pads=[pad] * 4,
+           strides=[stride, stride])
+    if bnp is not None:
+        gamma, beta, mean, var = bnp
+        prm = [g.weight(f"{name}.bn.{t}", v) for t, v in
+               (("weight", gamma), ("bias", beta), ("running_mean", mean), ("running_var", var))]
+        z = g.value(f"{name}.bn", shape)
+        g.node("BatchNormalization", [y] + prm, [z], epsilon=float(BN_EPS), momentum=0.9)
+        y = z
+    if act == E.ACT_RELU:
+        z = g.value(f"{name}.relu", shape)
+        g.node("Relu", [y], [z])
+        y = z
+    elif act == E.ACT_SILU:
+        sg = g.value(f"{name}.sigmoid", shape)
+        g.node("Sigmoid", [y], [sg])
+        z = g.value(f"{name}.silu", shape)
+        g.node("Mul", [y, sg], [z])
+        y = z
+    elif act in (E.ACT_ADD, E.ACT_ADD_RELU):
+        assert residual is not None
+        z = g.value(f"{name}.add", shape)
+        g.node("Add", [residual, y] if act == E.ACT_ADD else [y, residual], [z])
+        y = z
+        if act == E.ACT_ADD_RELU:
+            z = g.value(f"{name}.relu", shape)
+            g.node("Relu", [y], [z])
+            y = z
+    else:
+        assert act == E.ACT_NONE and residual is None
     return y
 
 
+def _convert(og: OnnxGraph) -> E.Graph:
+    g = X.convert(og)
+    g.onnx = og
+    return g
+
+
 def conv_bn_relu(seed: int = 0, n: int = 1, c: int = 64, hw: int = 56, oc: int = 64):
-    """Single fused Conv3x3(s1,p1)+BN+ReLU (input 1x64x56x56 U[-1,1])."""
+    """Single Conv3x3(s1,p1)+BN+ReLU (input 1x64x56x56 U[-1,1]), one fused Conv after conversion."""
     rng = np.random.default_rng(seed)
-    g = E.Graph()
+    g = OnnxGraph()
     x = g.input("x", (n, c, hw, hw))
-    y = add_conv_bn(g, rng, "conv", x, oc, 3, 1, 1, act=E.ACT_RELU)
-    g.output(y)
+    g.output(add_conv_bn(g, rng, "conv", x, oc, 3, 1, 1, act=E.ACT_RELU))
     xin = rng.uniform(-1.0, 1.0, (n, c, hw, hw)).astype(np.float32)
-    return g, xin
+    return _convert(g), xin
 
 
 GEMM_SWEEP = [(1, 1000, 2048), (32, 1000, 2048), (3136, 256, 64), (784, 512, 128), (196, 1024, 256)]
@@ -89,15 +133,15 @@ GEMM_SWEEP = [(1, 1000, 2048), (32, 1000, 2048), (3136, 256, 64), (784, 512, 128
 def gemm_model(m: int, n: int, k: int, seed: int = 0):
     """Y = A B^T + bias: A ~ U(-1,1) [M,K] (model input), B ~ N(0,1/K) [N,K], bias ~ N(0,0.01) [N]."""
     rng = np.random.default_rng(seed)
-    g = E.Graph()
+    g = OnnxGraph()
     a = g.input("A", (m, k))
     b = g.weight("B", (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32))
     c = g.weight("bias", rng.normal(0.0, 0.01, n).astype(np.float32))
-    y = g.tensor("Y", (m, n))
-    g.node(E.OP_GEMM, [a, b, c], [y], E.gemm_params(1.0, 1.0, 0, 1))
+    y = g.value("Y", (m, n))
+    g.node("Gemm", [a, b, c], [y], alpha=1.0, beta=1.0, transB=1)
     g.output(y)
     ain = rng.uniform(-1.0, 1.0, (m, k)).astype(np.float32)
-    return g, ain
+    return _convert(g), ain
 
 
 RESNET101_BLOCKS = (3, 4, 23, 3)
@@ -105,25 +149,24 @@ RESNET50_BLOCKS = (3, 4, 6, 3)
 
 
 def resnet(batch: int = 1, seed: int = 0, blocks=RESNET101_BLOCKS, hw: int = 224, num_classes: int = 1000):
-    """ResNet v1.5 (stride in the 3x3), BN folded, as the converter would fuse it.
+    """ResNet v1.5 (stride in the 3x3) with BatchNormalization nodes, converted.
 
-    Block order follows the exported graph: conv1, conv2, downsample, conv3.
-    The residual Add+ReLU fuses into whichever conv comes later in node order
-    with its partner already computed (SPINN/graph_opt.c:350-374): conv3 for
-    every block (the downsample conv of a stage's first block runs before
-    it and carries no post-op). Tail: ReduceMean over (H,W) keepdims,
-    Reshape to [B,2048], Gemm(transB=1) to the logits.
+    Block node order: conv1, conv2, downsample, conv3, Add, Relu. The residual
+    Add+Relu fuses into whichever conv comes later in node order with its
+    partner already computed (SPINN/graph_opt.c:350-374): conv3 for every
+    block (the downsample conv of a stage's first block runs before it and
+    carries no post-op). Tail: ReduceMean over (H,W) keepdims, Reshape to
+    [B,2048], Gemm(transB=1) to the logits.
     """
     rng = np.random.default_rng(seed)
-    g = E.Graph()
+    g = OnnxGraph()
     x = g.input("input", (batch, 3, hw, hw))
     t = add_conv_bn(g, rng, "stem", x, 64, 7, 2, 3, act=E.ACT_RELU)
     n, c, h, w = g.dims(t)
     oh, ow = _out_hw(h, w, 3, 3, 2, 2, 1, 1)
-    p = g.tensor("maxpool.out", (n, c, oh, ow))
-    g.node(E.OP_MAXPOOL, [t], [p], E.pool_params(3, 3, 2, 2, (1, 1, 1, 1)))
+    p = g.value("maxpool.out", (n, c, oh, ow))
+    g.node("MaxPool", [t], [p], ceil_mode=0, kernel_shape=[3, 3], pads=[1, 1, 1, 1], strides=[2, 2])
     t = p
-    in_c = 64
     for si, (nb, width) in enumerate(zip(blocks, (64, 128, 256, 512))):
         for bi in range(nb):
             stride = 2 if (bi == 0 and si > 0) else 1
@@ -135,20 +178,19 @@ def resnet(batch: int = 1, seed: int = 0, blocks=RESNET101_BLOCKS, hw: int = 224
             else:
                 ident = t
             t = add_conv_bn(g, rng, f"{name}.conv3", b, width * 4, 1, 1, 0, act=E.ACT_ADD_RELU, residual=ident)
-        in_c = width * 4
     n, c, h, w = g.dims(t)
-    m = g.tensor("mean.out", (n, c, 1, 1))
-    g.node(E.OP_REDUCEMEAN, [t], [m], E.reduce_params([2, 3], keepdims=1))
-    shape = g.weight("flatten.shape", np.array([n, c], np.int64), E.DT_INT64)
-    f = g.tensor("flatten.out", (n, c))
-    g.node(E.OP_RESHAPE, [m, shape], [f])
+    m = g.value("mean.out", (n, c, 1, 1))
+    g.node("ReduceMean", [t], [m], axes=[2, 3], keepdims=1)
+    shape = g.weight("flatten.shape", np.array([n, c], np.int64))
+    f = g.value("flatten.out", (n, c))
+    g.node("Reshape", [m, shape], [f])
     fw = g.weight("fc.weight", (rng.standard_normal((num_classes, c)) / np.sqrt(c)).astype(np.float32))
     fb = g.weight("fc.bias", rng.normal(0.0, 0.01, num_classes).astype(np.float32))
-    y = g.tensor("logits", (n, num_classes))
-    g.node(E.OP_GEMM, [f, fw, fb], [y], E.gemm_params(1.0, 1.0, 0, 1))
+    y = g.value("logits", (n, num_classes))
+    g.node("Gemm", [f, fw, fb], [y], alpha=1.0, beta=1.0, transB=1)
     g.output(y)
     xin = np.random.default_rng(seed + 1).uniform(-1.0, 1.0, (batch, 3, hw, hw)).astype(np.float32)
-    return g, xin
+    return _convert(g), xin
 
 
 def resnet101(batch: int = 1, seed: int = 0):
@@ -161,24 +203,24 @@ VGG_SCHEDULE = [(64, 112), (64, 112), (128, 56), (128, 56), (256, 28), (256, 28)
 def vgg_stack(batch: int = 8, seed: int = 0, in_c: int = 64, schedule=VGG_SCHEDULE):
     """8 chained Conv3x3(s1,p1)+BN+ReLU, 2x2/2 MaxPool between resolutions."""
     rng = np.random.default_rng(seed)
-    g = E.Graph()
+    g = OnnxGraph()
     x = g.input("x", (batch, in_c, schedule[0][1], schedule[0][1]))
     t = x
     for i, (oc, res) in enumerate(schedule):
         n, c, h, w = g.dims(t)
         if h != res:
             assert h == 2 * res
-            p = g.tensor(f"pool{i}.out", (n, c, res, res))
-            g.node(E.OP_MAXPOOL, [t], [p], E.pool_params(2, 2, 2, 2))
+            p = g.value(f"pool{i}.out", (n, c, res, res))
+            g.node("MaxPool", [t], [p], ceil_mode=0, kernel_shape=[2, 2], pads=[0, 0, 0, 0], strides=[2, 2])
             t = p
         t = add_conv_bn(g, rng, f"conv{i}", t, oc, 3, 1, 1, act=E.ACT_RELU)
     g.output(t)
     xin = np.random.default_rng(seed + 1).uniform(-1.0, 1.0, g.dims(x)).astype(np.float32)
-    return g, xin
+    return _convert(g), xin
 
 
-def _plain_conv(g: E.Graph, rng, name: str, x: int, oc: int, k: int = 1, bias: bool = True,
-                weight: np.ndarray | None = None) -> int:
+def _plain_conv(g: OnnxGraph, rng, name: str, x: str, oc: int, k: int = 1, bias: bool = True,
+                weight: np.ndarray | None = None) -> str:
     """A bare nn.Conv2d (no BatchNorm, no activation) with PyTorch's default
     init: weight and bias ~ U(-1/sqrt(fan_in), 1/sqrt(fan_in))."""
     n, c, h, w = g.dims(x)
@@ -189,28 +231,29 @@ def _plain_conv(g: E.Graph, rng, name: str, x: int, oc: int, k: int = 1, bias: b
     if bias:
         ins.append(g.weight(f"{name}.bias", rng.uniform(-bound, bound, oc).astype(np.float32)))
     oh, ow = _out_hw(h, w, k, k, 1, 1, k // 2, k // 2)
-    y = g.tensor(f"{name}.out", (n, oc, oh, ow))
-    g.node(E.OP_CONV, ins, [y], E.conv_params(k, k, 1, 1, (k // 2,) * 4, 1, E.ACT_NONE))
+    y = g.value(f"{name}.out", (n, oc, oh, ow))
+    g.node("Conv", ins, [y], dilations=[1, 1], group=1, kernel_shape=[k, k], pads=[k // 2] * 4, strides=[1, 1])
     return y
 
 
 def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postprocess: bool = False,
              max_det: int = 300):
     """YOLOv10n (width 0.25, depth 0.33; ultralytics yolov10n.yaml) as the
-    converter + graph optimizer would emit the exported detector, up to the
+    exporter leaves the detector, converted, up to the
     one-to-one head's decoded output [B, 4 + nc, anchors] (boxes x1y1x2y2 in
     pixels, class scores after Sigmoid), i.e. before the TopK post-processing.
 
-    Every Conv-BN-SiLU is one Conv node with act SILU (the export's
-    Conv -> Sigmoid -> Mul pattern, SPINN/graph_opt.c:395-481); convs built
-    with act=False carry no post-op, except where their single consumer is an
-    Add whose other operand already exists - the PSA block's pe, proj and
-    ffn.1 convs - which fuse it as act ADD (SPINN/graph_opt.c:301-374). The
-    Bottleneck / CIB shortcut Adds follow a SiLU conv and stay unfused Add
-    nodes. Node order is the export's execution order.
+    BN is folded into every conv at export (conv weight and bias); each
+    Conv-BN-SiLU is Conv -> Sigmoid -> Mul, which the converter fuses into one
+    Conv with act SILU (SPINN/graph_opt.c:431-496); convs built with act=False
+    carry no post-op, except where their single consumer is an Add whose other
+    operand already exists - the PSA block's pe, proj and ffn.1 convs - which
+    fuse it as act ADD (SPINN/graph_opt.c:304-421). The Bottleneck / CIB
+    shortcut Adds follow a SiLU conv and stay unfused Add nodes. Node order is
+    the export's execution order.
     """
     rng = np.random.default_rng(seed)
-    g = E.Graph()
+    g = OnnxGraph()
     x = g.input("images", (batch, 3, hw, hw))
     uid = [0]
 
@@ -219,7 +262,7 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postpro
         return f"{s}#{uid[0]}"
 
     def conv(name, t, oc, k=1, s=1, group=1, act=E.ACT_SILU, residual=None):
-        return add_conv_bn(g, rng, name, t, oc, k, s, k // 2, group, act, residual)
+        return add_conv_bn(g, rng, name, t, oc, k, s, k // 2, group, act, residual, fold=True)
 
     def split(name, t, sizes, axis=1):
         dims = g.dims(t)
@@ -227,34 +270,34 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postpro
         for i, sz in enumerate(sizes):
             d = list(dims)
             d[axis] = sz
-            outs.append(g.tensor(f"{name}.out{i}", tuple(d)))
-        sw = g.weight(nm(f"{name}.split"), np.array(sizes, np.int64), E.DT_INT64)
-        g.node(E.OP_SPLIT, [t, sw], outs, E.split_params(axis, len(sizes)))
+            outs.append(g.value(f"{name}.out{i}", tuple(d)))
+        sw = g.weight(nm(f"{name}.split"), np.array(sizes, np.int64))
+        g.node("Split", [t, sw], outs, axis=axis)
         return outs
 
     def concat(name, ts, axis=1):
         d = list(g.dims(ts[0]))
         d[axis] = sum(g.dims(t)[axis] for t in ts)
-        y = g.tensor(f"{name}.out", tuple(d))
-        g.node(E.OP_CONCAT, ts, [y], E.axis_params(axis))
+        y = g.value(f"{name}.out", tuple(d))
+        g.node("Concat", ts, [y], axis=axis)
         return y
 
     def binary(op, name, a, b):
         da, db = g.dims(a), g.dims(b)
-        y = g.tensor(f"{name}.out", da if int(np.prod(da)) >= int(np.prod(db)) else db)
+        y = g.value(f"{name}.out", da if int(np.prod(da)) >= int(np.prod(db)) else db)
         g.node(op, [a, b], [y])
         return y
 
     def reshape(name, t, dims):
-        sw = g.weight(nm(f"{name}.shape"), np.array(dims, np.int64), E.DT_INT64)
-        y = g.tensor(f"{name}.out", tuple(dims))
-        g.node(E.OP_RESHAPE, [t, sw], [y])
+        sw = g.weight(nm(f"{name}.shape"), np.array(dims, np.int64))
+        y = g.value(f"{name}.out", tuple(dims))
+        g.node("Reshape", [t, sw], [y])
         return y
 
     def transpose(name, t, perm):
         d = g.dims(t)
-        y = g.tensor(f"{name}.out", tuple(d[p] for p in perm))
-        g.node(E.OP_TRANSPOSE, [t], [y], E.transpose_params(perm))
+        y = g.value(f"{name}.out", tuple(d[p] for p in perm))
+        g.node("Transpose", [t], [y], perm=list(perm))
         return y
 
     def c2f(name, t, c2, n, shortcut):
@@ -263,7 +306,7 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postpro
         for i in range(n):
             a = conv(f"{name}.m.{i}.cv1", y[-1], c, 3)
             b = conv(f"{name}.m.{i}.cv2", a, c, 3)
-            y.append(binary(E.OP_ADD, f"{name}.m.{i}.add", y[-1], b) if shortcut else b)
+            y.append(binary("Add", f"{name}.m.{i}.add", y[-1], b) if shortcut else b)
         return conv(f"{name}.cv2", concat(f"{name}.cat", y), c2)
 
     def scdown(name, t, c2):
@@ -273,8 +316,8 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postpro
         n_, c1, h, w = g.dims(t)
         y = [conv(f"{name}.cv1", t, c1 // 2)]
         for i in range(3):
-            p = g.tensor(f"{name}.m{i}.out", g.dims(y[-1]))
-            g.node(E.OP_MAXPOOL, [y[-1]], [p], E.pool_params(5, 5, 1, 1, (2, 2, 2, 2)))
+            p = g.value(f"{name}.m{i}.out", g.dims(y[-1]))
+            g.node("MaxPool", [y[-1]], [p], ceil_mode=0, kernel_shape=[5, 5], pads=[2, 2, 2, 2], strides=[1, 1])
             y.append(p)
         return conv(f"{name}.cv2", concat(f"{name}.cat", y), c2)
 
@@ -287,15 +330,15 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postpro
         qkv = reshape(f"{name}.attn.view", qkv, (n_, heads, 2 * key_dim + head_dim, h * w))
         q, k, v = split(f"{name}.attn.split", qkv, [key_dim, key_dim, head_dim], axis=2)
         qt = transpose(f"{name}.attn.qT", q, (0, 1, 3, 2))
-        s = g.tensor(f"{name}.attn.scores", (n_, heads, h * w, h * w))
-        g.node(E.OP_MATMUL, [qt, k], [s])
+        s = g.value(f"{name}.attn.scores", (n_, heads, h * w, h * w))
+        g.node("MatMul", [qt, k], [s])
         scale = g.weight(nm(f"{name}.attn.scale"), np.array(key_dim ** -0.5, np.float32))
-        s = binary(E.OP_MUL, f"{name}.attn.scaled", s, scale)
-        p = g.tensor(f"{name}.attn.softmax", g.dims(s))
-        g.node(E.OP_SOFTMAX, [s], [p], E.axis_params(-1))
+        s = binary("Mul", f"{name}.attn.scaled", s, scale)
+        p = g.value(f"{name}.attn.softmax", g.dims(s))
+        g.node("Softmax", [s], [p], axis=-1)
         pt = transpose(f"{name}.attn.pT", p, (0, 1, 3, 2))
-        o = g.tensor(f"{name}.attn.av", (n_, heads, head_dim, h * w))
-        g.node(E.OP_MATMUL, [v, pt], [o])
+        o = g.value(f"{name}.attn.av", (n_, heads, head_dim, h * w))
+        g.node("MatMul", [v, pt], [o])
         o = reshape(f"{name}.attn.view2", o, (n_, c, h, w))
         vv = reshape(f"{name}.attn.v", v, (n_, c, h, w))
         x2 = conv(f"{name}.attn.pe", vv, c, 3, group=c, act=E.ACT_ADD, residual=o)
@@ -312,14 +355,15 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postpro
         m = conv(f"{name}.m.0.cv1.2", m, 2 * c, 7, group=2 * c)  # RepVGGDW, 3x3 branch merged at export
         m = conv(f"{name}.m.0.cv1.3", m, c)
         m = conv(f"{name}.m.0.cv1.4", m, c, 3, group=c)
-        y.append(binary(E.OP_ADD, f"{name}.m.0.add", y[-1], m))
+        y.append(binary("Add", f"{name}.m.0.add", y[-1], m))
         return conv(f"{name}.cv2", concat(f"{name}.cat", y), c2)
 
     def upsample(name, t):
         n_, c, h, w = g.dims(t)
         sc = g.weight(nm(f"{name}.scales"), np.array([1, 1, 2, 2], np.float32))
-        y = g.tensor(f"{name}.out", (n_, c, 2 * h, 2 * w))
-        g.node(E.OP_RESIZE, [t, sc], [y])
+        y = g.value(f"{name}.out", (n_, c, 2 * h, 2 * w))
+        g.node("Resize", [t, "", sc], [y], coordinate_transformation_mode="asymmetric", mode="nearest",
+               nearest_mode="floor")
         return y
 
     # backbone
@@ -362,12 +406,12 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postpro
     xcat = concat("model.23.cat", [lv for lv, _, _, _ in levels], axis=2)
     na = g.dims(xcat)[2]
     box, cls = split("model.23.split", xcat, [4 * reg_max, nc])
-    sig = g.tensor("model.23.sigmoid.out", g.dims(cls))
-    g.node(E.OP_SIGMOID, [cls], [sig])
+    sig = g.value("model.23.sigmoid.out", g.dims(cls))
+    g.node("Sigmoid", [cls], [sig])
     d = reshape("model.23.dfl.view", box, (batch, 4, reg_max, na))
     d = transpose("model.23.dfl.t", d, (0, 2, 1, 3))
-    sm = g.tensor("model.23.dfl.softmax", g.dims(d))
-    g.node(E.OP_SOFTMAX, [d], [sm], E.axis_params(1))
+    sm = g.value("model.23.dfl.softmax", g.dims(d))
+    g.node("Softmax", [d], [sm], axis=1)
     dist = _plain_conv(g, rng, "model.23.dfl.conv", sm, 1, bias=False,
                        weight=np.arange(reg_max, dtype=np.float32).reshape(1, reg_max, 1, 1))
     dist = reshape("model.23.dfl.view2", dist, (batch, 4, na))
@@ -381,75 +425,75 @@ def yolov10n(batch: int = 1, seed: int = 0, hw: int = 640, nc: int = 80, postpro
         st.append(np.full(h * w, stride, np.float32))
     anchors = g.weight("model.23.anchors", np.stack([np.concatenate(ax), np.concatenate(ay)])[None].astype(np.float32))
     strides = g.weight("model.23.strides", np.concatenate(st)[None].astype(np.float32))
-    x1y1 = binary(E.OP_SUB, "model.23.x1y1", anchors, lt)
-    x2y2 = binary(E.OP_ADD, "model.23.x2y2", anchors, rb)
-    dbox = binary(E.OP_MUL, "model.23.dbox", concat("model.23.xyxy", [x1y1, x2y2]), strides)
+    x1y1 = binary("Sub", "model.23.x1y1", anchors, lt)
+    x2y2 = binary("Add", "model.23.x2y2", anchors, rb)
+    dbox = binary("Mul", "model.23.dbox", concat("model.23.xyxy", [x1y1, x2y2]), strides)
     y = concat("model.23.out", [dbox, sig])
     if postprocess:
         y = _v10_postprocess(g, y, batch, na, nc, max_det, nm, split, transpose, concat)
     g.output(y)
     xin = np.random.default_rng(seed + 1).uniform(0.0, 1.0, (batch, 3, hw, hw)).astype(np.float32)
-    return g, xin
+    return _convert(g), xin
 
 
-def _v10_postprocess(g: E.Graph, y: int, batch: int, na: int, nc: int, max_det: int, nm, split, transpose,
-                     concat) -> int:
+def _v10_postprocess(g: OnnxGraph, y: str, batch: int, na: int, nc: int, max_det: int, nm, split, transpose,
+                     concat) -> str:
     """The exported one-to-one post-process after the decoded head [B, 4 + nc, A]:
     per-anchor best score, TopK anchors, gather of their boxes and class scores,
     TopK over anchor x class, label = index mod nc, anchor = index / nc, final
     box gather; output [B, k, 6] = (x1, y1, x2, y2, score, label). The node
     sequence is the one the ONNX export carries (Transpose, Split, ReduceMax, TopK,
     Unsqueeze, Tile, GatherElements, Flatten, TopK, Mod, Div, Cast, Concat)."""
-    i64 = E.DT_INT64
+    i64 = ONNX_INT64
     pre = "model.23.post"
     yt = transpose(f"{pre}.t", y, (0, 2, 1))                       # [B, A, 4 + nc]
     boxes, scores = split(f"{pre}.split", yt, [4, nc], axis=2)
-    best = g.tensor(f"{pre}.max", (batch, na))
-    g.node(E.OP_REDUCEMAX, [scores], [best], E.reduce_params([-1], keepdims=0))
+    best = g.value(f"{pre}.max", (batch, na))
+    g.node("ReduceMax", [scores], [best], axes=[-1], keepdims=0)
     k1 = min(max_det, na)
-    kt = g.weight(nm(f"{pre}.k"), np.array([max_det], np.int64), i64)
+    kt = g.weight(nm(f"{pre}.k"), np.array([max_det], np.int64))
 
     def topk(name, t, k):
-        v = g.tensor(f"{name}.values", g.dims(t)[:-1] + (k,))
-        ix = g.tensor(f"{name}.indices", g.dims(t)[:-1] + (k,), i64)
-        g.node(E.OP_TOPK, [t, kt], [v, ix], E.topk_params(-1, 1, 1))
+        v = g.value(f"{name}.values", g.dims(t)[:-1] + (k,))
+        ix = g.value(f"{name}.indices", g.dims(t)[:-1] + (k,), i64)
+        g.node("TopK", [t, kt], [v, ix], axis=-1, largest=1, sorted=1)
         return v, ix
 
     def unsqueeze(name, t):
-        u = g.tensor(f"{name}.out", g.dims(t) + (1,), g.tensors[t].dtype)
-        g.node(E.OP_UNSQUEEZE, [t, g.weight(nm(f"{name}.axes"), np.array([-1], np.int64), i64)], [u])
+        u = g.value(f"{name}.out", g.dims(t) + (1,), g.elem_type(t))
+        g.node("Unsqueeze", [t, g.weight(nm(f"{name}.axes"), np.array([-1], np.int64))], [u])
         return u
 
     def tile(name, t, reps):
         d = g.dims(t)
-        u = g.tensor(f"{name}.out", tuple(a * r for a, r in zip(d, reps)), g.tensors[t].dtype)
-        g.node(E.OP_TILE, [t, g.weight(nm(f"{name}.repeats"), np.array(reps, np.int64), i64)], [u])
+        u = g.value(f"{name}.out", tuple(a * r for a, r in zip(d, reps)), g.elem_type(t))
+        g.node("Tile", [t, g.weight(nm(f"{name}.repeats"), np.array(reps, np.int64))], [u])
         return u
 
     def gather(name, data, idx):
-        u = g.tensor(f"{name}.out", g.dims(idx))
-        g.node(E.OP_GATHER_ELEMENTS, [data, idx], [u], E.gather_params(1))
+        u = g.value(f"{name}.out", g.dims(idx))
+        g.node("GatherElements", [data, idx], [u], axis=1)
         return u
 
     def int_op(op, name, t, divisor):
-        u = g.tensor(f"{name}.out", g.dims(t), i64)
-        g.node(op, [t, divisor], [u])
+        u = g.value(f"{name}.out", g.dims(t), i64)
+        g.node(op, [t, divisor], [u], **({"fmod": 0} if op == "Mod" else {}))
         return u
 
     _, i1 = topk(f"{pre}.topk0", best, k1)
     i1u = unsqueeze(f"{pre}.unsq0", i1)
     boxes1 = gather(f"{pre}.gather0", boxes, tile(f"{pre}.tile0", i1u, (1, 1, 4)))
     scores1 = gather(f"{pre}.gather1", scores, tile(f"{pre}.tile1", i1u, (1, 1, nc)))
-    flat = g.tensor(f"{pre}.flat", (batch, k1 * nc))
-    g.node(E.OP_FLATTEN, [scores1], [flat], E.axis_params(1))
+    flat = g.value(f"{pre}.flat", (batch, k1 * nc))
+    g.node("Flatten", [scores1], [flat], axis=1)
     k2 = min(max_det, k1 * nc)
     s2, i2 = topk(f"{pre}.topk1", flat, k2)
-    ncw = g.weight(nm(f"{pre}.nc"), np.array(nc, np.int64), i64)
-    labels = int_op(E.OP_MOD, f"{pre}.mod", i2, ncw)
-    anchor = int_op(E.OP_DIV, f"{pre}.div", i2, ncw)
+    ncw = g.weight(nm(f"{pre}.nc"), np.array(nc, np.int64))
+    labels = int_op("Mod", f"{pre}.mod", i2, ncw)
+    anchor = int_op("Div", f"{pre}.div", i2, ncw)
     lab = unsqueeze(f"{pre}.unsq1", labels)
-    labf = g.tensor(f"{pre}.cast.out", g.dims(lab))
-    g.node(E.OP_CAST, [lab], [labf], E.cast_params(E.DT_FLOAT32))
+    labf = g.value(f"{pre}.cast.out", g.dims(lab))
+    g.node("Cast", [lab], [labf], to=1)
     boxes2 = gather(f"{pre}.gather2", boxes1, tile(f"{pre}.tile2", unsqueeze(f"{pre}.unsq2", anchor), (1, 1, 4)))
     return concat(f"{pre}.out", [boxes2, unsqueeze(f"{pre}.unsq3", s2), labf], axis=2)
 

@@ -1,0 +1,520 @@
+"""Pre-fusion model graphs: ONNX files out, and the ONNX -> ENNF conversion.
+
+A model is first built the way an exporter leaves it (`OnnxGraph`: named
+tensors, initializers, value_info for every intermediate, nodes with ONNX op
+types and attributes - Conv, BatchNormalization, Relu, Add, Sigmoid, Mul, ...).
+`OnnxGraph.to_onnx()` serialises it as an ONNX ModelProto, the reference
+converter's input; `OnnxGraph.convert()` produces what the reference converter
+writes for that file (SPINN/onnx2ennf.c:157-529 with SPINN/graph_opt.c:515-559):
+
+* tensor ids in first-seen order over initializers, graph inputs, graph
+  outputs, value_info, then node outputs / inputs (onnx2ennf.c:185-241);
+* reference counts taken on the graph BEFORE fusion (onnx2ennf.c:232-241),
+  truncated to the 8-bit field;
+* the graph optimizer's passes in order: Conv+BatchNormalization (folded in
+  float32 into the conv weight, the fused bias written over the BN bias
+  initializer, which becomes the conv's bias input), Conv+Add(+Relu) with the
+  residual appended as the conv's last input, Conv+Sigmoid+Mul (SiLU),
+  Conv+Relu (graph_opt.c:95-496); skipped nodes drop out of the node table,
+  their tensors and initializers stay in the tensor table and weight blob;
+* per-op parameter blocks as onnx2ennf_ops.c:91-438 extracts them, the fused
+  activation code in ENNF_ConvParams.reserved (onnx2ennf.c:341-347);
+* tensor meta from the initializer or the value_info, nothing (dtype 0, no
+  dims) for a name known only from a node (onnx2ennf.c:372-420).
+
+Parameter fields the reference converter leaves unwritten (it reuses one
+buffer across nodes without clearing it for these ops: Split.num_outputs,
+Gather/GatherElements.batch_dims, TopK and Cast reserved bytes) are written as
+zero here; `UNSET_PARAM_BYTES` lists them, and no operator reads them.
+"""
+from __future__ import annotations
+
+import struct
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import ennf as E
+
+# ONNX TensorProto.DataType -> ENNF_DataType (onnx2ennf.c:71-87)
+ONNX_FLOAT, ONNX_INT64 = 1, 7
+# (the ENNF enum shares ONNX's numbering for these; any other type maps to 0, undefined)
+_ONNX_TO_ENNF = {k: k for k in (1, 2, 3, 4, 5, 6, 7, 9, 10, 11, 12, 13)}
+_NP_TO_ONNX = {np.dtype(np.float32): ONNX_FLOAT, np.dtype(np.int64): ONNX_INT64, np.dtype(np.int32): 6}
+
+# ONNX op type -> ENNF op id (SPINN/ennf_op_types.c name table; ids as in ennf_op_types.h)
+OP_IDS = {
+    "Add": E.OP_ADD, "Sub": E.OP_SUB, "Mul": E.OP_MUL, "Div": E.OP_DIV, "Mod": E.OP_MOD,
+    "Conv": E.OP_CONV, "MaxPool": E.OP_MAXPOOL, "AveragePool": E.OP_AVGPOOL, "GlobalAveragePool": E.OP_GAP,
+    "BatchNormalization": E.OP_BN, "Relu": E.OP_RELU, "Sigmoid": E.OP_SIGMOID, "Softmax": E.OP_SOFTMAX,
+    "Gemm": E.OP_GEMM, "MatMul": E.OP_MATMUL, "Concat": E.OP_CONCAT, "Flatten": E.OP_FLATTEN,
+    "Identity": E.OP_IDENTITY, "Reshape": E.OP_RESHAPE, "Resize": E.OP_RESIZE, "Split": E.OP_SPLIT,
+    "Transpose": E.OP_TRANSPOSE, "ReduceMean": E.OP_REDUCEMEAN, "ReduceMax": E.OP_REDUCEMAX,
+    "Cast": E.OP_CAST, "GatherElements": E.OP_GATHER_ELEMENTS, "Tile": E.OP_TILE, "TopK": E.OP_TOPK,
+    "Unsqueeze": E.OP_UNSQUEEZE,
+}
+# ops whose parameter block the converter leaves empty (the switch's default case)
+_NO_PARAMS = {"Add", "Sub", "Mul", "Div", "Mod", "GlobalAveragePool", "Relu", "Sigmoid", "MatMul", "Identity",
+              "Reshape", "Resize", "Tile"}
+# (offset, length) of the parameter bytes the reference converter does not write, per op type
+UNSET_PARAM_BYTES = {"Split": (4, 4), "GatherElements": (4, 4), "TopK": (6, 2), "Cast": (2, 2)}
+
+NODE_SKIP, NODE_HAS_ACT = 1, 2  # graph_opt.h:27-28
+
+
+# ---------------------------------------------------------------------------
+# graph
+# ---------------------------------------------------------------------------
+@dataclass
+class OnnxNode:
+    op_type: str
+    inputs: list
+    outputs: list
+    attrs: dict = field(default_factory=dict)
+    name: str = ""
+
+
+@dataclass
+class OnnxGraph:
+    """An exporter-shaped graph. Tensors are referred to by name."""
+    nodes: list = field(default_factory=list)
+    initializers: dict = field(default_factory=dict)   # name -> ndarray, in file order
+    inputs: dict = field(default_factory=dict)         # name -> (elem_type, dims)
+    outputs: dict = field(default_factory=dict)        # name -> (elem_type, dims)
+    value_info: dict = field(default_factory=dict)     # name -> (elem_type, dims), node-output order
+    opset: int = 17
+    name: str = "model"
+
+    def input(self, name: str, dims, elem_type: int = ONNX_FLOAT) -> str:
+        """A graph input; a str entry in `dims` is a symbolic (dim_param) dimension."""
+        self.inputs[name] = (elem_type, _dims(dims))
+        return name
+
+    def weight(self, name: str, data: np.ndarray) -> str:
+        assert name not in self.initializers, name
+        self.initializers[name] = np.ascontiguousarray(data)
+        return name
+
+    def value(self, name: str, dims, elem_type: int = ONNX_FLOAT) -> str:
+        assert name not in self.value_info and name not in self.initializers, name
+        self.value_info[name] = (elem_type, _dims(dims))
+        return name
+
+    def output(self, name: str) -> None:
+        self.outputs[name] = self.value_info.pop(name)
+
+    def node(self, op_type: str, inputs, outputs, **attrs) -> None:
+        self.nodes.append(OnnxNode(op_type, list(inputs), list(outputs), dict(attrs),
+                                   f"{op_type}_{len(self.nodes)}"))
+
+    def dims(self, name: str) -> tuple:
+        for table in (self.value_info, self.inputs, self.outputs):
+            if name in table:
+                return table[name][1]
+        return tuple(self.initializers[name].shape)
+
+    def elem_type(self, name: str) -> int:
+        for table in (self.value_info, self.inputs, self.outputs):
+            if name in table:
+                return table[name][0]
+        return _NP_TO_ONNX[self.initializers[name].dtype]
+
+    # ---- ONNX serialisation ----
+    def to_onnx(self) -> bytes:
+        """ModelProto bytes (ir_version 8, one default-domain opset import)."""
+        g = b"".join(_len(1, _node_proto(n)) for n in self.nodes)
+        g += _len(2, self.name.encode())
+        g += b"".join(_len(5, _tensor_proto(k, v)) for k, v in self.initializers.items())
+        g += b"".join(_len(11, _value_info(k, *v)) for k, v in self.inputs.items())
+        g += b"".join(_len(12, _value_info(k, *v)) for k, v in self.outputs.items())
+        g += b"".join(_len(13, _value_info(k, *v)) for k, v in self.value_info.items())
+        opset = _len(1, b"") + _int(2, self.opset)
+        return _int(1, 8) + _len(2, b"spinn_amd") + _len(7, g) + _len(8, opset)
+
+    # ---- conversion ----
+    def convert(self) -> E.Graph:
+        return convert(self)
+
+
+# ---------------------------------------------------------------------------
+# protobuf wire format (the subset ONNX models use)
+# ---------------------------------------------------------------------------
+def _varint(v: int) -> bytes:
+    v &= (1 << 64) - 1  # int64 fields: negative values as their 64-bit two's complement
+    out = bytearray()
+    while True:
+        b = v & 0x7F
+        v >>= 7
+        if v:
+            out.append(b | 0x80)
+        else:
+            out.append(b)
+            return bytes(out)
+
+
+def _key(fno: int, wire: int) -> bytes:
+    return _varint(fno << 3 | wire)
+
+
+def _len(fno: int, payload: bytes) -> bytes:
+    return _key(fno, 2) + _varint(len(payload)) + payload
+
+
+def _int(fno: int, v: int) -> bytes:
+    return _key(fno, 0) + _varint(int(v))
+
+
+def _f32(fno: int, v: float) -> bytes:
+    return _key(fno, 5) + struct.pack("<f", v)
+
+
+def _packed(fno: int, vals) -> bytes:
+    return _len(fno, b"".join(_varint(int(v)) for v in vals))
+
+
+def _attribute(name: str, v) -> bytes:
+    b = _len(1, name.encode())
+    if isinstance(v, float):
+        return b + _f32(2, v) + _int(20, 1)
+    if isinstance(v, int):
+        return b + _int(3, v) + _int(20, 2)
+    if isinstance(v, str):
+        return b + _len(4, v.encode()) + _int(20, 3)
+    vals = list(v)
+    if vals and all(isinstance(x, float) for x in vals):
+        return b + _len(7, struct.pack(f"<{len(vals)}f", *vals)) + _int(20, 6)
+    return b + _packed(8, vals) + _int(20, 7)
+
+
+def _node_proto(n: OnnxNode) -> bytes:
+    b = b"".join(_len(1, s.encode()) for s in n.inputs)
+    b += b"".join(_len(2, s.encode()) for s in n.outputs)
+    b += _len(3, n.name.encode()) + _len(4, n.op_type.encode())
+    b += b"".join(_len(5, _attribute(k, v)) for k, v in n.attrs.items())
+    return b
+
+
+def _tensor_proto(name: str, a: np.ndarray) -> bytes:
+    b = _packed(1, a.shape) if a.ndim else b""
+    b += _int(2, _NP_TO_ONNX[a.dtype]) + _len(8, name.encode())
+    return b + _len(9, a.astype(a.dtype.newbyteorder("<"), copy=False).tobytes())
+
+
+def _dims(dims) -> tuple:
+    return tuple(d if isinstance(d, str) else int(d) for d in dims)
+
+
+def _value_info(name: str, elem_type: int, dims) -> bytes:
+    shape = b"".join(_len(1, _len(2, d.encode()) if isinstance(d, str) else _int(1, d)) for d in dims)
+    tensor_type = _int(1, elem_type) + _len(2, shape)
+    return _len(1, name.encode()) + _len(2, _len(1, tensor_type))
+
+
+# ---------------------------------------------------------------------------
+# parameter blocks (SPINN/onnx2ennf_ops.c:91-438)
+# ---------------------------------------------------------------------------
+def _ints(attrs, name, n):
+    v = [int(x) for x in attrs.get(name, [])][:n]
+    return v + [0] * (n - len(v))
+
+
+def op_params(op_type: str, attrs: dict) -> bytes:
+    """The parameter block the reference converter writes for one node."""
+    a = attrs
+    if op_type == "Conv":
+        return struct.pack("<4H4H8H4HHBB", *[x & 0xFFFF for x in _ints(a, "kernel_shape", 4)],
+                           *[x & 0xFFFF for x in _ints(a, "strides", 4)], *[x & 0xFFFF for x in _ints(a, "pads", 8)],
+                           *[x & 0xFFFF for x in _ints(a, "dilations", 4)], int(a.get("group", 1)) & 0xFFFF,
+                           _auto_pad(a), 0)
+    if op_type in ("MaxPool", "AveragePool"):
+        return struct.pack("<4H4H8H4HBBBBi", *[x & 0xFFFF for x in _ints(a, "kernel_shape", 4)],
+                           *[x & 0xFFFF for x in _ints(a, "strides", 4)], *[x & 0xFFFF for x in _ints(a, "pads", 8)],
+                           *[x & 0xFFFF for x in _ints(a, "dilations", 4)], _auto_pad(a),
+                           int(a.get("ceil_mode", 0)) & 0xFF, int(a.get("count_include_pad", 0)) & 0xFF,
+                           int(a.get("storage_order", 0)) & 0xFF, 0)
+    if op_type == "Gemm":
+        return struct.pack("<ffBB2x", float(a.get("alpha", 1.0)), float(a.get("beta", 1.0)),
+                           int(a.get("transA", 0)) & 0xFF, int(a.get("transB", 0)) & 0xFF)
+    if op_type == "BatchNormalization":
+        return struct.pack("<ffB3x", float(a.get("epsilon", 1e-5)), float(a.get("momentum", 0.9)),
+                           int(a.get("training_mode", 0)) & 0xFF)
+    if op_type == "Softmax":
+        return struct.pack("<i", int(a.get("axis", -1)))
+    if op_type in ("Concat", "Flatten"):
+        return struct.pack("<i", int(a.get("axis", 1)))
+    if op_type == "Split":
+        return struct.pack("<iI", int(a.get("axis", 0)), 0)
+    if op_type == "GatherElements":
+        return struct.pack("<ii", int(a.get("axis", 0)), 0)
+    if op_type == "TopK":
+        return struct.pack("<iBB2x", int(a.get("axis", -1)), int(a.get("largest", 1)) & 0xFF,
+                           int(a.get("sorted", 1)) & 0xFF)
+    if op_type == "Cast":
+        return struct.pack("<BB2x", int(a.get("to", 0)) & 0xFF, int(a.get("saturate", 1)) & 0xFF)
+    if op_type == "Transpose":
+        perm = [int(x) for x in a.get("perm", [])]
+        p = [x & 0xFF for x in perm[:8]] + [0] * (8 - min(len(perm), 8))
+        return struct.pack("<8BB3x", *p, len(perm) & 0xFF)
+    if op_type == "Unsqueeze":
+        axes = [int(x) for x in a.get("axes", [])][:8]
+        return struct.pack("<8iB3x", *(axes + [0] * (8 - len(axes))), len(axes))
+    if op_type in ("ReduceMean", "ReduceMax"):
+        axes = [int(x) for x in a.get("axes", [])][:8]
+        return struct.pack("<8iBBBB", *(axes + [0] * (8 - len(axes))), len(axes), int(a.get("keepdims", 1)) & 0xFF,
+                           int(a.get("noop_with_empty_axes", 0)) & 0xFF, 0)
+    if op_type in _NO_PARAMS:
+        return b""
+    raise NotImplementedError(f"parameter block of {op_type} is not restated")
+
+
+def _auto_pad(a) -> int:
+    s = a.get("auto_pad")
+    return {"SAME_UPPER": 1, "SAME_LOWER": 2, "VALID": 3}.get(s, 0) if s is not None else 0
+
+
+# ---------------------------------------------------------------------------
+# graph optimizer (SPINN/graph_opt.c) over a working copy of the graph
+# ---------------------------------------------------------------------------
+class _Opt:
+    def __init__(self, og: OnnxGraph, init: dict):
+        self.g = og
+        self.nodes = [OnnxNode(n.op_type, list(n.inputs), list(n.outputs), n.attrs, n.name) for n in og.nodes]
+        self.init = init
+        self.flags = [0] * len(self.nodes)
+        self.act = [E.ACT_NONE] * len(self.nodes)
+
+    def consumers(self, name: str, start: int) -> int:
+        """Uses of `name` by live nodes from `start` on, plus graph outputs (graph_opt.c:47-66)."""
+        c = sum(n.inputs.count(name) for i, n in enumerate(self.nodes[start:], start)
+                if not self.flags[i] & NODE_SKIP)
+        return c + sum(1 for o in self.g.outputs if o == name)
+
+    def first_user(self, name: str, start: int, any_input: bool = False):
+        """First live node from `start` on whose input 0 (or any input) is `name`."""
+        for j in range(start, len(self.nodes)):
+            if self.flags[j] & NODE_SKIP:
+                continue
+            ins = self.nodes[j].inputs
+            if (name in ins) if any_input else (len(ins) > 0 and ins[0] == name):
+                return j
+        return None
+
+    def fuse_conv_bn(self) -> int:                                     # graph_opt.c:95-225
+        fused = 0
+        for i in range(len(self.nodes) - 1):
+            conv = self.nodes[i]
+            if self.flags[i] & NODE_SKIP or conv.op_type != "Conv" or not conv.outputs:
+                continue
+            out = conv.outputs[0]
+            if self.consumers(out, i + 1) != 1:
+                continue
+            j = self.first_user(out, i + 1)
+            if j is None or self.nodes[j].op_type != "BatchNormalization":
+                continue
+            bn = self.nodes[j]
+            if len(bn.inputs) < 5 or any(bn.inputs[k] not in self.init for k in range(1, 5)):
+                continue
+            scale, beta, mean, var = (self.init[bn.inputs[k]] for k in range(1, 5))
+            eps = np.float32(bn.attrs.get("epsilon", 1e-5))
+            if len(conv.inputs) < 2 or conv.inputs[1] not in self.init:
+                continue
+            w = self.init[conv.inputs[1]]
+            oc = w.shape[0] if w.ndim else 0
+            if oc <= 0 or scale.size != oc:
+                continue
+            has_bias = len(conv.inputs) >= 3 and conv.inputs[2] != ""
+            b_old = self.init.get(conv.inputs[2]) if has_bias else None
+            # in float32, operation by operation, as the C loop computes it (graph_opt.c:181-198)
+            f = (scale.reshape(-1) / np.sqrt(var.reshape(-1) + eps)).astype(np.float32)
+            w.reshape(oc, -1)[...] *= f[:, None]
+            bo = np.zeros(oc, np.float32)
+            if b_old is not None:
+                k = min(oc, b_old.size)
+                bo[:k] = b_old.reshape(-1)[:k]
+            beta.reshape(-1)[...] = f * (bo - mean.reshape(-1)) + beta.reshape(-1)
+            conv.outputs[0] = bn.outputs[0]
+            if has_bias:
+                conv.inputs[2] = bn.inputs[2]
+            else:
+                conv.inputs = conv.inputs[:2] + [bn.inputs[2]]
+            self.flags[j] = NODE_SKIP
+            fused += 1
+        return fused
+
+    def fuse_conv_add(self) -> int:                                    # graph_opt.c:304-421
+        fused = 0
+        for i in range(len(self.nodes) - 1):
+            conv = self.nodes[i]
+            if self.flags[i] & NODE_SKIP or self.act[i] != E.ACT_NONE:
+                continue
+            if conv.op_type != "Conv" or not conv.outputs:
+                continue
+            out = conv.outputs[0]
+            if self.consumers(out, i + 1) != 1:
+                continue
+            j = self.first_user(out, i + 1, any_input=True)
+            if j is None or self.nodes[j].op_type != "Add" or len(self.nodes[j].inputs) != 2:
+                continue
+            add = self.nodes[j]
+            if add.inputs[0] == out:
+                res = add.inputs[1]
+            elif add.inputs[1] == out:
+                res = add.inputs[0]
+            else:
+                continue
+            if res in self.init:
+                continue
+            ready = any(res in self.nodes[k].outputs for k in range(i)) or res in self.g.inputs
+            if not ready:
+                continue
+            relu = None
+            if self.consumers(add.outputs[0], j + 1) == 1:
+                r = self.first_user(add.outputs[0], j + 1)
+                if r is not None and self.nodes[r].op_type == "Relu":
+                    relu = r
+            if relu is not None:
+                conv.outputs[0] = self.nodes[relu].outputs[0]
+                self.flags[j] = self.flags[relu] = NODE_SKIP
+                self.act[i] = E.ACT_ADD_RELU
+            else:
+                conv.outputs[0] = add.outputs[0]
+                self.flags[j] = NODE_SKIP
+                self.act[i] = E.ACT_ADD
+            self.flags[i] |= NODE_HAS_ACT
+            conv.inputs = conv.inputs + [res]
+            fused += 1
+        return fused
+
+    def fuse_conv_silu(self) -> int:                                   # graph_opt.c:431-496
+        fused = 0
+        for i in range(len(self.nodes) - 2):
+            conv = self.nodes[i]
+            if self.flags[i] & NODE_SKIP or self.act[i] != E.ACT_NONE:
+                continue
+            if conv.op_type != "Conv" or not conv.outputs:
+                continue
+            out = conv.outputs[0]
+            if self.consumers(out, i + 1) != 2:
+                continue
+            sig = mul = None
+            for j in range(i + 1, len(self.nodes)):
+                if self.flags[j] & NODE_SKIP or out not in self.nodes[j].inputs:
+                    continue
+                t = self.nodes[j].op_type
+                if t == "Sigmoid" and sig is None:
+                    sig = j
+                elif t == "Mul" and mul is None:
+                    mul = j
+                else:
+                    sig = mul = None
+                    break
+                if sig is not None and mul is not None:
+                    break
+            if sig is None or mul is None:
+                continue
+            s_out = self.nodes[sig].outputs[0]
+            if self.consumers(s_out, sig + 1) != 1:
+                continue
+            m = self.nodes[mul]
+            if len(m.inputs) != 2 or s_out not in m.inputs:
+                continue
+            conv.outputs[0] = m.outputs[0]
+            self.flags[sig] = self.flags[mul] = NODE_SKIP
+            self.act[i] = E.ACT_SILU
+            self.flags[i] |= NODE_HAS_ACT
+            fused += 1
+        return fused
+
+    def fuse_conv_relu(self) -> int:                                   # graph_opt.c:235-288
+        fused = 0
+        for i in range(len(self.nodes) - 1):
+            conv = self.nodes[i]
+            if self.flags[i] & NODE_SKIP or conv.op_type != "Conv" or not conv.outputs:
+                continue
+            out = conv.outputs[0]
+            if self.consumers(out, i + 1) != 1:
+                continue
+            j = self.first_user(out, i + 1)
+            if j is None or self.nodes[j].op_type != "Relu":
+                continue
+            conv.outputs[0] = self.nodes[j].outputs[0]
+            self.act[i] = E.ACT_RELU
+            self.flags[i] |= NODE_HAS_ACT
+            self.flags[j] = NODE_SKIP
+            fused += 1
+        return fused
+
+    def run(self, conv_add: bool = True, conv_silu: bool = True) -> None:   # graph_opt.c:515-545
+        for _ in range(10):
+            if self.fuse_conv_bn() == 0:
+                break
+        if conv_add:
+            self.fuse_conv_add()
+        if conv_silu:
+            self.fuse_conv_silu()
+        self.fuse_conv_relu()
+
+
+def convert(og: OnnxGraph, conv_add: bool = True, conv_silu: bool = True) -> E.Graph:
+    """ENNF graph of `og` as the reference converter writes it (SPINN/onnx2ennf.c:157-529).
+
+    `conv_add` / `conv_silu` False stand for the converter's SPINN_DISABLE_CONV_ADD /
+    SPINN_DISABLE_CONV_SILU switches (graph_opt.c:531,538)."""
+    ids: dict = {}
+
+    def tid(name: str) -> int:
+        if name not in ids:
+            ids[name] = len(ids)
+        return ids[name]
+
+    for name in og.initializers:
+        tid(name)
+    for table in (og.inputs, og.outputs, og.value_info):
+        for name in table:
+            tid(name)
+    ref = {}
+    for n in og.nodes:
+        for o in n.outputs:
+            tid(o)
+        for i in n.inputs:
+            k = tid(i)
+            ref[k] = ref.get(k, 0) + 1
+
+    init = {k: v.copy() for k, v in og.initializers.items()}   # the optimizer folds in place
+    opt = _Opt(og, init)
+    opt.run(conv_add, conv_silu)
+
+    g = E.Graph(opset=og.opset)
+    dynamic = False
+    for name, k in ids.items():
+        if name in init:
+            a = init[name]
+            g.tensor(name, tuple(a.shape)[:8], _ONNX_TO_ENNF[_NP_TO_ONNX[a.dtype]], a)
+        else:
+            et, dims = (None, None)
+            for table in (og.inputs, og.outputs, og.value_info):
+                if name in table:
+                    et, dims = table[name]
+                    break
+            if et is None:
+                g.tensor(name, (), 0)
+            else:
+                # a symbolic dimension reads as 0 and marks the file ENNF_FLAG_DYNAMIC_SHAPE
+                sym = [isinstance(d, str) for d in dims[:8]]
+                dynamic |= any(sym)
+                g.tensor(name, tuple(0 if q else d for d, q in zip(dims[:8], sym)), _ONNX_TO_ENNF.get(et, 0))
+        assert g.tensors[-1].id == k
+    g.ref_counts = [ref.get(k, 0) & 0xFF for k in range(len(ids))]
+    g.flags = 4 if dynamic else 0   # ENNF_FLAG_DYNAMIC_SHAPE
+    g.inputs = [ids[n] for n in og.inputs]
+    g.outputs = [ids[n] for n in og.outputs]
+    for i, n in enumerate(opt.nodes):
+        if opt.flags[i] & NODE_SKIP:
+            continue
+        op = OP_IDS.get(n.op_type, 0)
+        params = bytearray(op_params(n.op_type, n.attrs))
+        if opt.act[i] != E.ACT_NONE and n.op_type == "Conv":
+            params[43] = opt.act[i]
+        g.node(op, [ids[x] for x in n.inputs], [ids[x] for x in n.outputs], bytes(params),
+               E.NODE_FLAG_FUSED if opt.flags[i] & NODE_HAS_ACT else 0)
+    return g

@@ -1,0 +1,139 @@
+"""Graphs for the ONNX -> ENNF conversion checks: the benchmark models at small
+sizes plus graphs that exercise each guard of the reference graph optimizer
+(SPINN/graph_opt.c). Shared by make_golden.py (which runs the reference
+converter on them) and tests/test_converter.py."""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+
+from spinn_amd import ennf as E
+from spinn_amd import models
+from spinn_amd import onnx as X
+from spinn_amd.onnx import OnnxGraph
+
+
+def _w(rng, *shape):
+    return rng.standard_normal(shape).astype(np.float32)
+
+
+def _conv(g, rng, name, x, oc, bias=False):
+    n, c, h, w = g.dims(x)
+    ins = [x, g.weight(f"{name}.w", _w(rng, oc, c, 3, 3))]
+    if bias:
+        ins.append(g.weight(f"{name}.b", _w(rng, oc)))
+    y = g.value(f"{name}.y", (n, oc, h, w))
+    g.node("Conv", ins, [y], dilations=[1, 1], group=1, kernel_shape=[3, 3], pads=[1, 1, 1, 1], strides=[1, 1])
+    return y
+
+
+def _bn(g, rng, name, x):
+    c = g.dims(x)[1]
+    prm = [g.weight(f"{name}.{k}", rng.uniform(0.5, 1.5, c).astype(np.float32))
+           for k in ("scale", "bias", "mean", "var")]
+    y = g.value(f"{name}.y", g.dims(x))
+    g.node("BatchNormalization", [x] + prm, [y], epsilon=1e-3, momentum=0.9)
+    return y
+
+
+def _op(g, op, name, ins, shape=None, **attrs):
+    y = g.value(f"{name}.y", shape or g.dims(ins[0]))
+    g.node(op, ins, [y], **attrs)
+    return y
+
+
+def guard_graph(seed: int = 0) -> OnnxGraph:
+    """One graph, many patterns: which of them fuse is what the reference decides."""
+    rng = np.random.default_rng(seed)
+    g = OnnxGraph()
+    x = g.input("x", (1, 4, 5, 5))
+    # conv+bias+BN+Relu -> one conv (bias replaced by the folded BN bias)
+    a = _op(g, "Relu", "r0", [_bn(g, rng, "bn0", _conv(g, rng, "c0", x, 4, bias=True))])
+    # conv consumed twice: neither BN nor Relu fuses
+    c1 = _conv(g, rng, "c1", a, 4)
+    b1 = _bn(g, rng, "bn1", c1)
+    s1 = _op(g, "Add", "add1", [b1, c1])
+    # BN after a non-conv stays a BatchNormalization node
+    b2 = _bn(g, rng, "bn2", _op(g, "Relu", "r1", [s1]))
+    # Add with an initializer operand: no residual fusion
+    c3 = _conv(g, rng, "c3", b2, 4)
+    k3 = g.weight("k3", _w(rng, 1, 4, 5, 5))
+    s3 = _op(g, "Add", "add3", [c3, k3])
+    # residual produced after the conv: the later conv takes the Add (ADD, no Relu: two consumers)
+    c4 = _conv(g, rng, "c4", s3, 4)
+    c5 = _conv(g, rng, "c5", s3, 4)
+    s4 = _op(g, "Add", "add4", [c4, c5])
+    r4 = _op(g, "Relu", "r4", [s4])
+    t4 = _op(g, "Sigmoid", "t4", [s4])
+    # SiLU with a third consumer of the conv output: not fused
+    c6 = _conv(g, rng, "c6", _op(g, "Mul", "m45", [r4, t4]), 4)
+    sg6 = _op(g, "Sigmoid", "sg6", [c6])
+    m6 = _op(g, "Mul", "m6", [c6, sg6])
+    e6 = _op(g, "Relu", "e6", [c6])
+    # a proper SiLU, and a conv whose output is also a graph output (no Relu fusion)
+    c7 = _conv(g, rng, "c7", _op(g, "Add", "a67", [m6, e6]), 4)
+    sg7 = _op(g, "Sigmoid", "sg7", [c7])
+    m7 = _op(g, "Mul", "m7", [sg7, c7])
+    c8 = _conv(g, rng, "c8", m7, 4)
+    r8 = _op(g, "Relu", "r8", [c8])
+    # residual = graph input, Add + Relu after a BN-folded conv: ADD_RELU
+    c9 = _bn(g, rng, "bn9", _conv(g, rng, "c9", r8, 4))
+    s9 = _op(g, "Add", "add9", [x, c9])
+    r9 = _op(g, "Relu", "r9", [s9])
+    g.output(r9)
+    g.output(c8)
+    return g
+
+
+def dynamic_graph() -> OnnxGraph:
+    """A symbolic batch dimension (ENNF_FLAG_DYNAMIC_SHAPE, dims read as 0)."""
+    rng = np.random.default_rng(3)
+    g = OnnxGraph()
+    x = g.input("x", ("N", 4, 5, 5))
+    w = g.weight("w", _w(rng, 4, 4, 1, 1))
+    y = g.value("y", ("N", 4, 5, 5))
+    g.node("Conv", [x, w], [y], kernel_shape=[1, 1], strides=[1, 1], pads=[0, 0, 0, 0])
+    z = g.value("z", ("N", 4, 5, 5))
+    g.node("Relu", [y], [z])
+    g.output(z)
+    return g
+
+
+# name -> (graph maker, environment of the reference converter, convert() keywords)
+CASES = {
+    "guards": (guard_graph, {}, {}),
+    "dynamic": (dynamic_graph, {}, {}),
+    "conv0": (lambda: models.conv_bn_relu(seed=0)[0].onnx, {}, {}),
+    "gemm": (lambda: models.gemm_model(32, 1000, 2048, seed=1)[0].onnx, {}, {}),
+    "vgg": (lambda: models.vgg_stack(batch=2, seed=3, in_c=16,
+                                     schedule=[(16, 32), (16, 32), (32, 16), (32, 16)])[0].onnx, {}, {}),
+    "resnet_tiny": (lambda: models.resnet(batch=2, seed=0, blocks=(1, 2, 1, 1), hw=64, num_classes=10)[0].onnx,
+                    {}, {}),
+    "resnet_tiny_noadd": (lambda: models.resnet(batch=2, seed=0, blocks=(1, 2, 1, 1), hw=64,
+                                                num_classes=10)[0].onnx,
+                          {"SPINN_DISABLE_CONV_ADD": "1"}, {"conv_add": False}),
+    "yolov10n_64_post": (lambda: models.yolov10n(batch=1, seed=0, hw=64, postprocess=True)[0].onnx, {}, {}),
+    "yolov10n_64_nosilu": (lambda: models.yolov10n(batch=1, seed=0, hw=64)[0].onnx,
+                           {"SPINN_DISABLE_CONV_SILU": "1"}, {"conv_silu": False}),
+    "resnet101_b1": (lambda: models.resnet101(batch=1, seed=0)[0].onnx, {}, {}),
+}
+
+
+def mask_unset(buf: bytes) -> bytes:
+    """Zero the parameter bytes the reference converter leaves unwritten (onnx.UNSET_PARAM_BYTES)."""
+    out = bytearray(buf)
+    m = E.read(bytes(buf))
+    names = {v: k for k, v in X.OP_IDS.items()}
+    off = m["header"]["node_table_offset"]
+    for nd in m["nodes"]:
+        p = off + 8 + 2 * (len(nd["inputs"]) + len(nd["outputs"]))
+        span = X.UNSET_PARAM_BYTES.get(names.get(nd["op"]))
+        if span and len(nd["params"]) >= span[0] + span[1]:
+            out[p + span[0]:p + span[0] + span[1]] = bytes(span[1])
+        off = p + len(nd["params"])
+    return bytes(out)
+
+
+def digest(buf: bytes) -> np.ndarray:
+    return np.frombuffer(hashlib.sha256(buf).digest(), np.uint8)

@@ -5,7 +5,7 @@ with oracle/Makefile (the reference's run_time C sources compiled in place) and
 calls the reference functions on small seeded inputs. Each fixture is an .npz
 of inputs and the reference's outputs (no code), loaded with allow_pickle=False.
 
-    python tests/golden/make_golden.py [planner conv epilogue gemm winograd tensor_ops postproc models]
+    python tests/golden/make_golden.py [planner conv epilogue gemm winograd tensor_ops postproc models converter]
 
 Fixtures:
   planner_offsets.npz   spinn_load + spinn_plan_memory offsets and peak for
@@ -26,6 +26,9 @@ Fixtures:
                         detector's post-processing tail on small seeded inputs
   models_as_shipped.npz spinn_load + spinn_plan + spinn_run of generated models (YOLOv10n at
                         64x64, a 4-block ResNet at 64x64, batch 2): the reference's output and an input fingerprint
+  converter.npz         SHA-256 (and, for small files, the bytes) of the reference converter's
+                        output (SPINN/onnx2ennf.c, oracle/_ref/onnx2ennf) for the .onnx files of
+                        converter_cases.CASES, unwritten parameter bytes zeroed
 """
 from __future__ import annotations
 
@@ -407,10 +410,35 @@ def winograd(L):
     np.savez_compressed(HERE / "winograd.npz", **out)
 
 
+def converter(_L):
+    """SHA-256 of the reference converter's output (SPINN/onnx2ennf.c, built by `make -C oracle ref`)
+    for each graph of converter_cases.CASES, written as an .onnx file by spinn_amd.onnx, with the
+    parameter bytes the converter leaves unwritten zeroed; the small files are kept whole."""
+    import os
+    import subprocess
+    import tempfile
+
+    from tests.golden import converter_cases as CC
+    exe = HERE.parents[1] / "oracle" / "_ref" / "onnx2ennf"
+    out = {}
+    with tempfile.TemporaryDirectory() as td:
+        for name, (make, env, _kw) in CC.CASES.items():
+            src, dst = Path(td) / f"{name}.onnx", Path(td) / f"{name}.ennf"
+            src.write_bytes(make().to_onnx())
+            subprocess.run([str(exe), str(src), str(dst)], check=True, stdout=subprocess.DEVNULL,
+                           env={**os.environ, **env})
+            buf = CC.mask_unset(dst.read_bytes())
+            out[f"{name}_sha256"] = CC.digest(buf)
+            out[f"{name}_size"] = np.array([len(buf)], np.int64)
+            if len(buf) < 64 * 1024:
+                out[f"{name}_bytes"] = np.frombuffer(buf, np.uint8)
+    np.savez_compressed(HERE / "converter.npz", **out)
+
+
 def main():
     L = ref_lib()
     steps = {"planner": planner, "conv": conv_cases, "epilogue": epilogue, "gemm": gemm, "winograd": winograd,
-             "tensor_ops": tensor_ops, "postproc": postproc, "models": models_as_shipped}
+             "tensor_ops": tensor_ops, "postproc": postproc, "models": models_as_shipped, "converter": converter}
     for name in sys.argv[1:] or list(steps):
         steps[name](L)
     for f in sorted(HERE.glob("*.npz")):

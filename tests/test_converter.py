@@ -1,0 +1,141 @@
+"""The ONNX -> ENNF conversion (spinn_amd.onnx) against the reference converter.
+
+Every model the benchmarks and parity tests run is produced by spinn_amd.onnx.convert
+from an exporter-shaped graph. These tests hold its output to the reference
+converter's (SPINN/onnx2ennf.c + SPINN/graph_opt.c) byte for byte:
+  * against the SHA-256 of the reference converter's output for the same .onnx file
+    (tests/golden/converter.npz, written by make_golden.py), always;
+  * against the reference converter itself, run on the file written by
+    OnnxGraph.to_onnx(), where `make -C oracle ref` has built it (oracle/_ref/onnx2ennf).
+Parameter bytes the reference leaves unwritten are zeroed on both sides first."""
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from spinn_amd import ennf as E
+from spinn_amd import onnx as X
+from tests.golden import converter_cases as CC
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLD = np.load(ROOT / "tests" / "golden" / "converter.npz", allow_pickle=False)
+REF_CONVERTER = ROOT / "oracle" / "_ref" / "onnx2ennf"
+
+
+def _first_difference(ref: bytes, ours: bytes) -> str:
+    a, b = E.read(ref), E.read(ours)
+    if a["header"] != b["header"]:
+        return f"header {a['header']} != {b['header']}"
+    for i, (x, y) in enumerate(zip(a["nodes"], b["nodes"])):
+        if x != y:
+            return f"node {i}: {x} != {y}"
+    for k, t in a["tensors"].items():
+        if t != b["tensors"].get(k):
+            return f"tensor {k}: {t} != {b['tensors'].get(k)}"
+    for k, w in a["weights"].items():
+        if not np.array_equal(w, b["weights"].get(k)):
+            return f"weight data of tensor {k}"
+    d = next(i for i in range(min(len(ref), len(ours))) if ref[i] != ours[i]) if len(ref) == len(ours) else -1
+    return f"sizes {len(ref)} / {len(ours)}, first differing byte {d}"
+
+
+@pytest.mark.parametrize("name", list(CC.CASES))
+def test_convert_matches_reference_digest(name):
+    make, _env, kw = CC.CASES[name]
+    ours = CC.mask_unset(X.convert(make(), **kw).to_bytes())
+    assert len(ours) == int(GOLD[f"{name}_size"][0])
+    if f"{name}_bytes" in GOLD.files:
+        ref = GOLD[f"{name}_bytes"].tobytes()
+        assert ours == ref, _first_difference(ref, ours)
+    assert np.array_equal(CC.digest(ours), GOLD[f"{name}_sha256"])
+
+
+@pytest.mark.skipif(not REF_CONVERTER.exists(), reason="reference converter not built (make -C oracle ref)")
+@pytest.mark.parametrize("name", ["guards", "dynamic", "resnet_tiny", "resnet_tiny_noadd", "yolov10n_64_post",
+                                  "yolov10n_64_nosilu"])
+def test_convert_matches_reference_converter(tmp_path, name):
+    make, env, kw = CC.CASES[name]
+    g = make()
+    src, dst = tmp_path / "m.onnx", tmp_path / "m.ennf"
+    src.write_bytes(g.to_onnx())
+    subprocess.run([str(REF_CONVERTER), str(src), str(dst)], check=True, stdout=subprocess.DEVNULL,
+                   env={**os.environ, **env})
+    ref = CC.mask_unset(dst.read_bytes())
+    ours = CC.mask_unset(X.convert(g, **kw).to_bytes())
+    assert ours == ref, _first_difference(ref, ours)
+
+
+def test_guard_graph_fusions():
+    """What the optimizer's guards leave of the guard graph, read back from the file."""
+    g = X.convert(CC.guard_graph())
+    m = E.read(g.to_bytes())
+    names = {t.id: t.name for t in g.tensors}
+    ids = {t.name: t.id for t in g.tensors}
+    convs = {names[n["inputs"][1]].split(".")[0]: E.unpack_conv_params(n["params"])["act"]
+             for n in m["nodes"] if n["op"] == E.OP_CONV}
+    assert convs == {"c0": E.ACT_RELU, "c1": E.ACT_NONE, "c3": E.ACT_NONE, "c4": E.ACT_NONE, "c5": E.ACT_ADD,
+                     "c6": E.ACT_NONE, "c7": E.ACT_SILU, "c8": E.ACT_NONE, "c9": E.ACT_ADD_RELU}
+    ops = [n["op"] for n in m["nodes"]]
+    assert ops.count(E.OP_BN) == 2          # bn1 (conv consumed twice) and bn2 (after a Relu)
+    # c0 had its own bias: the folded bias replaces it as input 2; the old one stays a weight
+    conv = {names[n["inputs"][1]]: n for n in m["nodes"] if n["op"] == E.OP_CONV}
+    c0 = conv["c0.w"]
+    assert names[c0["inputs"][2]] == "bn0.bias" and m["tensors"][ids["c0.b"]]["is_weight"] == 1
+    # the residual is the last input of the fused conv; reference counts are pre-fusion
+    c9 = conv["c9.w"]
+    assert names[c9["inputs"][-1]] == "x" and names[c9["outputs"][0]] == "r9.y"
+    assert m["tensors"][ids["c9.y"]]["ref_count"] == 1 and m["tensors"][ids["x"]]["ref_count"] == 2
+
+
+def test_dynamic_dims_flag():
+    m = E.read(X.convert(CC.dynamic_graph()).to_bytes())
+    assert m["header"]["flags"] == 4
+    assert m["tensors"][m["inputs"][0]]["dims"] == (0, 4, 5, 5)
+
+
+def test_onnx_wire_format_round_trip():
+    """The protobuf writer, decoded by a minimal independent reader: fields and values survive."""
+    g = CC.dynamic_graph()
+    buf = g.to_onnx()
+
+    def fields(b):
+        i, out = 0, []
+        while i < len(b):
+            key, i = _varint(b, i)
+            fno, wt = key >> 3, key & 7
+            if wt == 0:
+                v, i = _varint(b, i)
+            elif wt == 2:
+                n, i = _varint(b, i)
+                v, i = b[i:i + n], i + n
+            elif wt == 5:
+                v, i = b[i:i + 4], i + 4
+            else:
+                raise AssertionError(wt)
+            out.append((fno, v))
+        return out
+
+    top = dict(fields(buf))
+    assert top[1] == 8                      # ir_version
+    graph = fields(top[7])
+    nodes = [dict(fields(v)) for f, v in graph if f == 1]
+    assert [n[4] for n in nodes] == [b"Conv", b"Relu"]
+    init = [dict(fields(v)) for f, v in graph if f == 5]
+    assert init[0][8] == b"w" and init[0][2] == 1
+    assert np.array_equal(np.frombuffer(init[0][9], np.float32), g.initializers["w"].ravel())
+    inp = dict(fields(next(v for f, v in graph if f == 11)))
+    dims = [dict(fields(v)) for f, v in fields(dict(fields(dict(fields(inp[2]))[1]))[2])]
+    assert dims[0] == {2: b"N"} and [d[1] for d in dims[1:]] == [4, 5, 5]
+
+
+def _varint(b, i):
+    v = s = 0
+    while True:
+        c = b[i]
+        i += 1
+        v |= (c & 0x7F) << s
+        s += 7
+        if not c & 0x80:
+            return v, i

@@ -37,10 +37,12 @@ def test_ennf_roundtrip(tmp_path):
     for nd, gn in zip(m["nodes"], g.nodes):
         assert nd["op"] == gn.op and nd["inputs"] == gn.inputs and nd["outputs"] == gn.outputs
         assert nd["params"] == gn.params and nd["flags"] == gn.flags
+    # reference counts are those of the graph before fusion (SPINN/onnx2ennf.c:232-241)
+    ids = {t.name: t.id for t in g.tensors}
     ref = {t.id: 0 for t in g.tensors}
-    for n in g.nodes:
+    for n in g.onnx.nodes:
         for i in n.inputs:
-            ref[i] += 1
+            ref[ids[i]] += 1
     for t in g.tensors:
         mt = m["tensors"][t.id]
         assert mt["dims"] == t.dims and mt["ref_count"] == ref[t.id] and mt["is_weight"] == int(t.is_weight)
