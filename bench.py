@@ -40,7 +40,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "conv-layer fp32 GFLOP/s (% MFMA peak); ResNet-101 images/sec @ b1/b32, 1 GPU"
 PEAK_FP32_MFMA = 157.3e12  # MI355X dense fp32 matrix peak, FLOP/s
-ALGO_NAMES = {1: "implicit_gemm", 2: "winograd", 3: "direct"}
+ALGO_NAMES = {1: "implicit_gemm", 2: "winograd", 3: "direct", 4: "winograd_f43"}
 
 
 def host_threads() -> int:
@@ -95,11 +95,11 @@ def algo_of(N, r, policy) -> int:
     d = N.ConvDesc(r["n"], r["c"], r["h"], r["w"], r["oc"], r["oh"], r["ow"], r["kh"], r["kw"], r["sh"], r["sw"],
                    r["ph"], r["pw"], r["group"], r["act"], 0, 0)
     a = N.lib().spinn_hip_conv_select_algo(C.byref(d))
-    if a == N.ALGO_WINOGRAD and policy == N.POLICY_IGEMM:
+    if a in (N.ALGO_WINOGRAD, N.ALGO_WINOGRAD_F43) and policy == N.POLICY_IGEMM:
         return N.ALGO_IMPLICIT_GEMM
     if a == N.ALGO_IMPLICIT_GEMM and policy == N.POLICY_WINOGRAD and r["kh"] == 3 and r["kw"] == 3 \
             and r["sh"] == 1 and r["sw"] == 1 and r["group"] == 1:
-        return N.ALGO_WINOGRAD
+        return N.ALGO_WINOGRAD_F43
     return a
 
 

@@ -31,7 +31,8 @@ enum {
     SPINN_CONV_ALGO_AUTO = 0,
     SPINN_CONV_ALGO_IMPLICIT_GEMM = 1, /* im2col fused into the tile load; 1x1 s1 p0 reads X directly */
     SPINN_CONV_ALGO_WINOGRAD = 2,      /* F(2x2,3x3), 3x3 s1 group 1 only; needs packed_w */
-    SPINN_CONV_ALGO_DIRECT = 3         /* grouped / depthwise direct convolution */
+    SPINN_CONV_ALGO_DIRECT = 3,        /* grouped / depthwise direct convolution */
+    SPINN_CONV_ALGO_WINOGRAD_F43 = 4   /* F(4x4,3x3), same eligibility and operands as WINOGRAD */
 };
 
 /*

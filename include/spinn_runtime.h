@@ -97,7 +97,7 @@ typedef struct {
 /* Which algorithm eligible 3x3 stride-1 convolutions use (spinn_set_conv_policy). */
 #define SPINN_CONV_POLICY_AUTO 0     /* per-shape choice of the compute layer */
 #define SPINN_CONV_POLICY_IGEMM 1    /* always the implicit GEMM */
-#define SPINN_CONV_POLICY_WINOGRAD 2 /* Winograd F(2x2,3x3) wherever eligible */
+#define SPINN_CONV_POLICY_WINOGRAD 2 /* Winograd wherever eligible (F(4x4,3x3) unless AUTO picked F(2x2,3x3)) */
 
 /* Planner error codes (SPINN/run_time/spinn_memory_planner.h:17-20). */
 #define SPINN_MEM_OK 0

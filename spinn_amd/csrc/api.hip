@@ -32,11 +32,28 @@ static int env_winograd() {
     return v;
 }
 
-static bool winograd_pays(const SpinnHipConvDesc *d) {
-    // Winograd cuts GEMM flops 2.25x but moves V (4x the input) and M (4x the
-    // output) through memory in three launches; measured on MI355X it wins
-    // from 128 channels in and out once there are >= 256 2x2 output tiles
-    // (1.6x at 128@28x28 batch 32), and loses at 64 channels or at batch 1.
+static int env_winograd_tile() {
+    // SPINN_WINOGRAD_TILE=2|4 picks the Winograd tile under AUTO; unset = F(4,3).
+    static int v = [] {
+        const char *e = std::getenv("SPINN_WINOGRAD_TILE");
+        return (e && e[0] == '2') ? 2 : 4;
+    }();
+    return v;
+}
+
+static bool winograd_pays(const SpinnHipConvDesc *d, int m) {
+    // Winograd moves V and M through memory in three launches. F(2,3) cuts GEMM flops
+    // 2.25x with V / M 4x the input / output; measured on MI355X it wins from 128
+    // channels in and out once there are >= 256 2x2 output tiles (1.6x at 128@28x28
+    // batch 32). F(4,3) cuts flops 4x with V / M 2.25x the input / output and wins from
+    // 128 channels with >= 128 4x4 tiles (512@7x7 batch 32: 45 against 50 us for F(2,3)),
+    // and at 64 channels with >= 256 tiles (64@56x56 batch 32: 72 against 92 us for the
+    // implicit GEMM; at batch 1, 196 tiles, it loses).
+    if (m == 4) {
+        const int64_t tiles = (int64_t)d->n * ((d->oh + 3) / 4) * ((d->ow + 3) / 4);
+        const bool wide = d->c >= 128 && d->oc >= 128;
+        return d->c >= 64 && d->oc >= 64 && tiles >= (wide ? 128 : 256);
+    }
     const int64_t tiles = (int64_t)d->n * ((d->oh + 1) / 2) * ((d->ow + 1) / 2);
     return d->c >= 128 && d->oc >= 128 && tiles >= 256;
 }
@@ -49,7 +66,9 @@ static int select_algo(const SpinnHipConvDesc *d) {
     if (stem_conv_pays(d)) return SPINN_CONV_ALGO_DIRECT;
     if (winograd_eligible(d)) {
         const int w = env_winograd();
-        if (w == 1 || (w < 0 && winograd_pays(d))) return SPINN_CONV_ALGO_WINOGRAD;
+        const int m = env_winograd_tile();
+        if (w == 1 || (w < 0 && winograd_pays(d, m)))
+            return m == 4 ? SPINN_CONV_ALGO_WINOGRAD_F43 : SPINN_CONV_ALGO_WINOGRAD;
     }
     return SPINN_CONV_ALGO_IMPLICIT_GEMM;
 }
@@ -81,7 +100,8 @@ size_t spinn_hip_conv_workspace_size(const SpinnHipConvDesc *d) {
     if (!conv_desc_ok(d)) return 0;
     switch (select_algo(d)) {
     case SPINN_CONV_ALGO_IMPLICIT_GEMM: return igemm_workspace_bytes(d);
-    case SPINN_CONV_ALGO_WINOGRAD: return winograd_eligible(d) ? winograd_workspace_bytes(d) : 0;
+    case SPINN_CONV_ALGO_WINOGRAD: return winograd_eligible(d) ? winograd_workspace_bytes(d, 2) : 0;
+    case SPINN_CONV_ALGO_WINOGRAD_F43: return winograd_eligible(d) ? winograd_workspace_bytes(d, 4) : 0;
     default: return 0;
     }
 }
@@ -90,7 +110,10 @@ size_t spinn_hip_conv_packed_size(const SpinnHipConvDesc *d) {
     if (!conv_desc_ok(d)) return 0;
     switch (select_algo(d)) {
     case SPINN_CONV_ALGO_IMPLICIT_GEMM: return (size_t)igemm_packed_floats(d) * sizeof(float);
-    case SPINN_CONV_ALGO_WINOGRAD: return winograd_eligible(d) ? (size_t)winograd_packed_floats(d) * sizeof(float) : 0;
+    case SPINN_CONV_ALGO_WINOGRAD:
+        return winograd_eligible(d) ? (size_t)winograd_packed_floats(d, 2) * sizeof(float) : 0;
+    case SPINN_CONV_ALGO_WINOGRAD_F43:
+        return winograd_eligible(d) ? (size_t)winograd_packed_floats(d, 4) * sizeof(float) : 0;
     default: return 0;
     }
 }
@@ -98,11 +121,13 @@ size_t spinn_hip_conv_packed_size(const SpinnHipConvDesc *d) {
 int spinn_hip_conv_pack_weights(const SpinnHipConvDesc *d, const float *w, float *packed, void *stream) {
     if (!conv_desc_ok(d) || !w || !packed) return SPINN_HIP_EINVAL;
     hipStream_t st = (hipStream_t)stream;
-    switch (select_algo(d)) {
+    const int algo = select_algo(d);
+    switch (algo) {
     case SPINN_CONV_ALGO_IMPLICIT_GEMM: return igemm_pack(d, w, packed, st);
     case SPINN_CONV_ALGO_WINOGRAD:
+    case SPINN_CONV_ALGO_WINOGRAD_F43:
         if (!winograd_eligible(d)) return SPINN_HIP_EUNSUPPORTED;
-        return winograd_pack(d, w, packed, st);
+        return winograd_pack(d, algo == SPINN_CONV_ALGO_WINOGRAD ? 2 : 4, w, packed, st);
     default: return SPINN_HIP_OK; // reads w directly
     }
 }
@@ -114,14 +139,17 @@ int spinn_hip_conv(const SpinnHipConvDesc *d, const float *x, const float *w, co
     const bool has_res = d->act == SPINN_ACT_ADD || d->act == SPINN_ACT_ADD_RELU;
     if (has_res != (residual != nullptr)) return SPINN_HIP_EINVAL;
     hipStream_t st = (hipStream_t)stream;
-    switch (select_algo(d)) {
+    const int algo = select_algo(d);
+    switch (algo) {
     case SPINN_CONV_ALGO_IMPLICIT_GEMM:
         if (!packed_w) return SPINN_HIP_EINVAL;
         return igemm_conv(d, x, packed_w, bias, residual, y, workspace, workspace_bytes, st);
     case SPINN_CONV_ALGO_WINOGRAD:
+    case SPINN_CONV_ALGO_WINOGRAD_F43:
         if (!winograd_eligible(d)) return SPINN_HIP_EUNSUPPORTED;
         if (!packed_w) return SPINN_HIP_EINVAL;
-        return winograd_conv(d, x, packed_w, bias, residual, y, workspace, workspace_bytes, st);
+        return winograd_conv(d, algo == SPINN_CONV_ALGO_WINOGRAD ? 2 : 4, x, packed_w, bias, residual, y,
+                             workspace, workspace_bytes, st);
     case SPINN_CONV_ALGO_DIRECT:
         if (!w) return SPINN_HIP_EINVAL;
         return direct_conv(d, x, w, bias, residual, y, st);

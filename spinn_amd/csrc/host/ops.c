@@ -140,12 +140,13 @@ int spinn_conv_desc_from_tensors(SpinnTensor **in, int n_in, const void *params,
     d->algo = SPINN_CONV_ALGO_AUTO;
     int algo = spinn_hip_conv_select_algo(d);
     if (algo < 0) return -1;
-    if (algo == SPINN_CONV_ALGO_WINOGRAD && g_spinn_exec.conv_policy == SPINN_CONV_POLICY_IGEMM) {
+    const int wino = algo == SPINN_CONV_ALGO_WINOGRAD || algo == SPINN_CONV_ALGO_WINOGRAD_F43;
+    if (wino && g_spinn_exec.conv_policy == SPINN_CONV_POLICY_IGEMM) {
         algo = SPINN_CONV_ALGO_IMPLICIT_GEMM;
     } else if (algo == SPINN_CONV_ALGO_IMPLICIT_GEMM && g_spinn_exec.conv_policy == SPINN_CONV_POLICY_WINOGRAD) {
-        d->algo = SPINN_CONV_ALGO_WINOGRAD;
+        d->algo = SPINN_CONV_ALGO_WINOGRAD_F43;
         if (spinn_hip_conv_packed_size(d) == 0) algo = SPINN_CONV_ALGO_IMPLICIT_GEMM; /* not eligible */
-        else algo = SPINN_CONV_ALGO_WINOGRAD;
+        else algo = SPINN_CONV_ALGO_WINOGRAD_F43;
     }
     d->algo = algo;
     *bias = (n_real > 2 && in[2] && in[2]->data) ? (const float *)in[2]->data : NULL;

@@ -66,12 +66,12 @@ size_t gemm_workspace_bytes(const SpinnHipGemmDesc *d);
 int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const float *C, float *Y, void *ws,
              size_t ws_bytes, hipStream_t st);
 
-// Winograd F(2x2,3x3) (winograd.hip)
+// Winograd F(2x2,3x3) / F(4x4,3x3) (winograd.hip); m = output tile edge, 2 or 4
 bool winograd_eligible(const SpinnHipConvDesc *d);
-int64_t winograd_packed_floats(const SpinnHipConvDesc *d);
-int winograd_pack(const SpinnHipConvDesc *d, const float *w, float *packed, hipStream_t st);
-size_t winograd_workspace_bytes(const SpinnHipConvDesc *d);
-int winograd_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+int64_t winograd_packed_floats(const SpinnHipConvDesc *d, int m);
+int winograd_pack(const SpinnHipConvDesc *d, int m, const float *w, float *packed, hipStream_t st);
+size_t winograd_workspace_bytes(const SpinnHipConvDesc *d, int m);
+int winograd_conv(const SpinnHipConvDesc *d, int m, const float *x, const float *packed, const float *bias,
                   const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st);
 
 // grouped / depthwise direct convolution (direct_conv.hip)

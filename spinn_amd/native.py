@@ -25,7 +25,7 @@ SPINN_HIP_EINVAL = -1
 SPINN_HIP_EUNSUPPORTED = -2
 SPINN_HIP_EWORKSPACE = -3
 
-ALGO_AUTO, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_DIRECT = 0, 1, 2, 3
+ALGO_AUTO, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_DIRECT, ALGO_WINOGRAD_F43 = 0, 1, 2, 3, 4
 ACT_NONE, ACT_RELU, ACT_CLIP, ACT_SILU, ACT_ADD, ACT_ADD_RELU = 0, 1, 2, 3, 4, 5
 ENNF_MAX_DIMS = 8
 POLICY_AUTO, POLICY_IGEMM, POLICY_WINOGRAD = 0, 1, 2

@@ -50,6 +50,11 @@ CASES = [
     ("winograd_add_relu", 2, 64, 28, 28, 64, 3, 1, 1, 1, 5, 2),
     ("winograd_odd", 1, 16, 15, 13, 8, 3, 1, 1, 1, 1, 2),
     ("winograd_c256", 1, 256, 14, 14, 256, 3, 1, 1, 1, 1, 2),
+    ("winograd43_add_relu", 2, 64, 28, 28, 64, 3, 1, 1, 1, 5, 4),   # F(4x4,3x3)
+    ("winograd43_odd", 1, 16, 15, 13, 8, 3, 1, 1, 1, 1, 4),          # partial 4x4 tiles at both edges
+    ("winograd43_c256", 1, 256, 14, 14, 256, 3, 1, 1, 1, 1, 4),
+    ("winograd43_c512_add", 2, 512, 7, 7, 512, 3, 1, 1, 1, 4, 4),
+    ("winograd43_p0_silu", 1, 8, 10, 12, 40, 3, 1, 0, 1, 3, 4),      # no padding: 8x10 output
 ]
 
 

@@ -206,11 +206,14 @@ def test_conv_algo_selection(native):
         d = native.ConvDesc(n, c, h, w, oc, oh, oh, k, k, s, s, p, p, g, 0, 0, 0)
         return L.spinn_hip_conv_select_algo(C.byref(d))
 
-    assert algo(1, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM
-    assert algo(32, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_WINOGRAD
-    assert algo(32, 128, 28, 28, 128, 3, 1, 1, 1) == native.ALGO_WINOGRAD
+    assert algo(32, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43
+    assert algo(32, 128, 28, 28, 128, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43
     assert algo(1, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM  # 49 output tiles: too few
-    assert algo(32, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM   # 64 channels
+    assert algo(32, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43    # 64 channels, 6272 4x4 tiles
+    assert algo(1, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM    # 64 channels, 196 4x4 tiles
+    assert algo(32, 512, 7, 7, 512, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43    # 128 4x4 tiles
+    assert algo(1, 128, 28, 28, 128, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM  # 49 4x4 tiles
+    assert algo(8, 32, 80, 80, 32, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM    # 32 channels
     assert algo(1, 256, 14, 14, 256, 3, 2, 1, 1) == native.ALGO_IMPLICIT_GEMM
     assert algo(1, 128, 20, 20, 128, 3, 2, 1, 128) == native.ALGO_DIRECT
     assert algo(16, 3, 640, 640, 16, 3, 2, 1, 1) == native.ALGO_DIRECT          # RGB stem into 16 channels
