@@ -210,12 +210,12 @@ class Graph:
         blob = bytearray()
         n_weights = 0
         for t in self.tensors:
-            if t.is_weight:
-                raw = t.data.tobytes()
+            raw = t.data.tobytes() if t.is_weight else b""
+            n_weights += 1 if t.is_weight else 0
+            if raw:
                 entries += _ENTRY.pack(t.id, 0, len(blob), len(raw), 0)
                 blob += raw
-                n_weights += 1
-            else:
+            else:  # activations and empty initializers: a zero entry (onnx2ennf.c:451-456, 500)
                 entries += _ENTRY.pack(t.id, 0, 0, 0, 0)
         hdr = _HDR.pack(ENNF_MAGIC, 2, 0, len(self.nodes), nt, n_weights, len(blob), len(self.inputs),
                         len(self.outputs), self.opset, self.flags, graph_meta_off, node_off, meta_off, weight_off, 0,

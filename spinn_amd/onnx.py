@@ -312,11 +312,12 @@ class _Opt:
             if j is None or self.nodes[j].op_type != "BatchNormalization":
                 continue
             bn = self.nodes[j]
-            if len(bn.inputs) < 5 or any(bn.inputs[k] not in self.init for k in range(1, 5)):
-                continue
+            if len(bn.inputs) < 5 or any(self.init.get(bn.inputs[k]) is None or self.init[bn.inputs[k]].size == 0
+                                         for k in range(1, 5)):
+                continue   # parameters must be initializers with data (graph_opt.c:31-45, 140-143)
             scale, beta, mean, var = (self.init[bn.inputs[k]] for k in range(1, 5))
             eps = np.float32(bn.attrs.get("epsilon", 1e-5))
-            if len(conv.inputs) < 2 or conv.inputs[1] not in self.init:
+            if len(conv.inputs) < 2 or conv.inputs[1] not in self.init or self.init[conv.inputs[1]].size == 0:
                 continue
             w = self.init[conv.inputs[1]]
             oc = w.shape[0] if w.ndim else 0
@@ -324,6 +325,8 @@ class _Opt:
                 continue
             has_bias = len(conv.inputs) >= 3 and conv.inputs[2] != ""
             b_old = self.init.get(conv.inputs[2]) if has_bias else None
+            if b_old is not None and b_old.size == 0:
+                b_old = None
             # in float32, operation by operation, as the C loop computes it (graph_opt.c:181-198)
             f = (scale.reshape(-1) / np.sqrt(var.reshape(-1) + eps)).astype(np.float32)
             w.reshape(oc, -1)[...] *= f[:, None]

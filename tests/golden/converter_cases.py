@@ -81,7 +81,11 @@ def guard_graph(seed: int = 0) -> OnnxGraph:
     c9 = _bn(g, rng, "bn9", _conv(g, rng, "c9", r8, 4))
     s9 = _op(g, "Add", "add9", [x, c9])
     r9 = _op(g, "Relu", "r9", [s9])
-    g.output(r9)
+    # Resize with an empty roi initializer (no payload: a zero weight entry) and a scales initializer
+    roi = g.weight("roi", np.zeros((0,), np.float32))
+    sc = g.weight("scales", np.array([1, 1, 2, 2], np.float32))
+    up = _op(g, "Resize", "up", [r9, roi, sc], shape=(1, 4, 10, 10), mode="nearest")
+    g.output(up)
     g.output(c8)
     return g
 
