@@ -139,3 +139,28 @@ def _varint(b, i):
         s += 7
         if not c & 0x80:
             return v, i
+
+
+@pytest.mark.skipif(not REF_CONVERTER.exists(), reason="reference converter not built (make -C oracle ref)")
+def test_runtime_loads_reference_converter_output(native, tmp_path):
+    """A file written by the reference converter itself loads into this runtime and plans to the
+    same arena offsets and peak as the file spinn_amd.onnx.convert writes for the same graph."""
+    from spinn_amd import models
+    g, _ = models.yolov10n(batch=1, seed=0, hw=64, postprocess=True)
+    src, ref_path = tmp_path / "m.onnx", tmp_path / "ref.ennf"
+    src.write_bytes(g.onnx.to_onnx())
+    subprocess.run([str(REF_CONVERTER), str(src), str(ref_path)], check=True, stdout=subprocess.DEVNULL)
+    ours_path = g.write(tmp_path / "ours.ennf")
+    L = native.lib()
+    plans = []
+    for path in (ref_path, ours_path):
+        ctx = L.spinn_load(str(path).encode())
+        assert ctx
+        try:
+            peak = L.spinn_plan_memory(ctx, 0)
+            c = ctx.contents
+            assert peak > 0 and c.num_nodes == len(g.nodes)
+            plans.append((peak, [c.tensors[i].offset for i in range(c.num_tensors)]))
+        finally:
+            L.spinn_free(ctx)
+    assert plans[0] == plans[1]
