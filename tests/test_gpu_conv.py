@@ -46,6 +46,8 @@ CASES = [
     ("depthwise_ragged_s1", 3, 16, 37, 45, 16, 3, 1, 1, 16, 1, 0),   # tiles past the plane edge
     ("depthwise5x5_s1", 1, 8, 19, 70, 8, 5, 1, 2, 8, 0, 0),
     ("depthwise_s2_ragged", 2, 12, 41, 67, 12, 3, 2, 1, 12, 3, 0),
+    ("depthwise_large_plane", 1, 4, 160, 161, 4, 3, 1, 1, 4, 1, 0),   # 5 x 6 tiles, ragged right edge
+    ("depthwise_tiny_planes", 4, 96, 7, 5, 96, 3, 1, 1, 96, 4, 0),    # 384 planes of one partial tile, residual
     ("grouped_direct_cg2", 1, 16, 12, 12, 8, 3, 1, 1, 8, 1, 0),      # two input channels per group: general kernel
     ("winograd_add_relu", 2, 64, 28, 28, 64, 3, 1, 1, 1, 5, 2),
     ("winograd_odd", 1, 16, 15, 13, 8, 3, 1, 1, 1, 1, 2),
