@@ -1,10 +1,13 @@
 """End-to-end GPU parity: ENNF models through spinn_load / spinn_plan / spinn_run
 (every conv, Gemm and glue op on the device, activations in one HBM arena)
 against the oracle's CPU run of the same file and input."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
 from oracle import oracle as O
+from spinn_amd import ennf as E
 from spinn_amd import models
 from spinn_amd import native as N
 from spinn_amd.runtime import Session
@@ -63,6 +66,28 @@ def test_resnet101_b1(hip, tmp_path):
     y, _, ref = _run_both(tmp_path, g, x, "r101")
     print(f"[r101 b1] |ref|max={np.abs(ref).max():.3e}", flush=True)
     assert_parity(y, ref, what="resnet101 b1")
+
+
+def test_resnet101_b4_winograd_f43(hip, tmp_path):
+    """Batch 4: AUTO runs the 3x3 stride-1 convs of stages 1 and 2 (64@56x56, 128@28x28) as
+    Winograd F(4x4,3x3); the 101-layer result stays within the bound of the oracle's
+    direct (im2col) convolution."""
+    g, x = models.resnet101(batch=4, seed=2)
+    algos = []
+    L = N.lib()
+    for nd in (n for n in g.nodes if n.op == E.OP_CONV):
+        p = E.unpack_conv_params(nd.params)
+        n, c, h, w = g.dims(nd.inputs[0])
+        oc, _, kh, kw = g.dims(nd.inputs[1])
+        _, _, oh, ow = g.dims(nd.outputs[0])
+        d = N.ConvDesc(n, c, h, w, oc, oh, ow, kh, kw, p["strides"][0], p["strides"][1], p["pads"][0], p["pads"][1],
+                       p["group"] or 1, p["act"], 0, 0)
+        algos.append(L.spinn_hip_conv_select_algo(C.byref(d)))
+    assert algos.count(N.ALGO_WINOGRAD_F43) == 6
+    y, y2, ref = _run_both(tmp_path, g, x, "r101b4")
+    print(f"[r101 b4] |ref|max={np.abs(ref).max():.3e}", flush=True)
+    assert_parity(y, ref, what="resnet101 b4 with F(4x4,3x3)")
+    assert np.array_equal(y, y2)
 
 
 def test_resnet101_b1_graph_replay(hip, tmp_path):
