@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256) void direct_conv_kernel(const float *__restric
 // outputs whose window covers it.
 constexpr int kDwTH = 32, kDwTW = 32, kDwRows = 4;
 
-template <int K, int S>
+template <int K, int S, bool PF>
 __global__ __launch_bounds__(256) void dw_tiled_kernel(const float *__restrict__ x, const float *__restrict__ w,
                                                        const float *__restrict__ bias, const float *__restrict__ res,
                                                        float *__restrict__ y, SpinnHipConvDesc d, int tiles_w,
@@ -76,19 +76,51 @@ __global__ __launch_bounds__(256) void dw_tiled_kernel(const float *__restrict__
     const int oh0 = th * kDwTH + ty * kDwRows, ow = tw * kDwTW + tx;
     const int ih0 = th * kDwTH * S - d.ph, iw0 = tw * kDwTW * S - d.pw;
     const int64_t hw = (int64_t)d.h * d.w, ohw = (int64_t)d.oh * d.ow;
-    for (int64_t plane = blockIdx.y; plane < planes; plane += gridDim.y) {
-        const int c = (int)(plane % d.c);
-        const float *xp = x + plane * hw;
-        for (int e = threadIdx.x; e < IH * IW; e += 256) {
+    // PF (planes of >= 4 tiles, several planes per workgroup): the window of the workgroup's
+    // next plane is loaded into registers while this one is computed and stored.
+    constexpr int NE = (IH * IW + 255) / 256;
+    float v[PF ? NE : 1];
+    auto load_window = [&](int64_t pl) {
+        const float *xp = x + pl * hw;
+#pragma unroll
+        for (int u = 0; u < NE; ++u) {
+            const int e = threadIdx.x + u * 256;
             const int r = e / IW, q = e - r * IW;
             const int ih = ih0 + r, iw = iw0 + q;
-            tile[r * LW + q] = ((unsigned)ih < (unsigned)d.h && (unsigned)iw < (unsigned)d.w) ? xp[(int64_t)ih * d.w + iw]
-                                                                                               : 0.f;
+            v[u] = (e < IH * IW && (unsigned)ih < (unsigned)d.h && (unsigned)iw < (unsigned)d.w)
+                       ? xp[(int64_t)ih * d.w + iw]
+                       : 0.f;
+        }
+    };
+    if constexpr (PF) {
+        if ((int64_t)blockIdx.y < planes) load_window(blockIdx.y);
+    }
+    for (int64_t plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        const int c = (int)(plane % d.c);
+        if constexpr (PF) {
+#pragma unroll
+            for (int u = 0; u < NE; ++u) {
+                const int e = threadIdx.x + u * 256;
+                const int r = e / IW, q = e - r * IW;
+                if (e < IH * IW) tile[r * LW + q] = v[u];
+            }
+        } else {
+            const float *xp = x + plane * hw;
+            for (int e = threadIdx.x; e < IH * IW; e += 256) {
+                const int r = e / IW, q = e - r * IW;
+                const int ih = ih0 + r, iw = iw0 + q;
+                tile[r * LW + q] = ((unsigned)ih < (unsigned)d.h && (unsigned)iw < (unsigned)d.w)
+                                       ? xp[(int64_t)ih * d.w + iw]
+                                       : 0.f;
+            }
         }
         float wk[K * K];
 #pragma unroll
         for (int i = 0; i < K * K; ++i) wk[i] = w[(int64_t)c * K * K + i];
         __syncthreads();
+        if constexpr (PF) {
+            if (plane + gridDim.y < planes) load_window(plane + gridDim.y);
+        }
         float acc[kDwRows];
 #pragma unroll
         for (int r = 0; r < kDwRows; ++r) acc[r] = 0.f;
@@ -203,8 +235,19 @@ static int launch_dw(const SpinnHipConvDesc *d, const float *x, const float *w, 
                      float *y, hipStream_t st) {
     const int tiles_h = (d->oh + kDwTH - 1) / kDwTH, tiles_w = (d->ow + kDwTW - 1) / kDwTW;
     const int64_t planes = (int64_t)d->n * d->c;
-    dim3 grid((unsigned)(tiles_h * tiles_w), (unsigned)std::min<int64_t>(planes, 65535));
-    hipLaunchKernelGGL((dw_tiled_kernel<K, S>), grid, dim3(256), 0, st, x, w, bias, res, y, *d, tiles_w, planes);
+    const int64_t tiles = (int64_t)tiles_h * tiles_w;
+    if (tiles >= 4) {
+        // Measured on YOLOv10n batch 16: planes of >= 4 tiles gain from up to 4 planes per
+        // workgroup with the next window prefetched (80x80: 22.1 -> 19.3 us, 80->40 stride 2:
+        // 36.0 -> 29.4 us); one-tile planes lose, so they keep one plane per workgroup.
+        const int64_t gy = std::min<int64_t>({planes, (int64_t)65535,
+                                              std::max<int64_t>((planes + 3) / 4, (4096 + tiles - 1) / tiles)});
+        hipLaunchKernelGGL((dw_tiled_kernel<K, S, true>), dim3((unsigned)tiles, (unsigned)gy), dim3(256), 0, st, x,
+                           w, bias, res, y, *d, tiles_w, planes);
+    } else {
+        hipLaunchKernelGGL((dw_tiled_kernel<K, S, false>), dim3((unsigned)tiles, (unsigned)std::min<int64_t>(planes, 65535)),
+                           dim3(256), 0, st, x, w, bias, res, y, *d, tiles_w, planes);
+    }
     return check_launch();
 }
 
