@@ -18,6 +18,10 @@ graph). Prints ONE JSON line:
                     recorded around every node of K profiled model passes)
   conv_*            the per-node-event aggregate over every conv layer
                     (Winograd layers credited at the direct-conv FLOP count)
+  other_configs     config 0 (one Conv3x3+BN+ReLU), the Gemm sweep, the VGG
+                    3x3 stack (implicit GEMM vs Winograd), YOLOv10n at batch 1
+                    and 16 with operator families and the depthwise layers'
+                    achieved HBM bandwidth (live back-to-back launches)
   cpu_baseline      the reference's own CPU runtime (or the oracle's
                     restatement when the reference build is absent) on this
                     host's cores, ResNet-101 batch 1, a bounded sample
@@ -254,6 +258,15 @@ def yolo_bench(N, Session, models, tmp: Path, reps: int) -> dict:
                 f = fam.setdefault(k, [0, 0.0])
                 f[0] += 1
                 f[1] += float(node_ms[i])
+            dw = [r for r in conv_table(g) if r["group"] > 1 and r["group"] == r["c"] == r["oc"]]
+            dw_ms, _, dw_b, n_dw = conv_kernels_live(N, dw, N.ALGO_DIRECT)
+            if dw_ms > 0:
+                ent["depthwise_bandwidth"] = {
+                    "layers": n_dw, "bytes": int(dw_b), "kernel_us": round(dw_ms * 1e3, 1),
+                    "achieved": round(dw_b / (dw_ms * 1e-3) / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                    "frac": round(dw_b / (dw_ms * 1e-3) / 8e12, 4),
+                    "method": "input + weights + output (+ residual) bytes of the depthwise layers / their "
+                              "kernel time, each layer launched 10x back to back between HIP events"}
             ent["node_ms_total"] = round(float(node_ms.sum()), 4)
             ent["families_ms"] = {k: {"nodes": v[0], "ms": round(v[1], 4)}
                                   for k, v in sorted(fam.items(), key=lambda kv: -kv[1][1])}
@@ -348,54 +361,61 @@ def gemm_compare(reps: int = 5) -> None:
     print(json.dumps({"gemm_compare": True, "torch_fp32_matmul_us": lib_us}), flush=True)
 
 
-def igemm_kernel_live(N, rows, policy, reps: int = 10):
-    """Live kernel time of the implicit-GEMM conv layers: every distinct layer shape of the pass
-    is launched through spinn_hip_conv `reps` times back to back between two HIP events on the
-    stream the kernel runs on (the null stream), so the figure carries no event or launch gap
-    between nodes, unlike the per-node event pass. Returns (kernel ms per pass summed over the
-    layers, direct-conv FLOPs per pass, layers)."""
+def conv_kernels_live(N, rows, algo: int, reps: int = 10):
+    """Live kernel time of a set of conv layers: every distinct layer shape is launched through
+    spinn_hip_conv with algorithm `algo`, `reps` times back to back between two HIP events on
+    the stream the kernel runs on (the null stream), so the figure carries no event or launch
+    gap between nodes, unlike the per-node event pass. Returns (kernel ms summed over the
+    layers, direct-conv FLOPs, algorithmic bytes - input, weights, output, residual - and the
+    number of layers)."""
     import ctypes as C
     from spinn_amd.devbuf import DeviceBuffer, time_launches
     L = N.lib()
-    ig = [r for r in rows if algo_of(N, r, policy) == N.ALGO_IMPLICIT_GEMM]
-    if not ig:
-        return 0.0, 0.0, 0
+    if not rows:
+        return 0.0, 0.0, 0.0, 0
     fields = ("n", "c", "h", "w", "oc", "oh", "ow", "kh", "kw", "sh", "sw", "ph", "pw", "group", "act")
     shapes = {}
-    for r in ig:
+    for r in rows:
         shapes.setdefault(tuple(r[f] for f in fields), []).append(r)
     nbytes = lambda *dims: 4 * int(np.prod(dims))  # noqa: E731
-    bufs = dict(x=max(nbytes(r["n"], r["c"], r["h"], r["w"]) for r in ig),
-                y=max(nbytes(r["n"], r["oc"], r["oh"], r["ow"]) for r in ig),
-                w=max(nbytes(r["oc"], r["c"] // r["group"], r["kh"], r["kw"]) for r in ig),
-                b=max(nbytes(r["oc"]) for r in ig))
+    bufs = dict(x=max(nbytes(r["n"], r["c"], r["h"], r["w"]) for r in rows),
+                y=max(nbytes(r["n"], r["oc"], r["oh"], r["ow"]) for r in rows),
+                w=max(nbytes(r["oc"], r["c"] // r["group"], r["kh"], r["kw"]) for r in rows),
+                b=max(nbytes(r["oc"]) for r in rows))
     bufs["r"] = bufs["y"]
     dev = {k: DeviceBuffer(v) for k, v in bufs.items()}
     for k, b in dev.items():
         N.check(L.spinn_hip_fill_u32(b.ptr, 0, bufs[k], None), "fill")
-    total_ms = total_f = 0.0
+    total_ms = total_f = total_b = 0.0
     try:
         for key, rs in shapes.items():
             r = rs[0]
-            d = N.ConvDesc(*key, N.ALGO_IMPLICIT_GEMM, 0)
-            pk = DeviceBuffer(L.spinn_hip_conv_packed_size(C.byref(d)))
+            d = N.ConvDesc(*key, algo, 0)
+            psz = L.spinn_hip_conv_packed_size(C.byref(d))
+            pk = DeviceBuffer(psz) if psz else None
             wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
             ws = DeviceBuffer(wsz) if wsz else None
-            N.check(L.spinn_hip_conv_pack_weights(C.byref(d), dev["w"].ptr, pk.ptr, None), "pack")
-            res = dev["r"].ptr if r["act"] in (4, 5) else None
-            launch = lambda: L.spinn_hip_conv(C.byref(d), dev["x"].ptr, dev["w"].ptr, pk.ptr,  # noqa: E731
-                                              dev["b"].ptr, res, dev["y"].ptr, ws.ptr if ws else None, wsz, None)
+            if pk:
+                N.check(L.spinn_hip_conv_pack_weights(C.byref(d), dev["w"].ptr, pk.ptr, None), "pack")
+            has_res = r["act"] in (4, 5)
+            res = dev["r"].ptr if has_res else None
+            launch = lambda: L.spinn_hip_conv(C.byref(d), dev["x"].ptr, dev["w"].ptr,  # noqa: E731
+                                              pk.ptr if pk else None, dev["b"].ptr, res, dev["y"].ptr,
+                                              ws.ptr if ws else None, wsz, None)
             N.check(launch(), "conv")
             ms = time_launches(launch, reps)
+            byts = (nbytes(r["n"], r["c"], r["h"], r["w"]) + nbytes(r["oc"], r["c"] // r["group"], r["kh"], r["kw"])
+                    + nbytes(r["n"], r["oc"], r["oh"], r["ow"]) * (2 if has_res else 1))
             total_ms += ms * len(rs)
             total_f += r["flops"] * len(rs)
-            pk.free()
-            if ws:
-                ws.free()
+            total_b += byts * len(rs)
+            for buf in (pk, ws):
+                if buf:
+                    buf.free()
     finally:
         for b in dev.values():
             b.free()
-    return total_ms, total_f, len(ig)
+    return total_ms, total_f, total_b, len(rows)
 
 
 def igemm_algorithmic_bytes(batch: int, policy: str) -> float:
@@ -631,7 +651,8 @@ def main() -> int:
     all_ms = float(node_ms.sum())
     conv_tflops = tot_f / (tot_t * 1e-3) / 1e12
     ig_node_tflops = ig_f / (ig_t * 1e-3) / 1e12 if ig_t > 0 else 0.0
-    ig_live_ms, ig_live_f, _ = igemm_kernel_live(N, rows, policy)
+    ig_rows = [r for r in rows if algo_of(N, r, policy) == N.ALGO_IMPLICIT_GEMM]
+    ig_live_ms, ig_live_f, _, _ = conv_kernels_live(N, ig_rows, N.ALGO_IMPLICIT_GEMM)
     ig_tflops = ig_live_f / (ig_live_ms * 1e-3) / 1e12 if ig_live_ms > 0 else ig_node_tflops
     print(f"[bench] implicit-GEMM kernels: {ig_live_ms:.3f} ms per pass back to back "
           f"({ig_tflops:.1f} TFLOP/s), {ig_t:.3f} ms in the per-node event pass ({ig_node_tflops:.1f})",
