@@ -59,11 +59,13 @@ SpinnContext *spinn_load(const char *path) {
     if (read_exact(fp, &cnt, 2)) goto fail;
     for (uint16_t i = 0; i < cnt; i++) {
         if (read_exact(fp, &id, 2)) goto fail;
+        if (id >= ctx->num_tensors) goto fail;
         if (i < 16) ctx->input_ids[i] = id;
     }
     if (read_exact(fp, &cnt, 2)) goto fail;
     for (uint16_t i = 0; i < cnt; i++) {
         if (read_exact(fp, &id, 2)) goto fail;
+        if (id >= ctx->num_tensors) goto fail;
         if (i < 16) ctx->output_ids[i] = id;
     }
 
@@ -75,9 +77,24 @@ SpinnContext *spinn_load(const char *path) {
         if (read_exact(fp, &m, sizeof(m))) goto fail;
         if (m.tensor_id >= ctx->num_tensors) goto fail;
         SpinnTensor *t = &ctx->tensors[m.tensor_id];
+        /* Every launch and buffer bound is sized from these fields: a tensor
+         * whose element count is not the product of its dims, or whose byte
+         * size does not fit 32 bits, is a malformed file. */
+        if (m.ndim > ENNF_MAX_DIMS) goto fail;
+        if (m.ndim > 0) {
+            uint64_t prod = 1;
+            for (int d = 0; d < m.ndim; d++) {
+                prod *= m.dims[d];
+                if (prod > UINT32_MAX) goto fail;
+            }
+            if (prod != m.elem_count) goto fail;
+        } else if (m.elem_count > 1) {
+            goto fail;
+        }
+        if ((uint64_t)m.elem_count * ennf_dtype_bytes(m.dtype) > UINT32_MAX) goto fail;
         t->id = m.tensor_id;
         t->dtype = m.dtype;
-        t->ndim = m.ndim > ENNF_MAX_DIMS ? ENNF_MAX_DIMS : m.ndim;
+        t->ndim = m.ndim;
         memcpy(t->dims, m.dims, sizeof(m.dims));
         t->elem_count = m.elem_count;
         t->is_weight = m.is_weight;
@@ -154,8 +171,28 @@ static int dispatch_node(SpinnContext *ctx, uint32_t i) {
                              node->num_outputs);
 }
 
+/* Bytes of a weight's payload in the file, from its dense entry (0 = none). */
+static uint32_t weight_payload_bytes(SpinnContext *ctx, uint16_t tensor_id) {
+    uint32_t entry_pos = ctx->header.reserved[0] + (uint32_t)tensor_id * (uint32_t)sizeof(ENNF_WeightEntry);
+    ENNF_WeightEntry e;
+    if (!ctx->ennf_fp || fseek(ctx->ennf_fp, entry_pos, SEEK_SET) || read_exact(ctx->ennf_fp, &e, sizeof(e)))
+        return 0;
+    return e.data_size;
+}
+
 int spinn_plan(SpinnContext *ctx, uint32_t max_arena_bytes) {
     if (!ctx) return -1;
+    /* A weight whose payload is shorter than its tensor would be read past
+     * its end by the upload below: reject the file before any device work. */
+    for (uint32_t i = 0; i < ctx->num_tensors; i++) {
+        SpinnTensor *t = &ctx->tensors[i];
+        if (!t->is_weight || t->size == 0) continue;
+        uint32_t have = weight_payload_bytes(ctx, (uint16_t)i);
+        if (have > 0 && have < t->size) {
+            ctx->last_error = -1;
+            return -1;
+        }
+    }
     int peak = spinn_plan_memory(ctx, max_arena_bytes);
     if (peak < 0) return peak;
     if (!ctx->stream && spinn_hip_stream_create(&ctx->stream) != 0) return -2;
@@ -341,7 +378,13 @@ int spinn_run(SpinnContext *ctx, void *input_data, void *output_data) {
             rc = spinn_hip_graph_capture_begin(ctx->stream);
             if (rc == 0) {
                 int r = run_nodes(ctx, NULL);
-                int e = spinn_hip_graph_capture_end(ctx->stream, &ctx->graph_exec);
+                void *exec = NULL;
+                int e = spinn_hip_graph_capture_end(ctx->stream, &exec);
+                /* A node that failed left its launches out of the capture: keep
+                 * no graph, so the next run captures again and fails again
+                 * instead of replaying the incomplete one. */
+                if (r == 0 && e == 0) ctx->graph_exec = exec;
+                else if (exec) spinn_hip_graph_destroy(exec);
                 rc = r ? r : e;
             }
         }

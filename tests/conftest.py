@@ -1,10 +1,13 @@
 """Shared fixtures: the `gpu` marker, the native library, device buffers and the
 parity bar.
 
-Parity bar (fp32, from the task's tolerance): max-abs error <= 1e-3 and
-relative L2 error <= 1e-4. For outputs whose magnitude exceeds 1 (deep
-random-init networks reach 1e3..1e6), the max-abs bound is scaled by the
-output's max-abs value, i.e. it becomes a relative max-error bound.
+Parity bar (fp32): max-abs error <= 1e-3 and relative L2 error <= 1e-4,
+held as absolute bounds by every single-operator test. Whole-model tests
+opt in to `scale_by_ref=True`: random-init deep networks amplify their
+activations layer after layer (ResNet-101 logits reach ~5e8, decoded detector
+boxes ~640), where fp32's own spacing exceeds 1e-3, so there the max-abs bound
+is multiplied by max(1, max|ref|) - a relative max-error bound. The rel-L2
+bound is never scaled.
 """
 from __future__ import annotations
 
@@ -29,6 +32,7 @@ def pytest_configure(config):
 
 
 def errors(y, ref):
+    """(max-abs error, relative L2 error, max(1, max|ref|)) of y against ref."""
     y = np.asarray(y, np.float64)
     ref = np.asarray(ref, np.float64)
     assert y.shape == ref.shape, (y.shape, ref.shape)
@@ -41,10 +45,15 @@ def errors(y, ref):
     return max_abs, rel, scale
 
 
-def assert_parity(y, ref, max_abs=MAX_ABS, rel_l2=REL_L2, what=""):
-    ma, rel, scale = errors(y, ref)
-    assert ma <= max_abs * scale and rel <= rel_l2, (
-        f"{what}: max_abs={ma:.3e} (bound {max_abs * scale:.3e}), rel_l2={rel:.3e} (bound {rel_l2:.1e})")
+def assert_parity(y, ref, max_abs=MAX_ABS, rel_l2=REL_L2, what="", scale_by_ref=False):
+    """Assert the parity bar; prints the figures so a passing run records them."""
+    ma, rel, mref = errors(y, ref)
+    bound = max_abs * (mref if scale_by_ref else 1.0)
+    print(f"[parity] {what}: max_abs={ma:.3e} (bound {bound:.3e}) rel_l2={rel:.3e} max|ref|={mref:.3e}",
+          flush=True)
+    assert ma <= bound and rel <= rel_l2, (
+        f"{what}: max_abs={ma:.3e} (bound {bound:.3e}), rel_l2={rel:.3e} (bound {rel_l2:.1e}), "
+        f"max|ref|={mref:.3e}")
 
 
 @pytest.fixture(scope="session")

@@ -4,7 +4,8 @@ and the float64 closed form, through the C ABI.
 Shapes cover every kernel path: tap-ordered implicit GEMM (C/g % 16 == 0),
 the (c,kh,kw) gather for small channel counts, 1x1 stride 1/2, split-K for
 small grids, grouped implicit GEMM, the direct (depthwise) kernel and
-Winograd F(2x2,3x3), with each fused post-op (none, ReLU, SiLU, Add, Add+ReLU).
+Winograd F(2x2,3x3) / F(4x4,3x3), with each fused post-op code (none, ReLU,
+CLIP, SiLU, Add, Add+ReLU). Every case is held to the absolute bound.
 """
 import zlib
 
@@ -57,6 +58,11 @@ CASES = [
     ("winograd43_c256", 1, 256, 14, 14, 256, 3, 1, 1, 1, 1, 4),
     ("winograd43_c512_add", 2, 512, 7, 7, 512, 3, 1, 1, 1, 4, 4),
     ("winograd43_p0_silu", 1, 8, 10, 12, 40, 3, 1, 0, 1, 3, 4),      # no padding: 8x10 output
+    # act 2 (CLIP) is a declared code that applies nothing (SPINN/graph_opt.h:33)
+    ("clip_conv3x3", 2, 64, 14, 14, 64, 3, 1, 1, 1, 2, 0),
+    ("clip_pw1x1_splitk", 1, 1024, 7, 8, 256, 1, 1, 0, 1, 2, 0),
+    ("clip_winograd43", 1, 128, 28, 28, 128, 3, 1, 1, 1, 2, 4),
+    ("clip_depthwise", 1, 32, 20, 20, 32, 3, 1, 1, 32, 2, 0),
 ]
 
 

@@ -175,4 +175,4 @@ def test_yolov10n_with_topk_tail(hip, tmp_path, batch, hw):
     if batch == 1:
         # and the decoded head is within tolerance of the oracle's
         ref_pre = O.Model(pp).run(x, gp.dims(gp.outputs[0]))
-        assert_parity(pre, ref_pre, what="decoded head before the tail")
+        assert_parity(pre, ref_pre, what="decoded head before the tail", scale_by_ref=True)

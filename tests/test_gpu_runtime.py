@@ -44,20 +44,20 @@ def test_vgg_stack_small(hip, tmp_path):
     sched = [(16, 32), (16, 32), (32, 16), (32, 16)]
     g, x = models.vgg_stack(batch=2, seed=3, in_c=16, schedule=sched)
     y, _, ref = _run_both(tmp_path, g, x, "vgg_small")
-    assert_parity(y, ref, what="vgg small")
+    assert_parity(y, ref, what="vgg small", scale_by_ref=True)
 
 
 def test_vgg_stack_winograd_policy(hip, tmp_path):
     sched = [(32, 28), (32, 28), (64, 14), (64, 14)]
     g, x = models.vgg_stack(batch=2, seed=4, in_c=32, schedule=sched)
     y, _, ref = _run_both(tmp_path, g, x, "vgg_wino", policy=N.POLICY_WINOGRAD)
-    assert_parity(y, ref, what="vgg winograd vs im2col oracle")
+    assert_parity(y, ref, what="vgg winograd vs im2col oracle", scale_by_ref=True)
 
 
 def test_resnet50_b1(hip, tmp_path):
     g, x = models.resnet(batch=1, seed=5, blocks=models.RESNET50_BLOCKS, hw=96)
     y, y2, ref = _run_both(tmp_path, g, x, "r50")
-    assert_parity(y, ref, what="resnet50@96 b1")
+    assert_parity(y, ref, what="resnet50@96 b1", scale_by_ref=True)
     assert np.array_equal(y, y2)
 
 
@@ -65,7 +65,7 @@ def test_resnet101_b1(hip, tmp_path):
     g, x = models.resnet101(batch=1, seed=0)
     y, _, ref = _run_both(tmp_path, g, x, "r101")
     print(f"[r101 b1] |ref|max={np.abs(ref).max():.3e}", flush=True)
-    assert_parity(y, ref, what="resnet101 b1")
+    assert_parity(y, ref, what="resnet101 b1", scale_by_ref=True)
 
 
 def test_resnet101_b4_winograd_f43(hip, tmp_path):
@@ -86,7 +86,7 @@ def test_resnet101_b4_winograd_f43(hip, tmp_path):
     assert algos.count(N.ALGO_WINOGRAD_F43) == 6
     y, y2, ref = _run_both(tmp_path, g, x, "r101b4")
     print(f"[r101 b4] |ref|max={np.abs(ref).max():.3e}", flush=True)
-    assert_parity(y, ref, what="resnet101 b4 with F(4x4,3x3)")
+    assert_parity(y, ref, what="resnet101 b4 with F(4x4,3x3)", scale_by_ref=True)
     assert np.array_equal(y, y2)
 
 
@@ -110,7 +110,7 @@ def test_yolov10n(hip, tmp_path, batch, hw):
     g, x = models.yolov10n(batch=batch, seed=7, hw=hw)
     print(f"[yolov10n] b{batch} {hw}x{hw}", flush=True)
     y, y2, ref = _run_both(tmp_path, g, x, f"y10_b{batch}")
-    assert_parity(y, ref, what=f"yolov10n b{batch}@{hw}")
+    assert_parity(y, ref, what=f"yolov10n b{batch}@{hw}", scale_by_ref=True)
     assert np.array_equal(y, y2)
     assert_parity(y[:, 4:], ref[:, 4:], what="class scores")
 
@@ -126,4 +126,66 @@ def test_yolov10n_b16_graph_replay(hip, tmp_path):
     for o in outs:
         assert np.array_equal(o, y_eager)
     ref = O.Model(path).run(x, g.dims(g.outputs[0]))
-    assert_parity(y_eager, ref, what="yolov10n b16")
+    assert_parity(y_eager, ref, what="yolov10n b16", scale_by_ref=True)
+
+
+def test_graph_mode_failed_node_is_not_replayed(hip, tmp_path):
+    """A node that fails host-side validation during graph capture leaves no graph
+    behind: every later graph-mode run captures again and reports the failure
+    again, instead of replaying a graph without that node and returning 0."""
+    rng = np.random.default_rng(0)
+    g = E.Graph()
+    x = g.input("x", (1, 8, 8, 8))
+    r = g.tensor("r", (1, 8, 8, 8))
+    g.node(E.OP_RELU, [x], [r])
+    # 4 weight channels for an 8-channel input with group 1: op_conv2d refuses it
+    w = g.weight("w", rng.standard_normal((8, 4, 3, 3)).astype(np.float32))
+    y = g.tensor("y", (1, 8, 8, 8))
+    g.node(E.OP_CONV, [r, w], [y], E.conv_params(3, 3, pads=(1, 1, 1, 1)))
+    g.output(y)
+    path = g.write(tmp_path / "bad_conv.ennf")
+    L = N.lib()
+    s = Session(path, plan=False)
+    try:
+        assert L.spinn_plan(s.ctx, 0) < 0  # the prepare pass already refuses the conv
+        L.spinn_set_graph_mode(s.ctx, 1)
+        xin = np.ones((1, 8, 8, 8), np.float32)
+        for i in range(2):
+            with pytest.raises(N.SpinnError):
+                s.run(xin)
+            assert s.c.last_error_node == 1, i
+    finally:
+        s.close()
+
+
+def test_cli_driver_protocol(hip, tmp_path):
+    """spinn_amd/bin/spinn_run on the Conv3x3+BN+ReLU model: the reference CLI's
+    protocol (SPINN/run_time/main.c:17-139) - synthetic input x[i] = i/1000, 3
+    warm-ups then best / average, the `SPINN Result:` line parsed the way
+    SPINN/ennf2c/verify_three_way.py:29-44 parses it, and the SPINN_DUMP binary
+    dump of the output - against the oracle on the same input. The synthetic
+    input reaches 200, so the outputs reach the hundreds and the max-abs bound
+    is taken relative to max|ref|."""
+    import os
+    import subprocess
+    from spinn_amd import build
+    g, _ = models.conv_bn_relu(seed=0)
+    path = g.write(tmp_path / "cfg0.ennf")
+    dump = tmp_path / "out.bin"
+    env = dict(os.environ, SPINN_DUMP=str(dump))
+    for extra in ([], ["5"], ["5", "--graph"]):
+        print(f"[cli] spinn_run {' '.join(extra)}", flush=True)
+        r = subprocess.run([str(build.CLI), str(path), *extra], capture_output=True, text=True, env=env,
+                           timeout=60)
+        assert r.returncode == 0, r.stderr[-2000:]
+        line = next(l for l in r.stdout.splitlines() if l.startswith("SPINN Result:"))
+        vals = np.array([float(v) for v in line[len("SPINN Result:"):].split()])
+        n_in = int(np.prod(g.dims(g.inputs[0])))
+        x = (np.arange(n_in, dtype=np.float32) / np.float32(1000)).reshape(g.dims(g.inputs[0]))
+        ref = O.Model(path).run(x, g.dims(g.outputs[0]))
+        dumped = np.fromfile(dump, np.float32).reshape(ref.shape)
+        assert_parity(dumped, ref, what=f"cli dump {extra}", scale_by_ref=True)
+        assert vals.size == ref.size
+        assert np.abs(vals - dumped.ravel()).max() <= 5e-7 + 1e-6 * np.abs(dumped).max()  # %.6f print
+        if extra:
+            assert "Warmup: 3, Runs: 5" in r.stderr and "Best:" in r.stderr and "Avg:" in r.stderr

@@ -3,6 +3,7 @@
 conventions and the exported C ABI. No GPU calls."""
 import ctypes as C
 import re
+import struct
 from pathlib import Path
 
 import numpy as np
@@ -280,3 +281,95 @@ def test_bench_traffic_summary_scaling(tmp_path, monkeypatch):
     assert s["fetch_bytes_per_launch"] == 200 * 1024 * 2
     assert s["write_bytes_per_launch"] == 20 * 1024
     assert s["traffic_bytes_per_launch"] == 200 * 1024 * 2 + 20 * 1024
+
+
+def _hdr_fields(data):
+    """(entry table offset, graph meta offset, tensor meta offset) of an ENNF image."""
+    f = E._HDR.unpack_from(data, 0)
+    return f[16], f[11], f[13]
+
+
+def _crafted(tmp_path, name, patch):
+    g, _ = models.conv_bn_relu(seed=0)
+    data = bytearray(g.to_bytes())
+    patch(g, data)
+    p = tmp_path / f"{name}.ennf"
+    p.write_bytes(bytes(data))
+    return g, p
+
+
+def test_loader_rejects_inconsistent_metadata(native, tmp_path):
+    """Metadata that would size a launch or a copy wrongly is refused at load:
+    an element count that is not the product of the dims, a byte size past 32
+    bits, ndim above 8, graph input / output ids past the tensor table."""
+    L = native.lib()
+    meta = E._META.size
+
+    def elem_count_off_by_one(g, d):
+        _, _, mo = _hdr_fields(d)
+        off = mo + g.inputs[0] * meta + 36
+        struct.pack_into("<I", d, off, struct.unpack_from("<I", d, off)[0] + 1)
+
+    def huge_dims(g, d):
+        _, _, mo = _hdr_fields(d)
+        off = mo + g.inputs[0] * meta
+        struct.pack_into("<B8II", d, off + 3, 2, 65536, 65536, 0, 0, 0, 0, 0, 0, 0)
+
+    def ndim_nine(g, d):
+        _, _, mo = _hdr_fields(d)
+        struct.pack_into("<B", d, mo + g.inputs[0] * meta + 3, 9)
+
+    def output_id_past_table(g, d):
+        _, gm, _ = _hdr_fields(d)
+        n_in = struct.unpack_from("<H", d, gm)[0]
+        struct.pack_into("<H", d, gm + 2 + 2 * n_in + 2, len(g.tensors))
+
+    def input_id_past_table(g, d):
+        _, gm, _ = _hdr_fields(d)
+        struct.pack_into("<H", d, gm + 2, 0xFFFF)
+
+    for name, patch in [("count", elem_count_off_by_one), ("huge", huge_dims), ("ndim", ndim_nine),
+                        ("out_id", output_id_past_table), ("in_id", input_id_past_table)]:
+        _, p = _crafted(tmp_path, name, patch)
+        assert not L.spinn_load(str(p).encode()), name
+    # the unpatched file still loads
+    _, p = _crafted(tmp_path, "ok", lambda g, d: None)
+    ctx = L.spinn_load(str(p).encode())
+    assert ctx
+    L.spinn_free(ctx)
+
+
+def test_plan_rejects_short_weight_payload(native, tmp_path):
+    """A weight whose payload in the file is shorter than its tensor is refused by
+    spinn_plan before any device work (no host over-read by the upload)."""
+    L = native.lib()
+
+    def short_weight(g, d):
+        eo, _, _ = _hdr_fields(d)
+        wid = next(t.id for t in g.tensors if t.is_weight and t.data.size > 4)
+        off = eo + wid * E._ENTRY.size + 8
+        struct.pack_into("<I", d, off, struct.unpack_from("<I", d, off)[0] - 4)
+
+    _, p = _crafted(tmp_path, "short", short_weight)
+    ctx = L.spinn_load(str(p).encode())
+    assert ctx
+    try:
+        assert L.spinn_plan(ctx, 0) == -1
+    finally:
+        L.spinn_free(ctx)
+
+
+def test_headline_layer_list_matches_resnet101():
+    """The per-layer GPU parity list is exactly ResNet-101's distinct conv layers."""
+    from tests.test_gpu_headline import R101_LAYERS
+    g, _ = models.resnet101(batch=1, seed=0)
+    seen = {}
+    for nd in g.nodes:
+        if nd.op != E.OP_CONV:
+            continue
+        p = E.unpack_conv_params(nd.params)
+        _, c, h, w = g.dims(nd.inputs[0])
+        oc, _, k, _ = g.dims(nd.inputs[1])
+        key = (c, h, w, oc, k, p["strides"][0], p["pads"][0], p["act"])
+        seen[key] = seen.get(key, 0) + 1
+    assert {tuple(l[:8]): l[8] for l in R101_LAYERS} == seen

@@ -363,7 +363,7 @@ def test_oracle_yolov10n_matches_torch_float64(tmp_path):
     path = g.write(tmp_path / "y10_256.ennf")
     y = O.Model(path).run(x, g.dims(g.outputs[0]))
     ref = _torch_graph(path, x)
-    assert_parity(y, ref, what="oracle yolov10n vs torch float64")
+    assert_parity(y, ref, what="oracle yolov10n vs torch float64", scale_by_ref=True)
     # boxes are pixel coordinates on the 8/16/32 strides grid, scores in (0, 1)
     assert y.shape == (2, 84, 32 * 32 + 16 * 16 + 8 * 8)
     assert np.all((y[:, 4:] > 0) & (y[:, 4:] < 1))
@@ -373,7 +373,7 @@ def test_oracle_model_matches_torch_float64(tmp_path):
     g, x = models.resnet(batch=2, seed=2, blocks=(1, 2, 1, 1), hw=64, num_classes=37)
     path = g.write(tmp_path / "tiny_resnet.ennf")
     y = O.Model(path).run(x, g.dims(g.outputs[0]))
-    assert_parity(y, _torch_graph(path, x), what="oracle model vs torch float64")
+    assert_parity(y, _torch_graph(path, x), what="oracle model vs torch float64", scale_by_ref=True)
 
 
 @pytest.mark.parametrize("name", ["yolov10n_64", "resnet_64", "yolov10n_64_post"])
@@ -401,7 +401,7 @@ def test_oracle_model_as_shipped_matches_reference_runtime(name):
             O.lib().oracle_set_as_shipped(0)
         m.close()
     ref = f[f"{name}_y"]
-    assert_parity(y, ref, max_abs=1e-5, rel_l2=1e-6, what=f"{name} as-shipped vs reference spinn_run")
+    assert_parity(y, ref, max_abs=1e-5, rel_l2=1e-6, what=f"{name} as-shipped vs reference spinn_run", scale_by_ref=True)
 
 
 # ---------------------------------------------------------------------------
