@@ -334,7 +334,14 @@ int spinn_hip_binary_typed(int op, int dtype, const void *a, int64_t na, const v
     return binary_typed(op, dtype, a, na, b, nb, y, n, (hipStream_t)stream);
 }
 
-int spinn_hip_init(int device) { return hip_code(hipSetDevice(device)); }
+int spinn_hip_init(int device) {
+    int rc = hip_code(hipSetDevice(device));
+    if (rc) return rc;
+    // resolve the device address of spinn_hip_conv_noalloc's scratch array here,
+    // at set-up, rather than inside a caller's capture or serving loop
+    void *scratch = nullptr;
+    return noalloc_scratch(device, &scratch);
+}
 
 int spinn_hip_device_count(int *count) {
     if (!count) return SPINN_HIP_EINVAL;

@@ -56,6 +56,10 @@ void force_tiles(int bm, int bn, int split);
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cu_count();
 
+// Device address of spinn_hip_conv_noalloc's scratch array on `device` (the
+// current device), resolved once per device (noalloc.hip).
+int noalloc_scratch(int device, void **ptr);
+
 // implicit GEMM (conv_gemm.hip)
 int64_t igemm_packed_floats(const SpinnHipConvDesc *d);
 int igemm_pack(const SpinnHipConvDesc *d, const float *w, float *packed, hipStream_t st);

@@ -24,6 +24,7 @@ SPINN_HIP_OK = 0
 SPINN_HIP_EINVAL = -1
 SPINN_HIP_EUNSUPPORTED = -2
 SPINN_HIP_EWORKSPACE = -3
+NOALLOC_SCRATCH_BYTES = 128 << 20  # SPINN_HIP_NOALLOC_SCRATCH_BYTES
 
 ALGO_AUTO, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_DIRECT, ALGO_WINOGRAD_F43 = 0, 1, 2, 3, 4
 ACT_NONE, ACT_RELU, ACT_CLIP, ACT_SILU, ACT_ADD, ACT_ADD_RELU = 0, 1, 2, 3, 4, 5
@@ -125,6 +126,8 @@ _lib = None
 _SIGS = {
     "spinn_hip_conv": (C.c_int, [C.POINTER(ConvDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                  C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "spinn_hip_conv_noalloc": (C.c_int, [C.POINTER(ConvDesc), C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                         C.c_void_p, C.c_void_p, C.c_void_p]),
     "spinn_hip_conv_select_algo": (C.c_int, [C.POINTER(ConvDesc)]),
     "spinn_hip_conv_workspace_size": (C.c_size_t, [C.POINTER(ConvDesc)]),
     "spinn_hip_conv_packed_size": (C.c_size_t, [C.POINTER(ConvDesc)]),
