@@ -22,11 +22,14 @@ graph). Prints ONE JSON line:
                     3x3 stack (implicit GEMM vs Winograd), YOLOv10n at batch 1
                     and 16 with operator families and the depthwise layers'
                     achieved HBM bandwidth (live back-to-back launches)
-  cpu_baseline      the reference's own CPU runtime (or the oracle's
-                    restatement when the reference build is absent) on this
-                    host's cores, ResNet-101 batch 1, a bounded sample
+  cpu_baseline      the oracle's restatement of SPINN's CPU path (specified
+                    epilogue) on this host's cores and on 4 threads, plus the
+                    reference's own runtime as shipped when built; ResNet-101
+                    batch 1, a bounded sample
 
-Per-layer GFLOP/s and % of peak go to gpurun_out/bench_layers.json.
+Per-layer GFLOP/s and % of peak go to gpurun_out/bench_layers.json (per node,
+from events) and gpurun_out/bench_layers.md (per distinct layer shape, from
+back-to-back launches, with Winograd's executed FLOPs).
 """
 from __future__ import annotations
 
@@ -57,11 +60,22 @@ def host_threads() -> int:
     return n
 
 
-def cpu_baseline(model_b1: Path, in_shape, out_shape, seconds: float, label: str = "ResNet-101") -> dict | None:
-    kind = "reference" if (ROOT / "oracle" / "_ref" / "libspinn_ref.so").exists() else "port"
-    threads = host_threads()
+def host_cpu() -> str:
+    """CPU model and physical core count of this host, from lscpu."""
+    try:
+        info = dict(l.split(":", 1) for l in subprocess.run(["lscpu"], capture_output=True, text=True,
+                                                             timeout=10).stdout.splitlines() if ":" in l)
+        sockets = int(info.get("Socket(s)", "1").strip() or 1)
+        cores = int(info.get("Core(s) per socket", "0").strip() or 0) * sockets
+        return f"{info.get('Model name', '?').strip()}, {cores} physical cores, {os.cpu_count()} logical"
+    except Exception:
+        return "unknown"
+
+
+def _cpu_run(kind: str, model: Path, in_shape, out_shape, seconds: float, threads: int) -> dict | None:
+    """One oracle.cpu_bench process (the OpenMP thread count is fixed per process)."""
     env = dict(os.environ, OMP_NUM_THREADS=str(threads))
-    cmd = [sys.executable, "-m", "oracle.cpu_bench", "--kind", kind, "--model", str(model_b1),
+    cmd = [sys.executable, "-m", "oracle.cpu_bench", "--kind", kind, "--model", str(model),
            "--in-shape", ",".join(map(str, in_shape)), "--out-shape", ",".join(map(str, out_shape)),
            "--seconds", str(seconds)]
     try:
@@ -72,11 +86,43 @@ def cpu_baseline(model_b1: Path, in_shape, out_shape, seconds: float, label: str
         print(r.stderr[-2000:], file=sys.stderr)
         return None
     res = json.loads(r.stdout.strip().splitlines()[-1])
-    ips = res["batch"] / (res["avg_ms"] / 1e3)
-    return {"value": round(ips, 3), "unit": "images/s", "cores": threads, "kind": kind,
-            "sample": (f"{label} batch {res['batch']} forward, {res['runs']} runs after 3 warm-up "
-                       f"(reference CLI protocol), ~{seconds:.0f} s budget, OpenMP {threads} threads; "
-                       f"best {res['best_ms']:.1f} ms, mean {res['avg_ms']:.1f} ms per image")}
+    res["images_per_s"] = res["batch"] / (res["avg_ms"] / 1e3)
+    return res
+
+
+def cpu_baseline(model_b1: Path, in_shape, out_shape, seconds: float, label: str = "ResNet-101") -> dict | None:
+    """The CPU path timed on this host: the oracle's C restatement of SPINN's algorithm
+    (im2col + packed 6x16 AVX2 GEMM tiles, K block 256, N block 128, OpenMP over tiles,
+    with the epilogue as the reference specifies it) on all the host threads available,
+    then on 4 threads (the thread count of SPINN/OPTIMIZATION_PROGRESS.md:4), and the
+    reference's own runtime as shipped (oracle/_ref, which drops bias / activation /
+    residual on group-1 convs, SPINN/run_time/ops/mm/gemm_kernel.c:497-590) when built.
+    Protocol of SPINN/run_time/main.c:42,83-108: 3 warm-ups, then runs until the time
+    budget is spent; mean wall time per run including the input and output copies."""
+    threads = host_threads()
+    port = _cpu_run("port", model_b1, in_shape, out_shape, seconds, threads)
+    if port is None:
+        return None
+    out = {"value": round(port["images_per_s"], 3), "unit": "images/s", "cores": threads, "kind": "port",
+           "sample": (f"{label} batch {port['batch']} forward through the restated SPINN CPU path (specified "
+                      f"epilogue), {port['runs']} runs after 3 warm-up (reference CLI protocol), ~{seconds:.0f} s "
+                      f"budget, OpenMP {threads} threads; best {port['best_ms']:.1f} ms, mean "
+                      f"{port['avg_ms']:.1f} ms per forward"),
+           "host": host_cpu()}
+    if threads != 4:
+        p4 = _cpu_run("port", model_b1, in_shape, out_shape, seconds / 2, 4)
+        if p4:
+            out["threads_4"] = {"value": round(p4["images_per_s"], 3), "best_ms": round(p4["best_ms"], 2),
+                                "avg_ms": round(p4["avg_ms"], 2), "runs": p4["runs"]}
+    if (ROOT / "oracle" / "_ref" / "libspinn_ref.so").exists():
+        ref = _cpu_run("reference", model_b1, in_shape, out_shape, seconds / 2, threads)
+        if ref:
+            out["reference_as_shipped"] = {
+                "value": round(ref["images_per_s"], 3), "best_ms": round(ref["best_ms"], 2),
+                "avg_ms": round(ref["avg_ms"], 2), "runs": ref["runs"], "threads": threads,
+                "note": "the reference's own runtime built from its sources; it skips the epilogue of group-1 "
+                        "convs, so it does less work than the specified path"}
+    return out
 
 
 def conv_table(g):
@@ -141,7 +187,7 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
            the two outputs are apart (relative L2);
     yolo   YOLOv10n 640x640 at batch 1 and 16 (see yolo_bench)."""
     import ctypes as C
-    from spinn_amd.devbuf import DeviceBuffer, time_launches
+    from spinn_amd.devbuf import DeviceBuffer, time_cold, time_launches
     L = N.lib()
     out = {}
     g, x = models.conv_bn_relu(seed=0)
@@ -174,6 +220,8 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
     for b_ in (bx, bw, bb, by, bp) + ((bws,) if bws else ()):
         b_.free()
     gemms = []
+    fa, fb = DeviceBuffer(FLUSH_BYTES), DeviceBuffer(FLUSH_BYTES)
+    flush = lambda: N.check(L.spinn_hip_copy(fb.ptr, fa.ptr, FLUSH_BYTES, None), "flush")  # noqa: E731
     for (m, n, k) in models.GEMM_SWEEP:
         rng = np.random.default_rng(m * 7 + n)
         a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
@@ -190,10 +238,21 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
         byts = 4.0 * (m * k + n * k + n + m * n)
         bound = "hbm" if f / byts < PEAK_FP32_MFMA / 8e12 else "mfma"
         frac = (byts / (ms * 1e-3) / 8e12) if bound == "hbm" else (f / (ms * 1e-3) / PEAK_FP32_MFMA)
-        gemms.append({"mnk": [m, n, k], "us": round(ms * 1e3, 3), "gflops": round(f / (ms * 1e-3) / 1e9, 1),
-                      "gbps": round(byts / (ms * 1e-3) / 1e9, 1), "bound": bound, "frac_roofline": round(frac, 4)})
+        ent = {"mnk": [m, n, k], "us": round(ms * 1e3, 3), "gflops": round(f / (ms * 1e-3) / 1e9, 1),
+               "gbps": round(byts / (ms * 1e-3) / 1e9, 1), "bound": bound, "frac_roofline": round(frac, 4)}
+        if bound == "hbm":
+            # back to back, the 8 MB weight matrix stays in the 256 MB Infinity Cache (MALL);
+            # after a 512 MiB copy it comes from HBM
+            ms_c = time_cold(lambda: L.spinn_hip_gemm(C.byref(gd), ba.ptr, bb2.ptr, bc.ptr, by2.ptr,
+                                                      bws.ptr if bws else None, wsz, None), flush, 20)
+            ent["us_mall_resident"] = ent["us"]
+            ent["us_after_flush"] = round(ms_c * 1e3, 3)
+            ent["frac_hbm_after_flush"] = round(byts / (ms_c * 1e-3) / 8e12, 4)
+        gemms.append(ent)
         for b_ in (ba, bb2, bc, by2) + ((bws,) if bws else ()):
             b_.free()
+    fa.free()
+    fb.free()
     out["gemm_sweep"] = gemms
     gv, xv = models.vgg_stack(batch=8, seed=0)
     pv = gv.write(tmp / "vgg_b8.ennf")
@@ -276,6 +335,7 @@ def yolo_bench(N, Session, models, tmp: Path, reps: int) -> dict:
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "conv_igemm_traffic_resnet101_b32.json"
+FLUSH_BYTES = 512 << 20  # twice the 256 MB Infinity Cache
 CALIB_BYTES = 256 << 20
 
 
@@ -361,22 +421,37 @@ def gemm_compare(reps: int = 5) -> None:
     print(json.dumps({"gemm_compare": True, "torch_fp32_matmul_us": lib_us}), flush=True)
 
 
-def conv_kernels_live(N, rows, algo: int, reps: int = 10):
-    """Live kernel time of a set of conv layers: every distinct layer shape is launched through
-    spinn_hip_conv with algorithm `algo`, `reps` times back to back between two HIP events on
-    the stream the kernel runs on (the null stream), so the figure carries no event or launch
-    gap between nodes, unlike the per-node event pass. Returns (kernel ms summed over the
-    layers, direct-conv FLOPs, algorithmic bytes - input, weights, output, residual - and the
-    number of layers)."""
+def executed_flops(r, algo: int) -> float:
+    """MFMA FLOPs a layer actually executes: the direct count for the implicit GEMM
+    and the direct kernels; for Winograd F(m x m, 3x3) the (m+2)^2 batched GEMMs of
+    OC x C over T = N * ceil(OH/m) * ceil(OW/m) tiles (the transforms are not counted)."""
+    from spinn_amd import native as N
+    m = {N.ALGO_WINOGRAD: 2, N.ALGO_WINOGRAD_F43: 4}.get(algo)
+    if m is None:
+        return r["flops"]
+    tiles = r["n"] * -(-r["oh"] // m) * -(-r["ow"] // m)
+    return 2.0 * (m + 2) ** 2 * r["oc"] * r["c"] * tiles
+
+
+CONV_FIELDS = ("n", "c", "h", "w", "oc", "oh", "ow", "kh", "kw", "sh", "sw", "ph", "pw", "group", "act")
+
+
+def conv_layers_live(N, rows, algo_for, reps: int = 10) -> list:
+    """Live kernel time of every distinct conv layer shape in `rows`: launched through
+    spinn_hip_conv with the algorithm `algo_for(row)` names, `reps` times back to back
+    between two HIP events on the stream the kernels run on (the null stream), so the
+    figure carries no event or launch gap between nodes, unlike the per-node event pass.
+    One entry per shape: the row, its count, algorithm, ms per launch (all of the
+    layer's kernels), direct and executed FLOPs and algorithmic bytes (input, weights,
+    bias, output, residual; fp32, each once)."""
     import ctypes as C
     from spinn_amd.devbuf import DeviceBuffer, time_launches
     L = N.lib()
     if not rows:
-        return 0.0, 0.0, 0.0, 0
-    fields = ("n", "c", "h", "w", "oc", "oh", "ow", "kh", "kw", "sh", "sw", "ph", "pw", "group", "act")
+        return []
     shapes = {}
     for r in rows:
-        shapes.setdefault(tuple(r[f] for f in fields), []).append(r)
+        shapes.setdefault(tuple(r[f] for f in CONV_FIELDS), []).append(r)
     nbytes = lambda *dims: 4 * int(np.prod(dims))  # noqa: E731
     bufs = dict(x=max(nbytes(r["n"], r["c"], r["h"], r["w"]) for r in rows),
                 y=max(nbytes(r["n"], r["oc"], r["oh"], r["ow"]) for r in rows),
@@ -386,10 +461,11 @@ def conv_kernels_live(N, rows, algo: int, reps: int = 10):
     dev = {k: DeviceBuffer(v) for k, v in bufs.items()}
     for k, b in dev.items():
         N.check(L.spinn_hip_fill_u32(b.ptr, 0, bufs[k], None), "fill")
-    total_ms = total_f = total_b = 0.0
+    out = []
     try:
         for key, rs in shapes.items():
             r = rs[0]
+            algo = algo_for(r)
             d = N.ConvDesc(*key, algo, 0)
             psz = L.spinn_hip_conv_packed_size(C.byref(d))
             pk = DeviceBuffer(psz) if psz else None
@@ -405,17 +481,53 @@ def conv_kernels_live(N, rows, algo: int, reps: int = 10):
             N.check(launch(), "conv")
             ms = time_launches(launch, reps)
             byts = (nbytes(r["n"], r["c"], r["h"], r["w"]) + nbytes(r["oc"], r["c"] // r["group"], r["kh"], r["kw"])
-                    + nbytes(r["n"], r["oc"], r["oh"], r["ow"]) * (2 if has_res else 1))
-            total_ms += ms * len(rs)
-            total_f += r["flops"] * len(rs)
-            total_b += byts * len(rs)
+                    + nbytes(r["oc"]) + nbytes(r["n"], r["oc"], r["oh"], r["ow"]) * (2 if has_res else 1))
+            out.append(dict(row=r, count=len(rs), algo=algo, ms=ms, flops=r["flops"],
+                            exec_flops=executed_flops(r, algo), bytes=byts, split=bool(wsz) and algo == 1))
             for buf in (pk, ws):
                 if buf:
                     buf.free()
     finally:
         for b in dev.values():
             b.free()
-    return total_ms, total_f, total_b, len(rows)
+    return out
+
+
+def conv_kernels_live(N, rows, algo: int, reps: int = 10):
+    """(kernel ms summed over the layers, direct-conv FLOPs, algorithmic bytes, number of
+    layers) of `rows` run with one algorithm, from conv_layers_live."""
+    res = conv_layers_live(N, rows, lambda r: algo, reps)
+    return (sum(e["ms"] * e["count"] for e in res), sum(e["flops"] * e["count"] for e in res),
+            sum(e["bytes"] * e["count"] for e in res), sum(e["count"] for e in res))
+
+
+def layers_markdown(live: list, batch: int, policy: str) -> str:
+    """Per-layer table of one conv pass (one row per distinct layer shape)."""
+    lines = [f"# ResNet-101 v1.5 fp32 conv layers, batch {batch}, policy {policy}", "",
+             "Each distinct layer shape launched 10x back to back through `spinn_hip_conv` between HIP events "
+             "(`bench.py`, conv_layers_live). GFLOP = direct-convolution count 2*N*OC*OH*OW*C*KH*KW; "
+             "exec GFLOP = MFMA work actually issued (Winograd F(4x4,3x3): 36 GEMMs over 4x4 output tiles, "
+             "transforms not counted). % peak against 157.3 TFLOP/s fp32 MFMA.", "",
+             "| layer (C,H,W -> OC, k/s, act) | x | algo | split K | GFLOP | exec GFLOP | us / launch | "
+             "TFLOP/s direct | % peak direct | % peak executed |",
+             "|---|---|---|---|---|---|---|---|---|---|"]
+    tf = te = tt = 0.0
+    for e in live:
+        r = e["row"]
+        t = e["ms"] * 1e-3
+        lines.append(f"| {r['c']},{r['h']},{r['w']} -> {r['oc']}, {r['kh']}x{r['kw']}/s{r['sh']}, {r['act']} | "
+                     f"{e['count']} | {ALGO_NAMES.get(e['algo'], e['algo'])} | {'yes' if e['split'] else ''} | "
+                     f"{e['flops'] / 1e9:.2f} | {e['exec_flops'] / 1e9:.2f} | {e['ms'] * 1e3:.1f} | "
+                     f"{e['flops'] / t / 1e12:.1f} | {100 * e['flops'] / t / PEAK_FP32_MFMA:.1f} | "
+                     f"{100 * e['exec_flops'] / t / PEAK_FP32_MFMA:.1f} |")
+        tf += e["flops"] * e["count"]
+        te += e["exec_flops"] * e["count"]
+        tt += e["ms"] * 1e-3 * e["count"]
+    lines += ["", f"All {sum(e['count'] for e in live)} conv layers: {tt * 1e3:.3f} ms of kernel time, "
+                  f"{tf / 1e9:.1f} GFLOP direct ({tf / tt / 1e12:.1f} TFLOP/s, "
+                  f"{100 * tf / tt / PEAK_FP32_MFMA:.1f} % of peak), {te / 1e9:.1f} GFLOP executed "
+                  f"({te / tt / 1e12:.1f} TFLOP/s, {100 * te / tt / PEAK_FP32_MFMA:.1f} % of peak)."]
+    return "\n".join(lines) + "\n"
 
 
 def igemm_algorithmic_bytes(batch: int, policy: str) -> float:
@@ -509,7 +621,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--policy", choices=["auto", "igemm", "winograd"], default="auto")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=8.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch nodes one by one (for profilers)")
     ap.add_argument("--profile-pass", action="store_true",
@@ -651,16 +763,22 @@ def main() -> int:
     all_ms = float(node_ms.sum())
     conv_tflops = tot_f / (tot_t * 1e-3) / 1e12
     ig_node_tflops = ig_f / (ig_t * 1e-3) / 1e12 if ig_t > 0 else 0.0
-    ig_rows = [r for r in rows if algo_of(N, r, policy) == N.ALGO_IMPLICIT_GEMM]
-    ig_live_ms, ig_live_f, _, _ = conv_kernels_live(N, ig_rows, N.ALGO_IMPLICIT_GEMM)
+    live = conv_layers_live(N, rows, lambda r: algo_of(N, r, policy))
+    ig_live = [e for e in live if e["algo"] == N.ALGO_IMPLICIT_GEMM]
+    ig_live_ms = sum(e["ms"] * e["count"] for e in ig_live)
+    ig_live_f = sum(e["flops"] * e["count"] for e in ig_live)
     ig_tflops = ig_live_f / (ig_live_ms * 1e-3) / 1e12 if ig_live_ms > 0 else ig_node_tflops
+    live_ms = sum(e["ms"] * e["count"] for e in live)
+    live_f = sum(e["flops"] * e["count"] for e in live)
+    live_ef = sum(e["exec_flops"] * e["count"] for e in live)
     print(f"[bench] implicit-GEMM kernels: {ig_live_ms:.3f} ms per pass back to back "
-          f"({ig_tflops:.1f} TFLOP/s), {ig_t:.3f} ms in the per-node event pass ({ig_node_tflops:.1f})",
-          file=sys.stderr, flush=True)
+          f"({ig_tflops:.1f} TFLOP/s), {ig_t:.3f} ms in the per-node event pass ({ig_node_tflops:.1f}); "
+          f"all conv kernels {live_ms:.3f} ms", file=sys.stderr, flush=True)
     out_layers = Path(a.layers_out)
     out_layers.parent.mkdir(parents=True, exist_ok=True)
     out_layers.write_text(json.dumps(dict(batch=a.batch, policy=a.policy, node_ms_total=all_ms,
                                           conv_ms_total=tot_t, layers=layers), indent=1))
+    out_layers.with_suffix(".md").write_text(layers_markdown(live, a.batch, a.policy))
 
     ips = a.batch / (ms_B * 1e-3)
     line = {
@@ -686,6 +804,17 @@ def main() -> int:
         "conv_tflops_aggregate": round(conv_tflops, 3),
         "conv_frac_mfma_peak": round(conv_tflops * 1e12 / PEAK_FP32_MFMA, 4),
         "conv_share_of_node_time": round(tot_t / all_ms, 4) if all_ms > 0 else None,
+        "conv_kernels": {
+            "ms_per_pass": round(live_ms, 4),
+            "gflop_direct": round(live_f / 1e9, 2), "gflop_executed": round(live_ef / 1e9, 2),
+            "tflops_direct_equiv": round(live_f / (live_ms * 1e-3) / 1e12, 2),
+            "frac_mfma_peak_direct_equiv": round(live_f / (live_ms * 1e-3) / PEAK_FP32_MFMA, 4),
+            "tflops_executed": round(live_ef / (live_ms * 1e-3) / 1e12, 2),
+            "frac_mfma_peak_executed": round(live_ef / (live_ms * 1e-3) / PEAK_FP32_MFMA, 4),
+            "winograd_layers": sum(e["count"] for e in live if e["algo"] in (N.ALGO_WINOGRAD, N.ALGO_WINOGRAD_F43)),
+            "method": "every conv layer's kernels launched 10x back to back between HIP events; direct = "
+                      "2*N*OC*OH*OW*C*KH*KW (Winograd credited at the direct count), executed = the MFMA work "
+                      "issued (Winograd: (m+2)^2 tile GEMMs, transforms not counted)"},
         "roofline": {"bound": "mfma", "achieved": round(ig_tflops, 3), "peak": PEAK_FP32_MFMA / 1e12,
                      "unit": "TFLOP/s", "frac": round(ig_tflops * 1e12 / PEAK_FP32_MFMA, 4),
                      "traffic": measured_traffic(a.batch, a.policy),

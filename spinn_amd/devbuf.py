@@ -70,3 +70,28 @@ def time_launches(fn, reps: int, warmup: int = 3, stream=None) -> float:
     finally:
         L.spinn_hip_event_destroy(e0)
         L.spinn_hip_event_destroy(e1)
+
+
+def time_cold(fn, flush, reps: int) -> float:
+    """Mean milliseconds of one call of `fn` right after `flush` (work that evicts
+    the caches, e.g. a copy larger than the Infinity Cache): events bracket `fn`
+    alone, `reps` times, on the null stream."""
+    L = N.lib()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    N.check(L.spinn_hip_event_create(C.byref(e0)), "event")
+    N.check(L.spinn_hip_event_create(C.byref(e1)), "event")
+    total = 0.0
+    try:
+        for _ in range(reps):
+            flush()
+            N.check(L.spinn_hip_event_record(e0, None), "record")
+            N.check(fn(), "timed call")
+            N.check(L.spinn_hip_event_record(e1, None), "record")
+            N.check(L.spinn_hip_stream_sync(None), "sync")
+            ms = C.c_float()
+            N.check(L.spinn_hip_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
+            total += ms.value
+    finally:
+        L.spinn_hip_event_destroy(e0)
+        L.spinn_hip_event_destroy(e1)
+    return total / reps
