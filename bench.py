@@ -177,8 +177,9 @@ def profiled_node_ms(N, Session, path, x, policy, steps: int, warmup: int):
 def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> dict:
     """The other benchmark configurations, each on its own:
     cfg0   single fused Conv3x3+BN+ReLU 1x64x56x56 through spinn_hip_conv
-           (launch-bound: 2*reps back-to-back launches timed with events) and
-           through spinn_run with host copies;
+           (kernel time: 20 launches in a HIP graph replayed between events;
+           us_host_launches: back-to-back host launches, which the host's launch
+           rate bounds at these sizes) and through spinn_run with host copies;
     gemm   the Gemm sweep (transB=1, bias vector, alpha=beta=1) through spinn_hip_gemm,
            against the MFMA roofline or, for arithmetic intensity under the
            19.7 flop/B ridge, the HBM roofline;
@@ -187,7 +188,7 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
            the two outputs are apart (relative L2);
     yolo   YOLOv10n 640x640 at batch 1 and 16 (see yolo_bench)."""
     import ctypes as C
-    from spinn_amd.devbuf import DeviceBuffer, time_cold, time_launches
+    from spinn_amd.devbuf import DeviceBuffer, time_cold, time_graph, time_launches
     L = N.lib()
     out = {}
     g, x = models.conv_bn_relu(seed=0)
@@ -201,8 +202,10 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
     wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
     bws = DeviceBuffer(wsz) if wsz else None
     N.check(L.spinn_hip_conv_pack_weights(C.byref(d), bw.ptr, bp.ptr, None), "pack")
-    ms = time_launches(lambda: L.spinn_hip_conv(C.byref(d), bx.ptr, bw.ptr, bp.ptr, bb.ptr, None, by.ptr,
-                                                bws.ptr if bws else None, wsz, None), 2 * reps)
+    conv0 = lambda st: L.spinn_hip_conv(C.byref(d), bx.ptr, bw.ptr, bp.ptr, bb.ptr, None, by.ptr,  # noqa: E731
+                                        bws.ptr if bws else None, wsz, st)
+    ms = time_graph(conv0, 20)
+    ms_host = time_launches(lambda: conv0(None), 2 * reps)
     flops = 2.0 * 64 * 56 * 56 * 64 * 9
     byts = 4.0 * (x.size + wt.size + bias.size + 64 * 56 * 56)
     tmp = Path(tempfile.mkdtemp(prefix="spinn_suite_"))
@@ -213,7 +216,9 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
         for _ in range(reps):
             s0.run(x)
         run_ms = (time.perf_counter() - t0) / reps * 1e3
-    out["cfg0_conv3x3_bn_relu"] = {"kernel_us": round(ms * 1e3, 3), "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
+    out["cfg0_conv3x3_bn_relu"] = {"kernel_us": round(ms * 1e3, 3),
+                                   "us_host_launches": round(ms_host * 1e3, 3),
+                                   "gflops": round(flops / (ms * 1e-3) / 1e9, 1),
                                    "frac_mfma_peak": round(flops / (ms * 1e-3) / PEAK_FP32_MFMA, 4),
                                    "roofline_us": round(max(flops / PEAK_FP32_MFMA, byts / 8e12) * 1e6, 3),
                                    "spinn_run_ms_with_host_copies": round(run_ms, 4)}
@@ -232,13 +237,16 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
                             DeviceBuffer(4 * m * n))
         wsz = L.spinn_hip_gemm_workspace_size(C.byref(gd))
         bws = DeviceBuffer(wsz) if wsz else None
-        ms = time_launches(lambda: L.spinn_hip_gemm(C.byref(gd), ba.ptr, bb2.ptr, bc.ptr, by2.ptr,
-                                                    bws.ptr if bws else None, wsz, None), reps)
+        gemm = lambda st: L.spinn_hip_gemm(C.byref(gd), ba.ptr, bb2.ptr, bc.ptr, by2.ptr,  # noqa: E731
+                                           bws.ptr if bws else None, wsz, st)
+        ms = time_graph(gemm, 20)
+        ms_host = time_launches(lambda: gemm(None), reps)
         f = 2.0 * m * n * k
         byts = 4.0 * (m * k + n * k + n + m * n)
         bound = "hbm" if f / byts < PEAK_FP32_MFMA / 8e12 else "mfma"
         frac = (byts / (ms * 1e-3) / 8e12) if bound == "hbm" else (f / (ms * 1e-3) / PEAK_FP32_MFMA)
-        ent = {"mnk": [m, n, k], "us": round(ms * 1e3, 3), "gflops": round(f / (ms * 1e-3) / 1e9, 1),
+        ent = {"mnk": [m, n, k], "us": round(ms * 1e3, 3), "us_host_launches": round(ms_host * 1e3, 3),
+               "gflops": round(f / (ms * 1e-3) / 1e9, 1),
                "gbps": round(byts / (ms * 1e-3) / 1e9, 1), "bound": bound, "frac_roofline": round(frac, 4)}
         if bound == "hbm":
             # back to back, the 8 MB weight matrix stays in the 256 MB Infinity Cache (MALL);
@@ -294,6 +302,61 @@ def _op_family(N, nd, g, policy) -> str:
             E.OP_CAST: "cast"}.get(nd.op, f"op{nd.op}")
 
 
+def copy_nodes_live(N, g, reps: int = 10) -> dict:
+    """Achieved bandwidth of a graph's Concat and Split nodes: each node's block copies,
+    built as the runtime's op_concat / op_split builds them (runs of dims[axis] * inner
+    elements per outer index, SPINN/run_time/ops/tensor/concat.c:5-26, split.c:5-26), are
+    launched through spinn_hip_block_copy `reps` times in a HIP graph replayed between HIP
+    events; bytes = every element read once and written once."""
+    import ctypes as C
+    import struct
+    from spinn_amd import ennf as E
+    from spinn_amd.devbuf import DeviceBuffer, time_graph
+    L = N.lib()
+    out = {}
+    for op, name in ((E.OP_CONCAT, "concat"), (E.OP_SPLIT, "split")):
+        nodes = [nd for nd in g.nodes if nd.op == op]
+        if not nodes:
+            continue
+        tot_ms = tot_b = 0.0
+        for nd in nodes:
+            axis = struct.unpack_from("<i", nd.params)[0] if len(nd.params) >= 4 else 0
+            src = nd.inputs if op == E.OP_CONCAT else [nd.inputs[0]]
+            dst = [nd.outputs[0]] if op == E.OP_CONCAT else nd.outputs
+            dims = g.dims(src[0])
+            axis = axis + len(dims) if axis < 0 else axis
+            outer = int(np.prod(dims[:axis])) if axis > 0 else 1
+            inner = int(np.prod(dims[axis + 1:])) if axis + 1 < len(dims) else 1
+            pieces = src if op == E.OP_CONCAT else dst
+            lens = [g.dims(t)[axis] * inner for t in pieces]
+            row = sum(lens)
+            whole = DeviceBuffer(4 * outer * row)
+            parts = [DeviceBuffer(4 * outer * n) for n in lens]
+            blocks = (N.BlockCopy * len(lens))()
+            off = 0
+            for i, (n, b) in enumerate(zip(lens, parts)):
+                if op == E.OP_CONCAT:
+                    blocks[i] = N.BlockCopy(b.ptr, whole.ptr, n, 0, row, off, n)
+                else:
+                    blocks[i] = N.BlockCopy(whole.ptr, b.ptr, row, off, n, 0, n)
+                off += n
+            def launch(st, blocks=blocks, nb=len(lens), outer=outer):
+                rc = 0
+                for i0 in range(0, nb, 16):  # SPINN_HIP_MAX_BLOCKS per launch, as op_concat / op_split do
+                    sub = C.cast(C.byref(blocks, i0 * C.sizeof(N.BlockCopy)), C.POINTER(N.BlockCopy))
+                    rc = rc or L.spinn_hip_block_copy(sub, min(16, nb - i0), outer, st)
+                return rc
+            ms = time_graph(launch, reps)
+            tot_ms += ms
+            tot_b += 2 * 4.0 * outer * row
+            for b in parts + [whole]:
+                b.free()
+        out[name] = {"nodes": len(nodes), "bytes": int(tot_b), "kernel_us": round(tot_ms * 1e3, 1),
+                     "achieved": round(tot_b / (tot_ms * 1e-3) / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(tot_b / (tot_ms * 1e-3) / 8e12, 4)}
+    return out
+
+
 def yolo_bench(N, Session, models, tmp: Path, reps: int) -> dict:
     """YOLOv10n 640x640 at batch 1 and 16, the whole exported graph including the
     TopK post-processing tail (output [B, 300, 6]): images/s (graph replay, input
@@ -324,8 +387,10 @@ def yolo_bench(N, Session, models, tmp: Path, reps: int) -> dict:
                     "layers": n_dw, "bytes": int(dw_b), "kernel_us": round(dw_ms * 1e3, 1),
                     "achieved": round(dw_b / (dw_ms * 1e-3) / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
                     "frac": round(dw_b / (dw_ms * 1e-3) / 8e12, 4),
-                    "method": "input + weights + output (+ residual) bytes of the depthwise layers / their "
-                              "kernel time, each layer launched 10x back to back between HIP events"}
+                    "method": "input + weights + bias + output (+ residual) bytes of the depthwise layers / their "
+                              "kernel time, each layer launched 10x back to back in a HIP graph replayed between "
+                              "HIP events"}
+            ent["copy_bandwidth"] = copy_nodes_live(N, g)
             ent["node_ms_total"] = round(float(node_ms.sum()), 4)
             ent["families_ms"] = {k: {"nodes": v[0], "ms": round(v[1], 4)}
                                   for k, v in sorted(fam.items(), key=lambda kv: -kv[1][1])}
@@ -356,6 +421,61 @@ def calibration_kernels() -> None:
     a.free()
     b.free()
     print("[bench] calibration kernels done", flush=True)
+
+
+def small_launches(reps: int = 20) -> None:
+    """Launches for a kernel profiler: the Conv3x3+BN+ReLU 1x64x56x56 layer, the five Gemm
+    sweep shapes (transB=1, bias vector) and YOLOv10n's 13 depthwise layers at batch 16,
+    `reps` launches each on the null stream (run it under rocprofv3 --kernel-trace --stats)."""
+    import ctypes as C
+    from spinn_amd import models
+    from spinn_amd import native as N
+    from spinn_amd.devbuf import DeviceBuffer
+    L = N.lib()
+    N.check(L.spinn_hip_init(0), "spinn_hip_init")
+    g, x = models.conv_bn_relu(seed=0)
+    rows = conv_table(g)
+    gy, _ = models.yolov10n(batch=16, seed=0)
+    rows += [r for r in conv_table(gy) if r["group"] > 1 and r["group"] == r["c"] == r["oc"]]
+    nbytes = lambda *dims: 4 * int(np.prod(dims))  # noqa: E731
+    for r in rows:
+        d = N.ConvDesc(*(r[f] for f in CONV_FIELDS), 0, 0)
+        d.algo = L.spinn_hip_conv_select_algo(C.byref(d))
+        bx = DeviceBuffer(nbytes(r["n"], r["c"], r["h"], r["w"]))
+        bw = DeviceBuffer(nbytes(r["oc"], r["c"] // r["group"], r["kh"], r["kw"]))
+        bb = DeviceBuffer(nbytes(r["oc"]))
+        by = DeviceBuffer(nbytes(r["n"], r["oc"], r["oh"], r["ow"]))
+        br = DeviceBuffer(nbytes(r["n"], r["oc"], r["oh"], r["ow"])) if r["act"] in (4, 5) else None
+        for b_ in (bx, bw, bb, by) + ((br,) if br else ()):
+            N.check(L.spinn_hip_fill_u32(b_.ptr, 0, b_.nbytes, None), "fill")
+        psz = L.spinn_hip_conv_packed_size(C.byref(d))
+        bp = DeviceBuffer(psz) if psz else None
+        if bp:
+            N.check(L.spinn_hip_conv_pack_weights(C.byref(d), bw.ptr, bp.ptr, None), "pack")
+        wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
+        ws = DeviceBuffer(wsz) if wsz else None
+        for _ in range(reps):
+            N.check(L.spinn_hip_conv(C.byref(d), bx.ptr, bw.ptr, bp.ptr if bp else None, bb.ptr,
+                                     br.ptr if br else None, by.ptr, ws.ptr if ws else None, wsz, None), "conv")
+        N.check(L.spinn_hip_stream_sync(None), "sync")
+        for b_ in (bx, bw, bb, by, br, bp, ws):
+            if b_:
+                b_.free()
+    for (m, n, k) in models.GEMM_SWEEP:
+        gd = N.GemmDesc(m, n, k, 0, 1, 1, 1.0, 1.0, 1, 0, 0, 0, 0)
+        ba, bb2, bc, by2 = DeviceBuffer(4 * m * k), DeviceBuffer(4 * n * k), DeviceBuffer(4 * n), DeviceBuffer(4 * m * n)
+        for b_ in (ba, bb2, bc):
+            N.check(L.spinn_hip_fill_u32(b_.ptr, 0, b_.nbytes, None), "fill")
+        wsz = L.spinn_hip_gemm_workspace_size(C.byref(gd))
+        ws = DeviceBuffer(wsz) if wsz else None
+        for _ in range(reps):
+            N.check(L.spinn_hip_gemm(C.byref(gd), ba.ptr, bb2.ptr, bc.ptr, by2.ptr, ws.ptr if ws else None, wsz,
+                                     None), "gemm")
+        N.check(L.spinn_hip_stream_sync(None), "sync")
+        for b_ in (ba, bb2, bc, by2, ws):
+            if b_:
+                b_.free()
+    print("[bench] small-config launches done", flush=True)
 
 
 COMPARE_LAYERS = [  # (n, c, h, w, oc, k, stride, pad, act): ResNet-101 batch-32 layers
@@ -439,13 +559,14 @@ CONV_FIELDS = ("n", "c", "h", "w", "oc", "oh", "ow", "kh", "kw", "sh", "sw", "ph
 def conv_layers_live(N, rows, algo_for, reps: int = 10) -> list:
     """Live kernel time of every distinct conv layer shape in `rows`: launched through
     spinn_hip_conv with the algorithm `algo_for(row)` names, `reps` times back to back
-    between two HIP events on the stream the kernels run on (the null stream), so the
-    figure carries no event or launch gap between nodes, unlike the per-node event pass.
+    inside a HIP graph replayed between two HIP events on the stream the kernels run
+    on, so the figure carries no host launch gap or event between the launches, unlike
+    the per-node event pass.
     One entry per shape: the row, its count, algorithm, ms per launch (all of the
     layer's kernels), direct and executed FLOPs and algorithmic bytes (input, weights,
     bias, output, residual; fp32, each once)."""
     import ctypes as C
-    from spinn_amd.devbuf import DeviceBuffer, time_launches
+    from spinn_amd.devbuf import DeviceBuffer, time_graph
     L = N.lib()
     if not rows:
         return []
@@ -475,11 +596,10 @@ def conv_layers_live(N, rows, algo_for, reps: int = 10) -> list:
                 N.check(L.spinn_hip_conv_pack_weights(C.byref(d), dev["w"].ptr, pk.ptr, None), "pack")
             has_res = r["act"] in (4, 5)
             res = dev["r"].ptr if has_res else None
-            launch = lambda: L.spinn_hip_conv(C.byref(d), dev["x"].ptr, dev["w"].ptr,  # noqa: E731
-                                              pk.ptr if pk else None, dev["b"].ptr, res, dev["y"].ptr,
-                                              ws.ptr if ws else None, wsz, None)
-            N.check(launch(), "conv")
-            ms = time_launches(launch, reps)
+            launch = lambda st: L.spinn_hip_conv(C.byref(d), dev["x"].ptr, dev["w"].ptr,  # noqa: E731
+                                                 pk.ptr if pk else None, dev["b"].ptr, res, dev["y"].ptr,
+                                                 ws.ptr if ws else None, wsz, st)
+            ms = time_graph(launch, reps)
             byts = (nbytes(r["n"], r["c"], r["h"], r["w"]) + nbytes(r["oc"], r["c"] // r["group"], r["kh"], r["kw"])
                     + nbytes(r["oc"]) + nbytes(r["n"], r["oc"], r["oh"], r["ow"]) * (2 if has_res else 1))
             out.append(dict(row=r, count=len(rs), algo=algo, ms=ms, flops=r["flops"],
@@ -504,7 +624,8 @@ def conv_kernels_live(N, rows, algo: int, reps: int = 10):
 def layers_markdown(live: list, batch: int, policy: str) -> str:
     """Per-layer table of one conv pass (one row per distinct layer shape)."""
     lines = [f"# ResNet-101 v1.5 fp32 conv layers, batch {batch}, policy {policy}", "",
-             "Each distinct layer shape launched 10x back to back through `spinn_hip_conv` between HIP events "
+             "Each distinct layer shape launched 10x back to back through `spinn_hip_conv` inside a HIP graph "
+             "replayed between HIP events "
              "(`bench.py`, conv_layers_live). GFLOP = direct-convolution count 2*N*OC*OH*OW*C*KH*KW; "
              "exec GFLOP = MFMA work actually issued (Winograd F(4x4,3x3): 36 GEMMs over 4x4 output tiles, "
              "transforms not counted). % peak against 157.3 TFLOP/s fp32 MFMA.", "",
@@ -634,6 +755,9 @@ def main() -> int:
     ap.add_argument("--gemm-compare", action="store_true",
                     help="only the launches of the MFMA-engine PMC comparison (three ResNet-101 conv layers, an "
                          "8192^3 Gemm here and through torch/hipBLASLt)")
+    ap.add_argument("--small-launches", action="store_true",
+                    help="only launch the config-0 conv, the Gemm sweep and the YOLOv10n b16 depthwise layers "
+                         "20x each (for rocprofv3 --kernel-trace --stats)")
     ap.add_argument("--calibration-kernels", action="store_true",
                     help="only run the known-size fill/copy kernels that scale the HBM byte counters")
     ap.add_argument("--traffic-summary", metavar="DIR",
@@ -645,6 +769,9 @@ def main() -> int:
         return 2
     if a.calibration_kernels:
         calibration_kernels()
+        return 0
+    if a.small_launches:
+        small_launches()
         return 0
     if a.gemm_compare:
         gemm_compare()
@@ -812,7 +939,8 @@ def main() -> int:
             "tflops_executed": round(live_ef / (live_ms * 1e-3) / 1e12, 2),
             "frac_mfma_peak_executed": round(live_ef / (live_ms * 1e-3) / PEAK_FP32_MFMA, 4),
             "winograd_layers": sum(e["count"] for e in live if e["algo"] in (N.ALGO_WINOGRAD, N.ALGO_WINOGRAD_F43)),
-            "method": "every conv layer's kernels launched 10x back to back between HIP events; direct = "
+            "method": "every conv layer's kernels launched 10x back to back in a HIP graph replayed between HIP "
+                      "events; direct = "
                       "2*N*OC*OH*OW*C*KH*KW (Winograd credited at the direct count), executed = the MFMA work "
                       "issued (Winograd: (m+2)^2 tile GEMMs, transforms not counted)"},
         "roofline": {"bound": "mfma", "achieved": round(ig_tflops, 3), "peak": PEAK_FP32_MFMA / 1e12,
@@ -822,7 +950,7 @@ def main() -> int:
                      "launch_us": round(ig_live_ms / max(n_ig, 1) * 1e3, 2),
                      "achieved_node_events": round(ig_node_tflops, 3),
                      "method": "direct-conv FLOPs of the implicit-GEMM layers / their kernel time, each "
-                               "layer's kernel launched 10x back to back between HIP events "
+                               "layer's kernel launched 10x back to back in a HIP graph replayed between HIP events "
                                "(achieved_node_events: per-node events inside the model pass)"},
         "cpu_baseline": cpu,
         "other_configs": other,

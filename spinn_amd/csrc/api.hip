@@ -143,7 +143,7 @@ int spinn_hip_conv(const SpinnHipConvDesc *d, const float *x, const float *w, co
     switch (algo) {
     case SPINN_CONV_ALGO_IMPLICIT_GEMM:
         if (!packed_w) return SPINN_HIP_EINVAL;
-        return igemm_conv(d, x, packed_w, bias, residual, y, workspace, workspace_bytes, st);
+        return igemm_conv(d, x, w, packed_w, bias, residual, y, workspace, workspace_bytes, st);
     case SPINN_CONV_ALGO_WINOGRAD:
     case SPINN_CONV_ALGO_WINOGRAD_F43:
         if (!winograd_eligible(d)) return SPINN_HIP_EUNSUPPORTED;

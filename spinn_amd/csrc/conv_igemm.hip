@@ -260,14 +260,20 @@ static TileChoice igemm_tiles(const SpinnHipConvDesc *d) {
     return choose_tiles(OCg, ntot, K, d->group, d->group == 1);
 }
 
+static bool igemm_wavek(const SpinnHipConvDesc *d) {
+    return use_wavek(d->oc / d->group, d->n * d->oh * d->ow, (d->c / d->group) * d->kh * d->kw, d->group);
+}
+
 size_t igemm_workspace_bytes(const SpinnHipConvDesc *d) {
+    if (igemm_wavek(d)) return 0;
     TileChoice tc = igemm_tiles(d);
     if (tc.split <= 1) return 0;
     return (size_t)tc.split * d->oc * ((size_t)d->n * d->oh * d->ow) * sizeof(float);
 }
 
-int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed, const float *bias,
                const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st) {
+    if (igemm_wavek(d)) return wavek_conv(d, x, w, packed, bias, res, y, st);
     ConvKArgs a{};
     const int OCg = d->oc / d->group;
     a.ldw = (OCg + 3) / 4 * 4;

@@ -7,6 +7,7 @@
 // kernel is organised for HBM: one thread per output pixel, consecutive
 // threads on consecutive ow (coalesced loads and stores), the channel's
 // KHxKW filter broadcast from scalar registers, the epilogue fused.
+#include "mfma_core.h"
 #include "spinn_hip_internal.h"
 
 namespace spinn {
@@ -154,6 +155,120 @@ __global__ __launch_bounds__(256) void dw_tiled_kernel(const float *__restrict__
     }
 }
 
+// Depthwise convolution without LDS: one thread computes RPT x 4 outputs (RPT
+// rows of 4 horizontally adjacent outputs) of one plane, reading each input
+// row of its window as three 16-byte loads through a bounds-checked buffer
+// (zero outside the image) that the L1 / L2 share between neighbouring
+// threads. Thousands of independent threads with a dozen loads each keep the
+// HBM queue full without staging; the epilogue is fused and stores float4.
+// Needs 16-byte input rows (W % 4 == 0) and the begin column pad K/2 (the
+// window's columns then sit at compile-time positions of the three loads).
+template <int K, int S, int RPT, bool VEC>
+__global__ __launch_bounds__(256) void dw_direct_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                        const float *__restrict__ bias,
+                                                        const float *__restrict__ res, float *__restrict__ y,
+                                                        SpinnHipConvDesc d, int row_groups, int owq, int64_t total) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= total) return;
+    const int64_t per_plane = (int64_t)row_groups * owq;
+    const int64_t pl = t / per_plane;
+    const int rem = (int)(t - pl * per_plane);
+    const int rg = rem / owq;
+    const int q = rem - rg * owq;
+    const int c = (int)(pl % d.c);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(((int64_t)d.n * d.c) * d.h * d.w * 4));
+    float wk[K * K];
+#pragma unroll
+    for (int i = 0; i < K * K; ++i) wk[i] = w[(int64_t)c * K * K + i];
+    constexpr int IR = (RPT - 1) * S + K; // input rows of the thread's window
+    const int ih0 = rg * RPT * S - d.ph;
+    const int col0 = 4 * q * S - 4; // first column of the three 16-byte loads
+    const uint32_t plane_off = (uint32_t)(pl * d.h * d.w);
+    float acc[RPT][4];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[r][j] = 0.f;
+#pragma unroll
+    for (int ir = 0; ir < IR; ++ir) {
+        const int ih = ih0 + ir;
+        const bool row_ok = (unsigned)ih < (unsigned)d.h;
+        float v[12];
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            const int col = col0 + 4 * u;
+            const bool ok = row_ok && col >= 0 && col < d.w;
+            const f32x4 f = buf_f32x4(rx, ok ? (plane_off + (uint32_t)ih * d.w + col) * 4u : kOOB);
+            v[4 * u + 0] = f[0];
+            v[4 * u + 1] = f[1];
+            v[4 * u + 2] = f[2];
+            v[4 * u + 3] = f[3];
+        }
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const int kh = ir - r * S;
+            if (kh >= 0 && kh < K) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int kw = 0; kw < K; ++kw)
+                        acc[r][j] = fmaf(wk[kh * K + kw], v[4 - K / 2 + j * S + kw], acc[r][j]);
+            }
+        }
+    }
+    const float bv = bias ? bias[c] : 0.f;
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        const int oh = rg * RPT + r;
+        if (oh >= d.oh) break;
+        const int ow0 = 4 * q;
+        const int64_t o = (pl * d.oh + oh) * (int64_t)d.ow + ow0;
+        if constexpr (VEC) {
+            float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (res) rv = *reinterpret_cast<const float4 *>(res + o);
+            float4 out;
+            out.x = apply_act(acc[r][0] + bv + rv.x, d.act);
+            out.y = apply_act(acc[r][1] + bv + rv.y, d.act);
+            out.z = apply_act(acc[r][2] + bv + rv.z, d.act);
+            out.w = apply_act(acc[r][3] + bv + rv.w, d.act);
+            *reinterpret_cast<float4 *>(y + o) = out;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (ow0 + j < d.ow) {
+                    float vv = acc[r][j] + bv;
+                    if (res) vv += res[o + j];
+                    y[o + j] = apply_act(vv, d.act);
+                }
+            }
+        }
+    }
+}
+
+template <int K, int S, int RPT>
+static int launch_dw_direct(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias,
+                            const float *res, float *y, hipStream_t st) {
+    const int owq = (d->ow + 3) / 4;
+    const int row_groups = (d->oh + RPT - 1) / RPT;
+    const int64_t total = (int64_t)d->n * d->c * row_groups * owq;
+    const int64_t blocks = (total + 255) / 256;
+    if (blocks > INT32_MAX) return SPINN_HIP_EUNSUPPORTED;
+    const bool vec = d->ow % 4 == 0 && ((uintptr_t)y & 15u) == 0 && (!res || ((uintptr_t)res & 15u) == 0);
+    if (vec)
+        hipLaunchKernelGGL((dw_direct_kernel<K, S, RPT, true>), dim3((unsigned)blocks), dim3(256), 0, st, x, w, bias,
+                           res, y, *d, row_groups, owq, total);
+    else
+        hipLaunchKernelGGL((dw_direct_kernel<K, S, RPT, false>), dim3((unsigned)blocks), dim3(256), 0, st, x, w,
+                           bias, res, y, *d, row_groups, owq, total);
+    return check_launch();
+}
+
+static bool dw_direct_ok(const SpinnHipConvDesc *d) {
+    static_assert(3 * 2 + 3 - 3 / 2 <= 8 && 3 + 7 - 7 / 2 <= 8, "three 16-byte loads cover the window");
+    return d->w % 4 == 0 && d->pw == d->kw / 2 &&
+           (int64_t)d->n * d->c * d->h * d->w * 4 <= (int64_t)kMaxOperandBytes;
+}
+
 // Stem convolutions with few input channels (RGB images): one thread per
 // output pixel computes a chunk of 16 output channels, reading each input
 // channel's KH x KW window into registers once and the chunk's weights from
@@ -255,6 +370,15 @@ int direct_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const
                 float *y, hipStream_t st) {
     const int ohw = d->oh * d->ow;
     const bool depthwise = d->group == d->c && d->group == d->oc && d->kh == d->kw && d->sh == d->sw;
+    if (depthwise && dw_direct_ok(d) && (d->kh == 3 || d->kh == 5 || d->kh == 7) &&
+        (d->sh == 1 || (d->sh == 2 && d->kh == 3))) {
+        // Measured on YOLOv10n's 13 depthwise layers at batch 16: 114 us against 180 us for the
+        // LDS-tiled kernel below and 162 us for LDS staging by asynchronous copies in two stages.
+        if (d->kh == 3 && d->sh == 1) return launch_dw_direct<3, 1, 4>(d, x, w, bias, res, y, st);
+        if (d->kh == 3) return launch_dw_direct<3, 2, 2>(d, x, w, bias, res, y, st);
+        if (d->kh == 5) return launch_dw_direct<5, 1, 4>(d, x, w, bias, res, y, st);
+        return launch_dw_direct<7, 1, 2>(d, x, w, bias, res, y, st);
+    }
     if (depthwise && (int64_t)((d->oh + kDwTH - 1) / kDwTH) * ((d->ow + kDwTW - 1) / kDwTW) <= 65535) {
         if (d->kh == 3 && d->sh == 1) return launch_dw<3, 1>(d, x, w, bias, res, y, st);
         if (d->kh == 3 && d->sh == 2) return launch_dw<3, 2>(d, x, w, bias, res, y, st);

@@ -245,8 +245,12 @@ bool gemm_is_gemv(const SpinnHipGemmDesc *d) {
 
 } // namespace
 
+static bool gemm_wavek(const SpinnHipGemmDesc *d) {
+    return use_wavek(d->m, d->n, d->k, d->batch > 0 ? d->batch : 1);
+}
+
 size_t gemm_workspace_bytes(const SpinnHipGemmDesc *d) {
-    if (gemm_is_gemv(d)) return 0;
+    if (gemm_is_gemv(d) || gemm_wavek(d)) return 0;
     TileChoice tc = gemm_tiles(d);
     if (tc.split <= 1) return 0;
     return (size_t)tc.split * d->m * (size_t)d->n * sizeof(float);
@@ -289,6 +293,7 @@ int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const fl
                                d->beta, Y, d->m, d->n, d->k);
         return check_launch();
     }
+    if (gemm_wavek(d)) return wavek_gemm(d, A, B, C, Y, st);
     TileChoice tc = gemm_tiles(d);
     if (tc.split > 1) {
         const size_t need = (size_t)tc.split * d->m * (size_t)d->n * sizeof(float);

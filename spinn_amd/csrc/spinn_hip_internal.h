@@ -52,6 +52,16 @@ struct TileChoice {
 };
 TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split);
 void force_tiles(int bm, int bn, int split);
+// True when an (M x N x K) problem repeated `reps` times runs on the wave-K
+// kernel (32 x 32 tiles, K split over a workgroup's waves) instead of the
+// 64/128-wide tiles of choose_tiles.
+bool use_wavek(int M, int N, int K, int reps);
+
+// wave-K kernels (wavek.hip): no workspace, packed conv weights as igemm_pack
+int wavek_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed, const float *bias,
+               const float *res, float *y, hipStream_t st);
+int wavek_gemm(const SpinnHipGemmDesc *d, const float *A, const float *B, const float *C, float *Y,
+               hipStream_t st);
 
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cu_count();
@@ -64,7 +74,7 @@ int noalloc_scratch(int device, void **ptr);
 int64_t igemm_packed_floats(const SpinnHipConvDesc *d);
 int igemm_pack(const SpinnHipConvDesc *d, const float *w, float *packed, hipStream_t st);
 size_t igemm_workspace_bytes(const SpinnHipConvDesc *d);
-int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed, const float *bias,
                const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st);
 size_t gemm_workspace_bytes(const SpinnHipGemmDesc *d);
 int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const float *C, float *Y, void *ws,

@@ -1,5 +1,6 @@
 // tiles.hip - output-tile and split-K choice shared by the MFMA GEMM launches.
 #include "spinn_hip_internal.h"
+#include <cstdlib>
 
 namespace spinn {
 
@@ -12,6 +13,31 @@ void force_tiles(int bm, int bn, int split) {
     g_force_bm = bm;
     g_force_bn = bn;
     g_force_split = split;
+}
+
+static int env_wavek() {
+    // SPINN_WAVEK=0 never runs the wave-K kernel, 1 runs it for every shape;
+    // unset = per-shape choice.
+    static int v = [] {
+        const char *e = std::getenv("SPINN_WAVEK");
+        if (!e || !*e) return -1;
+        return e[0] == '0' ? 0 : 1;
+    }();
+    return v;
+}
+
+bool use_wavek(int M, int N, int K, int reps) {
+    if (g_force_bm) return g_force_bm == 32 && g_force_bn == 32;
+    const int e = env_wavek();
+    if (e >= 0) return e == 1;
+    // Measured on MI355X (ResNet-101 and YOLOv10n at batch 1, the Gemm sweep): the
+    // wave-K kernel wins where 64 x 64 tiles underfill the chip and K is 128..576
+    // (one to a few 32-deep chunks per wave); with longer K its one-float-per-lane
+    // operand loads cost more than the 64 x 64 tiles' split-K reduction launch,
+    // and below 128 it saves nothing.
+    const int cus = device_cu_count();
+    const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * reps;
+    return tiles64 < cus && K >= 128 && K <= 576;
 }
 
 static bool valid_tile(int bm, int bn) {

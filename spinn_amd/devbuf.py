@@ -95,3 +95,41 @@ def time_cold(fn, flush, reps: int) -> float:
         L.spinn_hip_event_destroy(e0)
         L.spinn_hip_event_destroy(e1)
     return total / reps
+
+
+def time_graph(fn, reps: int, replays: int = 5) -> float:
+    """Mean milliseconds per call of `fn(stream)` measured GPU-side: `reps` calls
+    are captured into one HIP graph on a stream of their own and the graph is
+    replayed `replays` times between two HIP events on that stream, so the
+    figure carries no host launch gap between the calls (which dominates
+    back-to-back launches of kernels of a few microseconds)."""
+    L = N.lib()
+    st = C.c_void_p()
+    N.check(L.spinn_hip_stream_create(C.byref(st)), "stream")
+    g = C.c_void_p()
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    N.check(L.spinn_hip_event_create(C.byref(e0)), "event")
+    N.check(L.spinn_hip_event_create(C.byref(e1)), "event")
+    try:
+        N.check(fn(st), "warm-up call")
+        N.check(L.spinn_hip_stream_sync(st), "sync")
+        N.check(L.spinn_hip_graph_capture_begin(st), "capture")
+        rcs = [fn(st) for _ in range(reps)]
+        N.check(L.spinn_hip_graph_capture_end(st, C.byref(g)), "capture end")
+        for rc in rcs:
+            N.check(rc, "captured call")
+        N.check(L.spinn_hip_graph_launch(g, st), "replay")
+        N.check(L.spinn_hip_event_record(e0, st), "record")
+        for _ in range(replays):
+            N.check(L.spinn_hip_graph_launch(g, st), "replay")
+        N.check(L.spinn_hip_event_record(e1, st), "record")
+        N.check(L.spinn_hip_stream_sync(st), "sync")
+        ms = C.c_float()
+        N.check(L.spinn_hip_event_elapsed_ms(e0, e1, C.byref(ms)), "elapsed")
+        return ms.value / (reps * replays)
+    finally:
+        if g:
+            L.spinn_hip_graph_destroy(g)
+        L.spinn_hip_event_destroy(e0)
+        L.spinn_hip_event_destroy(e1)
+        L.spinn_hip_stream_destroy(st)

@@ -120,6 +120,16 @@ def test_splitk_repeats_bit_identical(hip, torch_gpu, shape):
     n, c, h, w, oc, k, p, act = shape
     L = hip.lib()
     d = conv_desc(hip, n, c, h, w, oc, k, k, 1, 1, p, p, 1, act, hip.ALGO_IMPLICIT_GEMM)
+    L.spinn_hip_tune_force_tiles(64, 64, 4)  # 64 x 64 tiles, K split 4 ways over workgroups
+    try:
+        _splitk_repeats(hip, torch, L, d, shape)
+    finally:
+        L.spinn_hip_tune_force_tiles(0, 0, 0)
+
+
+def _splitk_repeats(hip, torch, L, d, shape):
+    import ctypes as C
+    n, c, h, w, oc, k, p, act = shape
     wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
     assert wsz > 0, "shape no longer splits K; pick one that does"
     x, wt, b, r = _inputs(11, n, c, h, w, oc, k, 1, act, d.oh, d.ow)

@@ -15,7 +15,8 @@ from tests.hipops import conv_desc
 
 pytestmark = pytest.mark.gpu
 
-# pairs of (n, c, h, w, oc, k, stride, pad, group, act, algo): a larger call, then a smaller one
+# pairs of (n, c, h, w, oc, k, stride, pad, group, act, algo): a larger call, then a smaller one;
+# "splitk" pairs run with 64 x 64 tiles and K split 4 ways over workgroups (partials in the scratch)
 PAIRS = [
     ("splitk_then_smaller_splitk", (1, 1024, 7, 8, 256, 1, 1, 0, 1, 5, 1), (1, 512, 7, 7, 512, 3, 1, 1, 1, 1, 1)),
     ("f43_b32_then_f43_b2", (32, 256, 14, 14, 256, 3, 1, 1, 1, 1, 4), (2, 128, 28, 28, 128, 3, 1, 1, 1, 5, 4)),
@@ -46,14 +47,24 @@ def _operands(torch, L, hip, case, seed):
 
 @pytest.mark.parametrize("pair", PAIRS, ids=[p[0] for p in PAIRS])
 def test_noalloc_matches_workspace_entry_point(hip, torch_gpu, pair):
-    torch = torch_gpu
     L = hip.lib()
+    if "splitk" in pair[0]:
+        L.spinn_hip_tune_force_tiles(64, 64, 4)
+    try:
+        _compare_pair(hip, torch_gpu, L, pair)
+    finally:
+        L.spinn_hip_tune_force_tiles(0, 0, 0)
+
+
+def _compare_pair(hip, torch, L, pair):
     name, big, small = pair
     for i, case in enumerate((big, small)):
         d, (xd, wd, pk, bd, rd), ref = _operands(torch, L, hip, case, zlib.crc32(f"{name}{i}".encode()))
         wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
         print(f"[noalloc] {name} call {i}: algo={d.algo} scratch={wsz}", flush=True)
         assert wsz <= hip.NOALLOC_SCRATCH_BYTES
+        if "splitk" in name:
+            assert wsz > 0, "the split-K pair must use the scratch"
         ws = torch.empty(max(wsz // 4, 1), device="cuda") if wsz else None
         y_ws = torch.full((d.n, d.oc, d.oh, d.ow), float("nan"), device="cuda")
         y_na = torch.full((d.n, d.oc, d.oh, d.ow), float("nan"), device="cuda")
