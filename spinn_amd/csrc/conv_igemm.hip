@@ -36,7 +36,9 @@ struct ConvKArgs {
     int k_chunk;       // K per split (multiple of kBK)
 };
 
-template <int BM, int BN, int BK, class BLoader, bool SPLIT>
+// AC: the post-op class (act_class), fixed at compile time so the epilogue has no
+// per-element branch on it.
+template <int BM, int BN, int BK, class BLoader, bool SPLIT, int AC>
 __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
     using WT = WaveTiling<BM, BN>;
     constexpr int SA = LdsPad<BM>::stride;
@@ -124,20 +126,31 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
                 }
         }
     } else {
+        // A tile whose rows all exist (the usual case: OC a multiple of the tile)
+        // stores without a per-element row test.
+        const bool full_m = m0 + BM <= a.M;
 #pragma unroll
         for (int j = 0; j < WT::TN; ++j) {
             const int jcol = n0 + wn0 + j * 32 + l32;
             if (jcol >= ntot) continue;
             const int img = jcol / a.OHW;
             const int p = jcol - img * a.OHW;
-            const int64_t ybase = ((int64_t)img * a.OC + (int64_t)group * a.M) * a.OHW + p;
+            float *yp = a.y + ((int64_t)img * a.OC + (int64_t)group * a.M + m0 + wm0 + 4 * h) * a.OHW + p;
+            if (full_m) {
 #pragma unroll
-            for (int i = 0; i < WT::TM; ++i)
+                for (int i = 0; i < WT::TM; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < a.M) a.y[ybase + (int64_t)m * a.OHW] = apply_act(acc[i][j][r], a.act);
-                }
+                    for (int r = 0; r < 16; ++r)
+                        yp[(int64_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * a.OHW] = apply_act_c<AC>(acc[i][j][r]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int mo = i * 32 + 8 * (r >> 2) + (r & 3);
+                        if (m0 + wm0 + 4 * h + mo < a.M) yp[(int64_t)mo * a.OHW] = apply_act_c<AC>(acc[i][j][r]);
+                    }
+            }
         }
     }
 }
@@ -201,10 +214,14 @@ namespace {
 template <int BM, int BN, class BL>
 int launch_conv_tile(const ConvKArgs &a, int groups, int split, hipStream_t st) {
     dim3 grid((a.geom.ntot + BN - 1) / BN, (a.M + BM - 1) / BM, split > 1 ? split : groups);
-    if (split > 1)
-        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, kBK, BL, true>), grid, dim3(kThreads), 0, st, a);
+    if (split > 1) // the post-op runs in the reduction kernel
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, kBK, BL, true, 0>), grid, dim3(kThreads), 0, st, a);
+    else if (act_class(a.act) == 1)
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, kBK, BL, false, 1>), grid, dim3(kThreads), 0, st, a);
+    else if (act_class(a.act) == 3)
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, kBK, BL, false, 3>), grid, dim3(kThreads), 0, st, a);
     else
-        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, kBK, BL, false>), grid, dim3(kThreads), 0, st, a);
+        hipLaunchKernelGGL((conv_igemm_kernel<BM, BN, kBK, BL, false, 0>), grid, dim3(kThreads), 0, st, a);
     return check_launch();
 }
 

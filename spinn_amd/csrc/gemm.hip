@@ -85,6 +85,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_kernel(GemmKArgs a) {
                 const int m = m0 + wm0 + (q >> 4) * 32 + 8 * ((q & 15) >> 2) + 4 * h + (q & 3);
                 if (m < a.M) a.ws[((int64_t)z * a.M + m) * a.N + n] = acc[q >> 4][j][q & 15];
             }
+        } else if (a.c_mode == 0 && m0 + BM <= a.M) {
+            // no C and every row of the tile exists (the batched Winograd GEMMs):
+            // no per-element test or C load
+            float *yp = a.y + batch * a.stride_y + (int64_t)(m0 + wm0 + 4 * h) * a.N + n;
+#pragma unroll
+            for (int q = 0; q < NR; ++q)
+                yp[(int64_t)((q >> 4) * 32 + 8 * ((q & 15) >> 2) + (q & 3)) * a.N] = a.alpha * acc[q >> 4][j][q & 15];
         } else {
             float cv[NR];
 #pragma unroll

@@ -22,6 +22,18 @@ __device__ __forceinline__ float apply_act(float v, int act) {
     return v;
 }
 
+// The fused post-op as a compile-time class: 0 = none (NONE, CLIP, ADD), 1 = ReLU
+// (RELU, ADD_RELU), 3 = SiLU; the bias and residual are added before it.
+__host__ __device__ constexpr int act_class(int act) {
+    return (act == SPINN_ACT_RELU || act == SPINN_ACT_ADD_RELU) ? 1 : (act == SPINN_ACT_SILU ? 3 : 0);
+}
+template <int AC>
+__device__ __forceinline__ float apply_act_c(float v) {
+    if constexpr (AC == 1) return v < 0.f ? 0.f : v;
+    else if constexpr (AC == 3) return v / (1.0f + expf(-v));
+    else return v;
+}
+
 // Sum of the split-K partials ws[s * plane + e] for s = 0..nsplit-1, added in
 // split order starting from 0 (the order the partials' K ranges take). The
 // loads of a group of 8 splits are issued before the first add: a plain loop
