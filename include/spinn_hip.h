@@ -273,7 +273,8 @@ const char *spinn_hip_error_string(int code);
 
 /* Tuning hook: force the MFMA GEMM output tile (bm, bn in {64, 128}) and K
  * split for every later conv/Gemm launch and workspace query; bm = bn = 32
- * forces the wave-K kernel (32 x 32 tiles, K split over a workgroup's waves);
+ * (or 16) forces the wave-K kernel (32 x 32 or 16 x 16 tiles, K split over a
+ * workgroup's waves);
  * bm = 0 restores the per-shape choice. Change it only between plans: packed weights do not
  * depend on it, workspace sizes do. No counterpart in the reference. */
 void spinn_hip_tune_force_tiles(int bm, int bn, int split);

@@ -277,8 +277,11 @@ static TileChoice igemm_tiles(const SpinnHipConvDesc *d) {
     return choose_tiles(OCg, ntot, K, d->group, d->group == 1);
 }
 
-static bool igemm_wavek(const SpinnHipConvDesc *d) {
-    return use_wavek(d->oc / d->group, d->n * d->oh * d->ow, (d->c / d->group) * d->kh * d->kw, d->group);
+static int igemm_wavek(const SpinnHipConvDesc *d) {
+    const bool pointwise = d->kh == 1 && d->kw == 1 && d->sh == 1 && d->sw == 1 && d->ph == 0 && d->pw == 0 &&
+                           d->oh == d->h && d->ow == d->w;
+    return wavek_tile(d->oc / d->group, d->n * d->oh * d->ow, (d->c / d->group) * d->kh * d->kw, d->group,
+                      pointwise);
 }
 
 size_t igemm_workspace_bytes(const SpinnHipConvDesc *d) {
@@ -290,7 +293,7 @@ size_t igemm_workspace_bytes(const SpinnHipConvDesc *d) {
 
 int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed, const float *bias,
                const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st) {
-    if (igemm_wavek(d)) return wavek_conv(d, x, w, packed, bias, res, y, st);
+    if (const int ts = igemm_wavek(d)) return wavek_conv(d, ts, x, w, packed, bias, res, y, st);
     ConvKArgs a{};
     const int OCg = d->oc / d->group;
     a.ldw = (OCg + 3) / 4 * 4;

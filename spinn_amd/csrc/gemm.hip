@@ -252,8 +252,8 @@ bool gemm_is_gemv(const SpinnHipGemmDesc *d) {
 
 } // namespace
 
-static bool gemm_wavek(const SpinnHipGemmDesc *d) {
-    return use_wavek(d->m, d->n, d->k, d->batch > 0 ? d->batch : 1);
+static int gemm_wavek(const SpinnHipGemmDesc *d) {
+    return wavek_tile(d->m, d->n, d->k, d->batch > 0 ? d->batch : 1, false);
 }
 
 size_t gemm_workspace_bytes(const SpinnHipGemmDesc *d) {
@@ -300,7 +300,7 @@ int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const fl
                                d->beta, Y, d->m, d->n, d->k);
         return check_launch();
     }
-    if (gemm_wavek(d)) return wavek_gemm(d, A, B, C, Y, st);
+    if (const int ts = gemm_wavek(d)) return wavek_gemm(d, ts, A, B, C, Y, st);
     TileChoice tc = gemm_tiles(d);
     if (tc.split > 1) {
         const size_t need = (size_t)tc.split * d->m * (size_t)d->n * sizeof(float);

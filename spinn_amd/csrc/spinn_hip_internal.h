@@ -64,15 +64,15 @@ struct TileChoice {
 };
 TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split);
 void force_tiles(int bm, int bn, int split);
-// True when an (M x N x K) problem repeated `reps` times runs on the wave-K
-// kernel (32 x 32 tiles, K split over a workgroup's waves) instead of the
-// 64/128-wide tiles of choose_tiles.
-bool use_wavek(int M, int N, int K, int reps);
+// Output tile edge of the wave-K kernel (K split over a workgroup's waves) for
+// an (M x N x K) problem repeated `reps` times: 32 or 16, or 0 when it runs on the
+// 64/128-wide tiles of choose_tiles. `pointwise`: a 1x1 stride-1 unpadded conv.
+int wavek_tile(int M, int N, int K, int reps, bool pointwise);
 
 // wave-K kernels (wavek.hip): no workspace, packed conv weights as igemm_pack
-int wavek_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed, const float *bias,
+int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w, const float *packed, const float *bias,
                const float *res, float *y, hipStream_t st);
-int wavek_gemm(const SpinnHipGemmDesc *d, const float *A, const float *B, const float *C, float *Y,
+int wavek_gemm(const SpinnHipGemmDesc *d, int ts, const float *A, const float *B, const float *C, float *Y,
                hipStream_t st);
 
 // Compute units of the current device (cached per device; 256 on MI355X).

@@ -26,18 +26,25 @@ static int env_wavek() {
     return v;
 }
 
-bool use_wavek(int M, int N, int K, int reps) {
-    if (g_force_bm) return g_force_bm == 32 && g_force_bn == 32;
+int wavek_tile(int M, int N, int K, int reps, bool pointwise) {
+    if (g_force_bm) return (g_force_bm == g_force_bn && (g_force_bm == 32 || g_force_bm == 16)) ? g_force_bm : 0;
     const int e = env_wavek();
-    if (e >= 0) return e == 1;
-    // Measured on MI355X (ResNet-101 and YOLOv10n at batch 1, the Gemm sweep): the
-    // wave-K kernel wins where 64 x 64 tiles underfill the chip and K is 128..576
+    if (e >= 0) return e == 1 ? 32 : 0;
+    const int cus = device_cu_count();
+    const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * reps;
+    if (tiles64 >= cus) return 0;
+    // Measured on MI355X (ResNet-101 and YOLOv10n at batch 1, the Gemm sweep).
+    // 16 x 16 tiles: 1x1 convs whose 32 x 32 grid covers at most half the CUs with
+    // K of 256..1024 (the 1024 -> 256 layers at 14x14: 8.1 -> 5.8 us, split-K's
+    // reduction launch gone). Their B loads are one float per k and lane, so a
+    // 3x3 gather or a longer K stays on 32-wide or split-K tiles.
+    const int64_t tiles32 = (int64_t)((M + 31) / 32) * ((N + 31) / 32) * reps;
+    if (pointwise && tiles32 <= cus / 2 && K >= 256 && K <= 1024) return 16;
+    // 32 x 32 tiles where 64 x 64 tiles underfill the chip and K is 128..576
     // (one to a few 32-deep chunks per wave); with longer K its one-float-per-lane
     // operand loads cost more than the 64 x 64 tiles' split-K reduction launch,
     // and below 128 it saves nothing.
-    const int cus = device_cu_count();
-    const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * reps;
-    return tiles64 < cus && K >= 128 && K <= 576;
+    return (K >= 128 && K <= 576) ? 32 : 0;
 }
 
 static bool valid_tile(int bm, int bn) {

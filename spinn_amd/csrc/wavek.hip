@@ -2,8 +2,8 @@
 // 64 x 64 tiles (convolution layers at batch 1, the single Conv3x3+BN+ReLU
 // layer, the Gemm sweep, fully-connected layers over a batch).
 //
-// One workgroup owns one 32 x 32 output tile and splits its K range over its
-// KG waves. Each wave streams its operands from memory straight into MFMA
+// One workgroup owns one TS x TS output tile (TS = 32, or 16 where 32-wide
+// tiles still leave most CUs idle) and splits its K range over its KG waves. Each wave streams its operands from memory straight into MFMA
 // operand registers - no LDS staging and no barrier in the K loop, two chunks
 // of 32 k in flight - and the KG partial tiles are summed in a fixed order
 // through LDS before the fused epilogue. This replaces, for these shapes,
@@ -13,10 +13,13 @@
 // v_mfma_f32_32x32x2f32 register layout: A operand lane l = A[l%32][k],
 // B operand lane l = B[k][l%32], accumulator element r of lane l =
 // D[8*(r/4) + 4*(l/32) + r%4][l%32]; the two half-waves h = l/32 supply the
-// two k of a step. A block of 8 k is 4 steps q and half-wave h of step q takes
-// k = 4h + q: a k-contiguous operand is then one 16-byte load per lane per
-// block. (Which k feeds which step and half does not change the sum's terms;
-// A and B use the same assignment.)
+// two k of a step. v_mfma_f32_16x16x4f32: A lane l = A[l%16][k], B lane l =
+// B[k][l%16], accumulator element r of lane l = D[4*(l/16) + r][l%16]; the four
+// lane groups h = l/16 supply the four k of a step. A block of 4 * groups k
+// (8 or 16) is 4 steps q, and lane group h of step q takes k = 4h + q: a
+// k-contiguous operand is then one 16-byte load per lane per block. (Which k
+// feeds which step and group does not change the sum's terms; A and B use the
+// same assignment.)
 #include "mfma_core.h"
 #include "spinn_hip_internal.h"
 #include <type_traits>
@@ -25,10 +28,39 @@ namespace spinn {
 
 namespace {
 
-constexpr int kWkTile = 32;  // output tile edge
-constexpr int kWkChunk = 32; // k per chunk: 4 blocks of 8
+// The MFMA shape of a TS x TS tile: lane groups, k per block (4 steps), and
+// the accumulator.
+template <int TS>
+struct WkShape;
+template <>
+struct WkShape<32> {
+    using Acc = f32x16;
+    static constexpr int kAcc = 16;
+    static constexpr int kBlock = 8; // 2 lane groups x 4 steps
+    __device__ static int group(int lane) { return lane >> 5; }
+    __device__ static int col(int lane) { return lane & 31; }
+    __device__ static int row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+    __device__ static Acc mfma(float a, float b, const Acc &c) {
+        return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    }
+};
+template <>
+struct WkShape<16> {
+    using Acc = f32x4;
+    static constexpr int kAcc = 4;
+    static constexpr int kBlock = 16; // 4 lane groups x 4 steps
+    __device__ static int group(int lane) { return lane >> 4; }
+    __device__ static int col(int lane) { return lane & 15; }
+    __device__ static int row(int r, int lane) { return 4 * (lane >> 4) + r; }
+    __device__ static Acc mfma(float a, float b, const Acc &c) {
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+};
+// k per chunk: 4 blocks
+template <int TS>
+constexpr int wk_chunk() { return 4 * WkShape<TS>::kBlock; }
 
-// ---- operand fetchers: one 8-deep k block, the lane's 4 values (steps q) ----
+// ---- operand fetchers: one k block, the lane's 4 values (steps q) of lane group h ----
 
 // Source [K][ld] with the tile index contiguous: v[q] = src[(k0 + 4h + q) * ld + t].
 struct WkTContig {
@@ -110,7 +142,7 @@ struct WkPointwise {
 };
 
 // Implicit-GEMM B operand, K in (kh, kw, c) order with Cg % 16 == 0: a block
-// of 8 k lies in one tap, so one bounds test per block.
+// of 8 or 16 k lies in one tap, so one bounds test per block.
 struct WkTap {
     __amdgpu_buffer_rsrc_t rsrc;
     PixelOrigin px;
@@ -179,67 +211,73 @@ struct WkGather {
 
 // ---- the K loop of one wave and the cross-wave sum ----
 
-template <class AF, class BF>
+template <int TS, class AF, class BF>
 __device__ __forceinline__ void wk_fetch(const AF &af, const BF &bf, int k0, int h, float (&a)[4][4],
                                          float (&b)[4][4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-        af.fetch(k0 + 8 * u, h, a[u]);
-        bf.fetch(k0 + 8 * u, h, b[u]);
+        af.fetch(k0 + WkShape<TS>::kBlock * u, h, a[u]);
+        bf.fetch(k0 + WkShape<TS>::kBlock * u, h, b[u]);
     }
 }
 
-__device__ __forceinline__ void wk_mfma(const float (&a)[4][4], const float (&b)[4][4], f32x16 &acc) {
+template <int TS>
+__device__ __forceinline__ void wk_mfma(const float (&a)[4][4], const float (&b)[4][4],
+                                        typename WkShape<TS>::Acc &acc) {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][q], b[u][q], acc, 0, 0, 0);
+        for (int q = 0; q < 4; ++q) acc = WkShape<TS>::mfma(a[u][q], b[u][q], acc);
 }
 
-// The first `blocks` (wave-uniform) 8-deep blocks of a chunk: the MFMAs of a
-// chunk's all-zero tail blocks are skipped.
+// The first `blocks` (wave-uniform) blocks of a chunk: the MFMAs of a chunk's
+// all-zero tail blocks are skipped.
+template <int TS>
 __device__ __forceinline__ void wk_mfma_part(const float (&a)[4][4], const float (&b)[4][4], int blocks,
-                                             f32x16 &acc) {
+                                             typename WkShape<TS>::Acc &acc) {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
         if (u < blocks)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][q], b[u][q], acc, 0, 0, 0);
+            for (int q = 0; q < 4; ++q) acc = WkShape<TS>::mfma(a[u][q], b[u][q], acc);
 }
 
 // acc = sum over k in [kb, ke) of A[m][k] B[k][n] for this lane's accumulator
-// elements, with NB chunks of 32 k in flight (NB = 2 or 4): while chunk c
+// elements, with NB chunks of 4 blocks in flight (NB = 2 or 4): while chunk c
 // computes, chunks c+1 .. c+NB-1 are loading. A lone wave on its SIMD (small
-// grids) needs the deeper ring: one chunk is 16 MFMAs, about 0.4 us, well
+// grids) needs the deeper ring: one chunk is 16 MFMAs, about 0.2-0.4 us, well
 // under the memory latency under load. Fetchers read zero at and past their
 // k_end (= ke), so chunks past the end need no branch; every fetch has a use
 // on every path, so none can be sunk below the MFMAs it is meant to overlap.
-template <int NB, class AF, class BF>
-__device__ __forceinline__ void wk_accumulate(const AF &af, const BF &bf, int kb, int ke, int h, f32x16 &acc) {
+template <int TS, int NB, class AF, class BF>
+__device__ __forceinline__ void wk_accumulate(const AF &af, const BF &bf, int kb, int ke, int h,
+                                              typename WkShape<TS>::Acc &acc) {
     static_assert(NB == 2 || NB == 4, "ring of 2 or 4 chunks");
+    constexpr int kChunk = wk_chunk<TS>();
+    constexpr int kBlock = WkShape<TS>::kBlock;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    for (int r = 0; r < WkShape<TS>::kAcc; ++r) acc[r] = 0.f;
     if (kb >= ke) return;
-    const int nch = (ke - kb + kWkChunk - 1) / kWkChunk;
+    const int nch = (ke - kb + kChunk - 1) / kChunk;
     float a[NB][4][4], b[NB][4][4];
 #pragma unroll
-    for (int i = 0; i < NB - 1; ++i) wk_fetch(af, bf, kb + i * kWkChunk, h, a[i], b[i]);
+    for (int i = 0; i < NB - 1; ++i) wk_fetch<TS>(af, bf, kb + i * kChunk, h, a[i], b[i]);
     int c = 0;
     for (; c + NB <= nch; c += NB) {
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             // slot (i + NB - 1) % NB receives chunk c + i + NB - 1 while slot i computes chunk c + i
-            wk_fetch(af, bf, kb + (c + i + NB - 1) * kWkChunk, h, a[(i + NB - 1) % NB], b[(i + NB - 1) % NB]);
-            wk_mfma(a[i], b[i], acc);
+            wk_fetch<TS>(af, bf, kb + (c + i + NB - 1) * kChunk, h, a[(i + NB - 1) % NB], b[(i + NB - 1) % NB]);
+            wk_mfma<TS>(a[i], b[i], acc);
         }
     }
     // 0 .. NB-1 chunks left, in slots 0 .. NB-2; the last one may hold fewer than 4 blocks
 #pragma unroll
     for (int i = 0; i < NB - 1; ++i)
-        if (c + i < nch) wk_mfma_part(a[i], b[i], (ke - kb - (c + i) * kWkChunk + 7) / 8, acc);
+        if (c + i < nch) wk_mfma_part<TS>(a[i], b[i], (ke - kb - (c + i) * kChunk + kBlock - 1) / kBlock, acc);
 }
 
-// Per-wave K range: KG slices of kq (a multiple of the 8-deep block).
+// Per-wave K range: KG slices of kq (a multiple of the k block).
 __device__ __forceinline__ void wk_range(int K, int kq, int wave, int &kb, int &ke) {
     kb = min(K, wave * kq);
     ke = min(K, kb + kq);
@@ -247,20 +285,21 @@ __device__ __forceinline__ void wk_range(int K, int kq, int wave, int &kb, int &
 
 // Sum the KG partial tiles in wave order and hand each output (m, n) to
 // `store(m_local, n_local, v)`; consecutive threads take consecutive columns.
-template <int KG, class Store>
-__device__ __forceinline__ void wk_reduce_store(const f32x16 &acc, float (*red)[16][64], const Store &store) {
+template <int TS, int KG, class Store>
+__device__ __forceinline__ void wk_reduce_store(const typename WkShape<TS>::Acc &acc,
+                                                float (*red)[WkShape<TS>::kAcc][64], const Store &store) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) red[wave][r][lane] = acc[r];
+    for (int r = 0; r < WkShape<TS>::kAcc; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
-    for (int e = threadIdx.x; e < kWkTile * kWkTile; e += 64 * KG) {
+    for (int e = threadIdx.x; e < TS * TS; e += 64 * KG) {
         const int r = e >> 6;
         const int l = e & 63;
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < KG; ++w) v += red[w][r][l];
-        store(8 * (r >> 2) + 4 * (l >> 5) + (r & 3), l & 31, v);
+        store(WkShape<TS>::row(r, l), WkShape<TS>::col(l), v);
     }
 }
 
@@ -282,31 +321,32 @@ struct WkConvArgs {
 
 // AF: WkTContig over the packed W^T [K][ldw], or WkKContig<true> over the raw
 // weights W [OC][K] (K in (c, kh, kw) order, 16-byte loads along k).
-template <int KG, int NB, class AF, class BF>
+template <int TS, int KG, int NB, class AF, class BF>
 __global__ __launch_bounds__(64 * KG) void wavek_conv_kernel(WkConvArgs a) {
-    __shared__ float red[KG][16][64];
+    using S = WkShape<TS>;
+    __shared__ float red[KG][S::kAcc][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int h = lane >> 5;
+    const int h = S::group(lane);
     int tm, tn;
     xcd_tile(gridDim.y, gridDim.x, tm, tn);
-    const int m0 = tm * kWkTile, n0 = tn * kWkTile;
+    const int m0 = tm * TS, n0 = tn * TS;
     const int group = blockIdx.z;
     int kb, ke;
     wk_range(a.K, a.kq, wave, kb, ke);
     AF af;
     if constexpr (std::is_same<AF, WkTContig>::value)
         af.init(a.wpk + group * a.wpk_group_stride, (uint32_t)a.K * (uint32_t)a.ldw * 4u, (uint32_t)a.ldw,
-                m0 + (lane & 31), a.M, ke);
+                m0 + S::col(lane), a.M, ke);
     else
         af.init(a.wpk + group * a.wpk_group_stride, (uint32_t)a.M * (uint32_t)a.K * 4u, (uint32_t)a.K,
-                m0 + (lane & 31), a.M, ke);
+                m0 + S::col(lane), a.M, ke);
     BF bf;
-    bf.init(a.geom, n0 + (lane & 31), group, ke);
-    f32x16 acc;
-    wk_accumulate<NB>(af, bf, kb, ke, h, acc);
+    bf.init(a.geom, n0 + S::col(lane), group, ke);
+    typename S::Acc acc;
+    wk_accumulate<TS, NB>(af, bf, kb, ke, h, acc);
     const int ntot = a.geom.ntot;
-    wk_reduce_store<KG>(acc, red, [&](int ml, int nl, float v) {
+    wk_reduce_store<TS, KG>(acc, red, [&](int ml, int nl, float v) {
         const int m = m0 + ml, n = n0 + nl;
         if (m >= a.M || n >= ntot) return;
         const int img = n / a.OHW;
@@ -332,15 +372,16 @@ struct WkGemmArgs {
     float *__restrict__ y;
 };
 
-template <int KG, int NB, class AF, class BF>
+template <int TS, int KG, int NB, class AF, class BF>
 __global__ __launch_bounds__(64 * KG) void wavek_gemm_kernel(WkGemmArgs a) {
-    __shared__ float red[KG][16][64];
+    using S = WkShape<TS>;
+    __shared__ float red[KG][S::kAcc][64];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int h = lane >> 5;
+    const int h = S::group(lane);
     int tm, tn;
     xcd_tile(gridDim.y, gridDim.x, tm, tn);
-    const int m0 = tm * kWkTile, n0 = tn * kWkTile;
+    const int m0 = tm * TS, n0 = tn * TS;
     const int batch = blockIdx.z;
     int kb, ke;
     wk_range(a.K, a.kq, wave, kb, ke);
@@ -350,17 +391,17 @@ __global__ __launch_bounds__(64 * KG) void wavek_gemm_kernel(WkGemmArgs a) {
     const float *abase = a.a + batch * a.stride_a;
     const float *bbase = a.b + batch * a.stride_b;
     if constexpr (std::is_same<AF, WkTContig>::value)
-        af.init(abase, (uint32_t)(a.K * a.lda * 4), (uint32_t)a.lda, m0 + (lane & 31), a.M, ke);
+        af.init(abase, (uint32_t)(a.K * a.lda * 4), (uint32_t)a.lda, m0 + S::col(lane), a.M, ke);
     else
-        af.init(abase, (uint32_t)(a.M * a.lda * 4), (uint32_t)a.lda, m0 + (lane & 31), a.M, ke);
+        af.init(abase, (uint32_t)(a.M * a.lda * 4), (uint32_t)a.lda, m0 + S::col(lane), a.M, ke);
     // B columns are n: k-major [K][ldb] when not transposed, else [N][ldb] with k contiguous
     if constexpr (std::is_same<BF, WkTContig>::value)
-        bf.init(bbase, (uint32_t)(a.K * a.ldb * 4), (uint32_t)a.ldb, n0 + (lane & 31), a.N, ke);
+        bf.init(bbase, (uint32_t)(a.K * a.ldb * 4), (uint32_t)a.ldb, n0 + S::col(lane), a.N, ke);
     else
-        bf.init(bbase, (uint32_t)(a.N * a.ldb * 4), (uint32_t)a.ldb, n0 + (lane & 31), a.N, ke);
-    f32x16 acc;
-    wk_accumulate<NB>(af, bf, kb, ke, h, acc);
-    wk_reduce_store<KG>(acc, red, [&](int ml, int nl, float v) {
+        bf.init(bbase, (uint32_t)(a.N * a.ldb * 4), (uint32_t)a.ldb, n0 + S::col(lane), a.N, ke);
+    typename S::Acc acc;
+    wk_accumulate<TS, NB>(af, bf, kb, ke, h, acc);
+    wk_reduce_store<TS, KG>(acc, red, [&](int ml, int nl, float v) {
         const int m = m0 + ml, n = n0 + nl;
         if (m >= a.M || n >= a.N) return;
         v *= a.alpha;
@@ -371,57 +412,63 @@ __global__ __launch_bounds__(64 * KG) void wavek_gemm_kernel(WkGemmArgs a) {
 }
 
 // Waves per workgroup: doubled while the grid has fewer than 2048 waves and
-// each wave keeps at least one 32-deep chunk, up to 8 (512 threads: more would
-// cap a lane at 128 registers, below what the gather loaders hold).
-int wavek_waves(int64_t tiles, int K) {
+// each wave keeps at least one chunk, up to 8 (512 threads: more would cap a
+// lane at 128 registers, below what the gather loaders hold).
+int wavek_waves(int64_t tiles, int K, int chunk) {
     int kg = 1;
-    while (kg < 8 && tiles * kg < 2048 && K / (2 * kg) >= kWkChunk) kg *= 2;
+    while (kg < 8 && tiles * kg < 2048 && K / (2 * kg) >= chunk) kg *= 2;
     return kg;
 }
 
-int wavek_kq(int K, int kg) { return ((K + kg - 1) / kg + 7) / 8 * 8; }
+int wavek_kq(int K, int kg, int block) { return ((K + kg - 1) / kg + block - 1) / block * block; }
 
-template <int NB, class AF, class BF>
+template <int TS, int NB, class AF, class BF>
 int launch_wk_conv_nb(const WkConvArgs &a, int kg, dim3 grid, hipStream_t st) {
     switch (kg) {
-    case 1: hipLaunchKernelGGL((wavek_conv_kernel<1, NB, AF, BF>), grid, dim3(64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((wavek_conv_kernel<2, NB, AF, BF>), grid, dim3(128), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((wavek_conv_kernel<4, NB, AF, BF>), grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((wavek_conv_kernel<8, NB, AF, BF>), grid, dim3(512), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((wavek_conv_kernel<TS, 1, NB, AF, BF>), grid, dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((wavek_conv_kernel<TS, 2, NB, AF, BF>), grid, dim3(128), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((wavek_conv_kernel<TS, 4, NB, AF, BF>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((wavek_conv_kernel<TS, 8, NB, AF, BF>), grid, dim3(512), 0, st, a); break;
     }
     return check_launch();
 }
 
 // Waves with at most 2 chunks use the 2-deep ring, longer ones the 4-deep one.
-bool wk_deep(int kq) { return kq > 2 * kWkChunk; }
+bool wk_deep(int kq, int chunk) { return kq > 2 * chunk; }
 
 template <class AF, class BF>
-int launch_wk_conv(const WkConvArgs &a, int kg, dim3 grid, hipStream_t st) {
-    return wk_deep(a.kq) ? launch_wk_conv_nb<4, AF, BF>(a, kg, grid, st)
-                         : launch_wk_conv_nb<2, AF, BF>(a, kg, grid, st);
+int launch_wk_conv(const WkConvArgs &a, int ts, int kg, dim3 grid, hipStream_t st) {
+    if (ts == 16)
+        return wk_deep(a.kq, wk_chunk<16>()) ? launch_wk_conv_nb<16, 4, AF, BF>(a, kg, grid, st)
+                                             : launch_wk_conv_nb<16, 2, AF, BF>(a, kg, grid, st);
+    return wk_deep(a.kq, wk_chunk<32>()) ? launch_wk_conv_nb<32, 4, AF, BF>(a, kg, grid, st)
+                                         : launch_wk_conv_nb<32, 2, AF, BF>(a, kg, grid, st);
 }
 
-template <int NB, class AF, class BF>
+template <int TS, int NB, class AF, class BF>
 int launch_wk_gemm_nb(const WkGemmArgs &a, int kg, dim3 grid, hipStream_t st) {
     switch (kg) {
-    case 1: hipLaunchKernelGGL((wavek_gemm_kernel<1, NB, AF, BF>), grid, dim3(64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((wavek_gemm_kernel<2, NB, AF, BF>), grid, dim3(128), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((wavek_gemm_kernel<4, NB, AF, BF>), grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL((wavek_gemm_kernel<8, NB, AF, BF>), grid, dim3(512), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((wavek_gemm_kernel<TS, 1, NB, AF, BF>), grid, dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((wavek_gemm_kernel<TS, 2, NB, AF, BF>), grid, dim3(128), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((wavek_gemm_kernel<TS, 4, NB, AF, BF>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((wavek_gemm_kernel<TS, 8, NB, AF, BF>), grid, dim3(512), 0, st, a); break;
     }
     return check_launch();
 }
 
 template <class AF, class BF>
-int launch_wk_gemm(const WkGemmArgs &a, int kg, dim3 grid, hipStream_t st) {
-    return wk_deep(a.kq) ? launch_wk_gemm_nb<4, AF, BF>(a, kg, grid, st)
-                         : launch_wk_gemm_nb<2, AF, BF>(a, kg, grid, st);
+int launch_wk_gemm(const WkGemmArgs &a, int ts, int kg, dim3 grid, hipStream_t st) {
+    if (ts == 16)
+        return wk_deep(a.kq, wk_chunk<16>()) ? launch_wk_gemm_nb<16, 4, AF, BF>(a, kg, grid, st)
+                                             : launch_wk_gemm_nb<16, 2, AF, BF>(a, kg, grid, st);
+    return wk_deep(a.kq, wk_chunk<32>()) ? launch_wk_gemm_nb<32, 4, AF, BF>(a, kg, grid, st)
+                                         : launch_wk_gemm_nb<32, 2, AF, BF>(a, kg, grid, st);
 }
 
 } // namespace
 
-int wavek_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed, const float *bias,
-               const float *res, float *y, hipStream_t st) {
+int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w, const float *packed,
+               const float *bias, const float *res, float *y, hipStream_t st) {
     WkConvArgs a{};
     const int OCg = d->oc / d->group;
     const int Cg = d->c / d->group;
@@ -454,27 +501,27 @@ int wavek_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const 
     a.act = d->act;
     a.OC = d->oc;
     a.OHW = d->oh * d->ow;
-    const dim3 grid((a.geom.ntot + kWkTile - 1) / kWkTile, (a.M + kWkTile - 1) / kWkTile, d->group);
-    const int kg = wavek_waves((int64_t)grid.x * grid.y * grid.z, a.K);
-    a.kq = wavek_kq(a.K, kg);
+    const dim3 grid((a.geom.ntot + ts - 1) / ts, (a.M + ts - 1) / ts, d->group);
+    const int kg = wavek_waves((int64_t)grid.x * grid.y * grid.z, a.K, ts == 16 ? wk_chunk<16>() : wk_chunk<32>());
+    a.kq = wavek_kq(a.K, kg, ts == 16 ? WkShape<16>::kBlock : WkShape<32>::kBlock);
     if (raw) {
         using RA = WkKContig<true>;
-        if (pointwise) return launch_wk_conv<RA, WkPointwise>(a, kg, grid, st);
-        if (d->kh == 3 && d->kw == 3) return launch_wk_conv<RA, WkGather<3, 3>>(a, kg, grid, st);
-        if (d->kh == 7 && d->kw == 7) return launch_wk_conv<RA, WkGather<7, 7>>(a, kg, grid, st);
-        if (d->kh == 1 && d->kw == 1) return launch_wk_conv<RA, WkGather<1, 1>>(a, kg, grid, st);
-        return launch_wk_conv<RA, WkGather<0, 0>>(a, kg, grid, st);
+        if (pointwise) return launch_wk_conv<RA, WkPointwise>(a, ts, kg, grid, st);
+        if (d->kh == 3 && d->kw == 3) return launch_wk_conv<RA, WkGather<3, 3>>(a, ts, kg, grid, st);
+        if (d->kh == 7 && d->kw == 7) return launch_wk_conv<RA, WkGather<7, 7>>(a, ts, kg, grid, st);
+        if (d->kh == 1 && d->kw == 1) return launch_wk_conv<RA, WkGather<1, 1>>(a, ts, kg, grid, st);
+        return launch_wk_conv<RA, WkGather<0, 0>>(a, ts, kg, grid, st);
     }
     if (!packed) return SPINN_HIP_EINVAL;
-    if (pointwise) return launch_wk_conv<WkTContig, WkPointwise>(a, kg, grid, st);
-    if (Cg % kBK == 0) return launch_wk_conv<WkTContig, WkTap>(a, kg, grid, st); // the pack's tap order
-    if (d->kh == 3 && d->kw == 3) return launch_wk_conv<WkTContig, WkGather<3, 3>>(a, kg, grid, st);
-    if (d->kh == 7 && d->kw == 7) return launch_wk_conv<WkTContig, WkGather<7, 7>>(a, kg, grid, st);
-    if (d->kh == 1 && d->kw == 1) return launch_wk_conv<WkTContig, WkGather<1, 1>>(a, kg, grid, st);
-    return launch_wk_conv<WkTContig, WkGather<0, 0>>(a, kg, grid, st);
+    if (pointwise) return launch_wk_conv<WkTContig, WkPointwise>(a, ts, kg, grid, st);
+    if (Cg % kBK == 0) return launch_wk_conv<WkTContig, WkTap>(a, ts, kg, grid, st); // the pack's tap order
+    if (d->kh == 3 && d->kw == 3) return launch_wk_conv<WkTContig, WkGather<3, 3>>(a, ts, kg, grid, st);
+    if (d->kh == 7 && d->kw == 7) return launch_wk_conv<WkTContig, WkGather<7, 7>>(a, ts, kg, grid, st);
+    if (d->kh == 1 && d->kw == 1) return launch_wk_conv<WkTContig, WkGather<1, 1>>(a, ts, kg, grid, st);
+    return launch_wk_conv<WkTContig, WkGather<0, 0>>(a, ts, kg, grid, st);
 }
 
-int wavek_gemm(const SpinnHipGemmDesc *d, const float *A, const float *B, const float *C, float *Y,
+int wavek_gemm(const SpinnHipGemmDesc *d, int ts, const float *A, const float *B, const float *C, float *Y,
                hipStream_t st) {
     WkGemmArgs a{};
     a.a = A;
@@ -496,9 +543,9 @@ int wavek_gemm(const SpinnHipGemmDesc *d, const float *A, const float *B, const 
     const uint64_t a_bytes = (uint64_t)d->m * d->k * sizeof(float);
     const uint64_t b_bytes = (uint64_t)d->n * d->k * sizeof(float);
     if (a_bytes > kMaxOperandBytes || b_bytes > kMaxOperandBytes) return SPINN_HIP_EUNSUPPORTED;
-    const dim3 grid((d->n + kWkTile - 1) / kWkTile, (d->m + kWkTile - 1) / kWkTile, batch);
-    const int kg = wavek_waves((int64_t)grid.x * grid.y * grid.z, d->k);
-    a.kq = wavek_kq(d->k, kg);
+    const dim3 grid((d->n + ts - 1) / ts, (d->m + ts - 1) / ts, batch);
+    const int kg = wavek_waves((int64_t)grid.x * grid.y * grid.z, d->k, ts == 16 ? wk_chunk<16>() : wk_chunk<32>());
+    a.kq = wavek_kq(d->k, kg, ts == 16 ? WkShape<16>::kBlock : WkShape<32>::kBlock);
     // 16-byte loads along k need 4-aligned rows in every batch entry and a K that is a multiple of 4
     const bool va = ((uintptr_t)A & 15u) == 0 && a.lda % 4 == 0 && d->k % 4 == 0 &&
                     (batch == 1 || d->stride_a % 4 == 0);
@@ -506,18 +553,18 @@ int wavek_gemm(const SpinnHipGemmDesc *d, const float *A, const float *B, const 
                     (batch == 1 || d->stride_b % 4 == 0);
     if (d->trans_a) {
         if (d->trans_b)
-            return vb ? launch_wk_gemm<WkTContig, WkKContig<true>>(a, kg, grid, st)
-                      : launch_wk_gemm<WkTContig, WkKContig<false>>(a, kg, grid, st);
-        return launch_wk_gemm<WkTContig, WkTContig>(a, kg, grid, st);
+            return vb ? launch_wk_gemm<WkTContig, WkKContig<true>>(a, ts, kg, grid, st)
+                      : launch_wk_gemm<WkTContig, WkKContig<false>>(a, ts, kg, grid, st);
+        return launch_wk_gemm<WkTContig, WkTContig>(a, ts, kg, grid, st);
     }
     if (d->trans_b) {
-        if (va && vb) return launch_wk_gemm<WkKContig<true>, WkKContig<true>>(a, kg, grid, st);
-        if (va) return launch_wk_gemm<WkKContig<true>, WkKContig<false>>(a, kg, grid, st);
-        if (vb) return launch_wk_gemm<WkKContig<false>, WkKContig<true>>(a, kg, grid, st);
-        return launch_wk_gemm<WkKContig<false>, WkKContig<false>>(a, kg, grid, st);
+        if (va && vb) return launch_wk_gemm<WkKContig<true>, WkKContig<true>>(a, ts, kg, grid, st);
+        if (va) return launch_wk_gemm<WkKContig<true>, WkKContig<false>>(a, ts, kg, grid, st);
+        if (vb) return launch_wk_gemm<WkKContig<false>, WkKContig<true>>(a, ts, kg, grid, st);
+        return launch_wk_gemm<WkKContig<false>, WkKContig<false>>(a, ts, kg, grid, st);
     }
-    return va ? launch_wk_gemm<WkKContig<true>, WkTContig>(a, kg, grid, st)
-              : launch_wk_gemm<WkKContig<false>, WkTContig>(a, kg, grid, st);
+    return va ? launch_wk_gemm<WkKContig<true>, WkTContig>(a, ts, kg, grid, st)
+              : launch_wk_gemm<WkKContig<false>, WkTContig>(a, ts, kg, grid, st);
 }
 
 } // namespace spinn

@@ -58,6 +58,9 @@ CASES = [
     ("winograd43_c256", 1, 256, 14, 14, 256, 3, 1, 1, 1, 1, 4),
     ("winograd43_c512_add", 2, 512, 7, 7, 512, 3, 1, 1, 1, 4, 4),
     ("winograd43_p0_silu", 1, 8, 10, 12, 40, 3, 1, 0, 1, 3, 4),      # no padding: 8x10 output
+    ("winograd43_batch5_c3_add", 5, 3, 9, 11, 7, 3, 1, 1, 1, 4, 4),   # a 64-tile group spans 7 images
+    ("winograd43_batch3_res", 3, 12, 20, 24, 20, 3, 1, 1, 1, 5, 4),    # residual + ReLU, 30 tiles per image
+    ("winograd43_large_plane", 1, 4, 126, 126, 6, 3, 1, 1, 1, 1, 4),   # 32 x 32 tiles per plane
     # act 2 (CLIP) is a declared code that applies nothing (SPINN/graph_opt.h:33)
     ("clip_conv3x3", 2, 64, 14, 14, 64, 3, 1, 1, 1, 2, 0),
     ("clip_pw1x1_splitk", 1, 1024, 7, 8, 256, 1, 1, 0, 1, 2, 0),

@@ -1,6 +1,7 @@
-"""GPU parity of the wave-K kernels (32 x 32 output tiles, K split over the
-workgroup's waves, operands streamed straight into MFMA registers) forced onto
-conv and Gemm shapes through spinn_hip_tune_force_tiles(32, 32, 0): every
+"""GPU parity of the wave-K kernels (32 x 32 or 16 x 16 output tiles, K split
+over the workgroup's waves, operands streamed straight into MFMA registers)
+forced onto conv and Gemm shapes through spinn_hip_tune_force_tiles(ts, ts, 0)
+for both tile edges: every
 B-operand gather (1x1 pointwise, tap-ordered, (c,kh,kw) with 1x1 / 3x3 / 7x7 /
 runtime windows), the raw-weight (16-byte k loads) and packed-weight A paths,
 groups, ragged M / N / K edges, every fused post-op; Gemm in all transpose
@@ -19,12 +20,12 @@ from tests.hipops import conv_desc, run_conv, run_gemm
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture
-def force_wavek(hip):
+@pytest.fixture(params=[32, 16], ids=["ts32", "ts16"])
+def force_wavek(hip, request):
     L = hip.lib()
-    L.spinn_hip_tune_force_tiles(32, 32, 0)
+    L.spinn_hip_tune_force_tiles(request.param, request.param, 0)
     try:
-        yield
+        yield request.param
     finally:
         L.spinn_hip_tune_force_tiles(0, 0, 0)
 
@@ -50,7 +51,7 @@ CONV = [
 @pytest.mark.parametrize("case", CONV, ids=[c[0] for c in CONV])
 def test_wavek_conv(hip, torch_gpu, force_wavek, case):
     name, n, c, h, w, oc, k, s, p, g, act = case
-    print(f"[wavek conv] {name}", flush=True)
+    print(f"[wavek conv ts{force_wavek}] {name}", flush=True)
     d = conv_desc(hip, n, c, h, w, oc, k, k, s, s, p, p, g, act, hip.ALGO_IMPLICIT_GEMM)
     assert hip.lib().spinn_hip_conv_workspace_size(C.byref(d)) == 0
     rng = np.random.default_rng(zlib.crc32(name.encode()))
