@@ -206,6 +206,21 @@ __global__ void conv_pack_wt_kernel(const float *__restrict__ w, float *__restri
     }
 }
 
+// W [OC][Cg][KH][KW] -> [OC][K] with K in tap-major (kh, kw, c) order.
+__global__ void conv_pack_kcopy_kernel(const float *__restrict__ w, float *__restrict__ out, int OC, int Cg,
+                                       int KHW) {
+    const int K = Cg * KHW;
+    const int64_t total = (int64_t)OC * K;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int k = (int)(e % K);
+        const int64_t oc = e / K;
+        const int tap = k / Cg;
+        const int c = k - tap * Cg;
+        out[e] = w[(oc * Cg + c) * KHW + tap];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Host side: tile selection and launch.
 // ---------------------------------------------------------------------------
@@ -253,20 +268,41 @@ bool conv_pointwise_vec(const SpinnHipConvDesc *d, const float *x) {
 
 } // namespace
 
-int64_t igemm_packed_floats(const SpinnHipConvDesc *d) {
+// Floats of the W^T section [group][K][ldw] of the packed weights.
+static int64_t igemm_wt_floats(const SpinnHipConvDesc *d) {
     const int OCg = d->oc / d->group;
     const int ldw = (OCg + 3) / 4 * 4;
     const int64_t K = (int64_t)(d->c / d->group) * d->kh * d->kw;
     return (int64_t)d->group * K * ldw;
 }
 
+// Tap-ordered windows larger than 1x1 also keep W with K contiguous, [group][OCg][K]
+// in the same tap order, after W^T: the wave-K kernel's A operand then moves four k
+// per 16-byte load, as it does from the raw weights of a 1x1 conv.
+static bool igemm_has_kcopy(const SpinnHipConvDesc *d) { return conv_tap_order(d) && d->kh * d->kw > 1; }
+
+int64_t igemm_packed_floats(const SpinnHipConvDesc *d) {
+    const int64_t K = (int64_t)(d->c / d->group) * d->kh * d->kw;
+    return igemm_wt_floats(d) + (igemm_has_kcopy(d) ? (int64_t)d->oc * K : 0);
+}
+
+const float *igemm_kcopy(const SpinnHipConvDesc *d, const float *packed) {
+    return (packed && igemm_has_kcopy(d)) ? packed + igemm_wt_floats(d) : nullptr;
+}
+
 int igemm_pack(const SpinnHipConvDesc *d, const float *w, float *packed, hipStream_t st) {
     const int OCg = d->oc / d->group;
     const int ldw = (OCg + 3) / 4 * 4;
-    const int64_t total = igemm_packed_floats(d);
+    const int64_t total = igemm_wt_floats(d);
     const int blocks = (int)std::min<int64_t>((total + 255) / 256, 65535);
     hipLaunchKernelGGL(conv_pack_wt_kernel, dim3(blocks), dim3(256), 0, st, w, packed, d->group, OCg,
                        d->c / d->group, d->kh * d->kw, ldw, conv_tap_order(d) ? 1 : 0);
+    int rc = check_launch();
+    if (rc || !igemm_has_kcopy(d)) return rc;
+    const int64_t kc = (int64_t)d->oc * (d->c / d->group) * d->kh * d->kw;
+    const int kblocks = (int)std::min<int64_t>((kc + 255) / 256, 65535);
+    hipLaunchKernelGGL(conv_pack_kcopy_kernel, dim3(kblocks), dim3(256), 0, st, w, packed + total, d->oc,
+                       d->c / d->group, d->kh * d->kw);
     return check_launch();
 }
 
@@ -302,7 +338,7 @@ int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const 
     a.wpk = packed;
     a.wpk_group_stride = (int64_t)a.K * a.ldw;
     const uint64_t x_bytes = (uint64_t)d->n * d->c * d->h * d->w * sizeof(float);
-    const uint64_t w_bytes = (uint64_t)igemm_packed_floats(d) * sizeof(float);
+    const uint64_t w_bytes = (uint64_t)igemm_wt_floats(d) * sizeof(float);
     const uint64_t y_bytes = (uint64_t)d->n * d->oc * d->oh * d->ow * sizeof(float);
     if (x_bytes > kMaxOperandBytes || w_bytes > kMaxOperandBytes || y_bytes > kMaxOperandBytes)
         return SPINN_HIP_EUNSUPPORTED;

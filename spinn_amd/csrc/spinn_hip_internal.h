@@ -84,6 +84,9 @@ int noalloc_scratch(int device, void **ptr);
 
 // implicit GEMM (conv_gemm.hip)
 int64_t igemm_packed_floats(const SpinnHipConvDesc *d);
+// The k-contiguous tap-ordered weights [group][OCg][K] inside `packed`, or null
+// when the layer's packing has none (1x1 windows, (c, kh, kw) order).
+const float *igemm_kcopy(const SpinnHipConvDesc *d, const float *packed);
 int igemm_pack(const SpinnHipConvDesc *d, const float *w, float *packed, hipStream_t st);
 size_t igemm_workspace_bytes(const SpinnHipConvDesc *d);
 int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed, const float *bias,

@@ -306,7 +306,7 @@ __device__ __forceinline__ void wk_reduce_store(const typename WkShape<TS>::Acc 
 // ---- kernels ----
 
 struct WkConvArgs {
-    const float *wpk; // packed W^T [group][K][ldw], or the raw weights [OC][K] when raw_w
+    const float *wpk; // packed W^T [group][K][ldw], or weights [group][OCg][K] with K contiguous
     int64_t wpk_group_stride;
     int ldw;
     int M, K; // per group
@@ -320,7 +320,8 @@ struct WkConvArgs {
 };
 
 // AF: WkTContig over the packed W^T [K][ldw], or WkKContig<true> over the raw
-// weights W [OC][K] (K in (c, kh, kw) order, 16-byte loads along k).
+// weights W [OC][K] (K in (c, kh, kw) order) or the packing's tap-ordered
+// [OCg][K] copy (16-byte loads along k).
 template <int TS, int KG, int NB, class AF, class BF>
 __global__ __launch_bounds__(64 * KG) void wavek_conv_kernel(WkConvArgs a) {
     using S = WkShape<TS>;
@@ -485,11 +486,14 @@ int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w
     // when the packed layout is tap-ordered (16-channel multiples): there the packed
     // W^T and the one-test-per-block tap gather are used.
     const bool raw = w && a.K % 4 == 0 && ((uintptr_t)w & 15u) == 0 && (pointwise || Cg % kBK != 0);
-    a.wpk = raw ? w : packed;
-    a.wpk_group_stride = raw ? (int64_t)OCg * a.K : (int64_t)a.K * a.ldw;
+    // Tap-ordered windows read the packing's k-contiguous copy [OCg][K] the same way.
+    const float *kcopy = raw ? nullptr : igemm_kcopy(d, packed);
+    const bool tap_k = kcopy && ((uintptr_t)kcopy & 15u) == 0;
+    a.wpk = raw ? w : (tap_k ? kcopy : packed);
+    a.wpk_group_stride = (raw || tap_k) ? (int64_t)OCg * a.K : (int64_t)a.K * a.ldw;
     if (!a.wpk) return SPINN_HIP_EINVAL;
     const uint64_t x_bytes = (uint64_t)d->n * d->c * d->h * d->w * sizeof(float);
-    const uint64_t w_bytes = (uint64_t)d->group * a.K * (raw ? OCg : a.ldw) * sizeof(float);
+    const uint64_t w_bytes = (uint64_t)d->group * a.K * ((raw || tap_k) ? OCg : a.ldw) * sizeof(float);
     const uint64_t y_bytes = (uint64_t)d->n * d->oc * d->oh * d->ow * sizeof(float);
     if (x_bytes > kMaxOperandBytes || w_bytes > kMaxOperandBytes || y_bytes > kMaxOperandBytes)
         return SPINN_HIP_EUNSUPPORTED;
@@ -512,6 +516,7 @@ int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w
         if (d->kh == 1 && d->kw == 1) return launch_wk_conv<RA, WkGather<1, 1>>(a, ts, kg, grid, st);
         return launch_wk_conv<RA, WkGather<0, 0>>(a, ts, kg, grid, st);
     }
+    if (tap_k) return launch_wk_conv<WkKContig<true>, WkTap>(a, ts, kg, grid, st);
     if (!packed) return SPINN_HIP_EINVAL;
     if (pointwise) return launch_wk_conv<WkTContig, WkPointwise>(a, ts, kg, grid, st);
     if (Cg % kBK == 0) return launch_wk_conv<WkTContig, WkTap>(a, ts, kg, grid, st); // the pack's tap order
