@@ -726,6 +726,181 @@ def measured_traffic(batch: int, policy: str):
     return d.get("traffic_bytes_per_launch")
 
 
+def _kernel_label(name: str) -> str:
+    """A rocprofv3 kernel name without its argument list and namespaces."""
+    import re
+    n = name.replace("(anonymous namespace)::", "").replace("spinn::", "")
+    n = re.sub(r"\((?:[A-Za-z_:]*Args|[^()]*)\)$", "", n)
+    return n.replace("void ", "").strip()
+
+
+def trace_summary(path: Path, passes: int) -> str:
+    """Markdown tables (kernel family, then instantiation + grid) from a rocprofv3
+    --kernel-trace CSV; `passes` divides totals into per-pass figures."""
+    import collections
+    import csv
+    with open(path) as f:
+        rows = list(csv.DictReader(f))
+    inst = collections.defaultdict(list)
+    for r in rows:
+        grid = tuple(int(r.get(f"Grid_Size_{a}", 1) or 1) for a in "XYZ")
+        wg = tuple(int(r.get(f"Workgroup_Size_{a}", 1) or 1) for a in "XYZ")
+        groups = tuple(g // w for g, w in zip(grid, wg))
+        inst[(_kernel_label(r["Kernel_Name"]), groups, wg[0] * wg[1] * wg[2])].append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    fam = collections.defaultdict(lambda: [0, 0.0])
+    for (name, _, _), v in inst.items():
+        f_ = fam[name.split("<")[0]]
+        f_[0] += len(v)
+        f_[1] += sum(v)
+    total = sum(t for _, t in fam.values())
+    out = [f"| kernel family | calls | total us / pass | avg us | % |", "|---|---|---|---|---|"]
+    for name, (n, t) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"| {name} | {n} | {t / passes:.1f} | {t / n:.2f} | {100 * t / total:.1f} |")
+    out += ["", "| instantiation | workgroups (x,y,z) | threads | calls | avg us | min us | total us / pass |",
+            "|---|---|---|---|---|---|---|"]
+    for (name, groups, thr), v in sorted(inst.items(), key=lambda kv: -sum(kv[1])):
+        out.append(f"| `{name}` | {groups} | {thr} | {len(v)} | {sum(v) / len(v):.2f} | {min(v):.2f} | "
+                   f"{sum(v) / passes:.1f} |")
+    return "\n".join(out)
+
+
+def pmc_summary(d: Path) -> str:
+    """Per-dispatch averages of the rocprofv3 --pmc counter CSVs under `d`
+    (every *_counter_collection.csv), for the spinn kernels, plus derived ratios."""
+    import collections
+    import csv
+    vals = collections.defaultdict(lambda: collections.defaultdict(list))
+    for p in sorted(d.glob("*_counter_collection.csv")):
+        per = collections.defaultdict(dict)
+        with open(p) as f:
+            for r in csv.DictReader(f):
+                if "spinn::" not in r["Kernel_Name"]:
+                    continue
+                key = (_kernel_label(r["Kernel_Name"]), int(r["Grid_Size"]), int(r["Workgroup_Size"]))
+                per[(key, r["Dispatch_Id"])][r["Counter_Name"]] = float(r["Counter_Value"])
+        for (key, _), cs in per.items():
+            for c, v in cs.items():
+                vals[key][c].append(v)
+    out = []
+    for (name, grid, wg), cs in vals.items():
+        if "SQ_WAVES" not in cs or "conv_pack" in name:
+            continue
+        a = {c: sum(v) / len(v) for c, v in cs.items()}
+        waves = a["SQ_WAVES"]
+        out.append(f"### `{name}`, {grid // wg} workgroups of {wg} threads")
+        out.append("")
+        out.append("| counter | per dispatch | per wave |")
+        out.append("|---|---|---|")
+        for c in sorted(a):
+            if c == "GRBM_GUI_ACTIVE":
+                continue
+            out.append(f"| {c} | {a[c]:.0f} | {a[c] / waves:.1f} |")
+        mf = a.get("SQ_INSTS_MFMA")
+        if mf:
+            out.append("")
+            ratios = []
+            if "SQ_INSTS_VALU" in a:
+                ratios.append(f"VALU instructions other than MFMA per MFMA: {(a['SQ_INSTS_VALU'] - mf) / mf:.2f}")
+            if "SQ_INSTS_LDS" in a:
+                ratios.append(f"LDS instructions per MFMA: {a['SQ_INSTS_LDS'] / mf:.2f}")
+            if "SQ_INSTS_VMEM_RD" in a:
+                ratios.append(f"vector-memory reads per MFMA: {a['SQ_INSTS_VMEM_RD'] / mf:.2f}")
+            if "SQ_INSTS_SALU" in a:
+                ratios.append(f"scalar ALU instructions per MFMA: {a['SQ_INSTS_SALU'] / mf:.2f}")
+            if "SQ_WAIT_INST_ANY" in a and "SQ_WAVE_CYCLES" in a:
+                ratios.append(f"SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES: {a['SQ_WAIT_INST_ANY'] / a['SQ_WAVE_CYCLES']:.2f}")
+            if "SQ_WAIT_INST_LDS" in a and "SQ_WAVE_CYCLES" in a:
+                ratios.append(f"SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES: {a['SQ_WAIT_INST_LDS'] / a['SQ_WAVE_CYCLES']:.3f}")
+            out += [f"- {x}" for x in ratios]
+        out.append("")
+    return "\n".join(out)
+
+
+ENGINE_SCAN_SHAPES = [(1024, 14), (256, 14), (256, 56)]  # (output channels, plane edge) at batch 32
+ENGINE_SCAN_K = [64, 128, 256, 512, 1024, 2048]
+
+
+def engine_scan(reps: int = 10) -> None:
+    """Graph-timed 1x1 convs at batch 32 over input depths K (64x64 tiles, no K split):
+    time(K) = fixed + slope*K separates a launch's fixed cost (prologue, epilogue
+    stores, ramp) from the K loop's steady MFMA rate. One JSON line per shape."""
+    import ctypes as C
+    from spinn_amd import native as N
+    from spinn_amd.devbuf import DeviceBuffer, time_graph
+    L = N.lib()
+    N.check(L.spinn_hip_init(0), "spinn_hip_init")
+    for (oc, hw) in ENGINE_SCAN_SHAPES:
+        res = []
+        for c in ENGINE_SCAN_K:
+            n = 32
+            d = N.ConvDesc(n, c, hw, hw, oc, hw, hw, 1, 1, 1, 1, 0, 0, 1, 1, N.ALGO_IMPLICIT_GEMM, 0)
+            bufs = [DeviceBuffer(4 * v) for v in (n * c * hw * hw, oc * c, oc, n * oc * hw * hw)]
+            for b_ in bufs:
+                N.check(L.spinn_hip_fill_u32(b_.ptr, 0x3c23d70a, b_.nbytes, None), "fill")  # 0.01f
+            bx, bw, bb, by = bufs
+            bp = DeviceBuffer(L.spinn_hip_conv_packed_size(C.byref(d)))
+            N.check(L.spinn_hip_conv_pack_weights(C.byref(d), bw.ptr, bp.ptr, None), "pack")
+            L.spinn_hip_tune_force_tiles(64, 64, 0)
+            try:
+                ms = time_graph(lambda st: L.spinn_hip_conv(C.byref(d), bx.ptr, bw.ptr, bp.ptr, bb.ptr, None, by.ptr,
+                                                            None, 0, st), reps)
+            finally:
+                L.spinn_hip_tune_force_tiles(0, 0, 0)
+            fl = 2.0 * n * oc * hw * hw * c
+            res.append({"K": c, "us": round(ms * 1e3, 2), "tflops": round(fl / ms / 1e9, 1)})
+            for b_ in bufs + [bp]:
+                b_.free()
+        ks = [r["K"] for r in res[-3:]]
+        ts = [r["us"] for r in res[-3:]]
+        slope = (ts[-1] - ts[0]) / (ks[-1] - ks[0])
+        fixed = ts[0] - slope * ks[0]
+        steady = 2.0 * 32 * oc * hw * hw / (slope * 1e-6) / 1e12
+        print(json.dumps({"engine_scan": f"1x1 conv, batch 32, {oc} output channels, {hw}x{hw}",
+                          "tiles_64x64": ((oc + 63) // 64) * ((32 * hw * hw + 63) // 64), "points": res,
+                          "fit_over_last_three": {"fixed_us": round(fixed, 2), "us_per_k": round(slope, 4),
+                                                  "steady_tflops": round(steady, 1)}}), flush=True)
+    # tile edge: the two 14x14 ResNet-101 layer shapes and an 8192^3 Gemm, 64x64 vs 128x128 tiles
+    for (c, oc) in ((256, 1024), (1024, 256)):
+        n, hw = 32, 14
+        d = N.ConvDesc(n, c, hw, hw, oc, hw, hw, 1, 1, 1, 1, 0, 0, 1, 1, N.ALGO_IMPLICIT_GEMM, 0)
+        bufs = [DeviceBuffer(4 * v) for v in (n * c * hw * hw, oc * c, oc, n * oc * hw * hw)]
+        for b_ in bufs:
+            N.check(L.spinn_hip_fill_u32(b_.ptr, 0x3c23d70a, b_.nbytes, None), "fill")
+        bx, bw, bb, by = bufs
+        bp = DeviceBuffer(L.spinn_hip_conv_packed_size(C.byref(d)))
+        N.check(L.spinn_hip_conv_pack_weights(C.byref(d), bw.ptr, bp.ptr, None), "pack")
+        out = {}
+        for t in (64, 128):
+            L.spinn_hip_tune_force_tiles(t, t, 0)
+            try:
+                ms = time_graph(lambda st: L.spinn_hip_conv(C.byref(d), bx.ptr, bw.ptr, bp.ptr, bb.ptr, None, by.ptr,
+                                                            None, 0, st), reps)
+            finally:
+                L.spinn_hip_tune_force_tiles(0, 0, 0)
+            out[f"{t}x{t}"] = {"us": round(ms * 1e3, 2), "tflops": round(2.0 * n * oc * hw * hw * c / ms / 1e9, 1)}
+        print(json.dumps({"engine_scan": f"tile edge, 1x1 conv batch 32 {c}->{oc} at 14x14", **out}), flush=True)
+        for b_ in bufs + [bp]:
+            b_.free()
+    m = 8192
+    ba, bb2, by2 = DeviceBuffer(4 * m * m), DeviceBuffer(4 * m * m), DeviceBuffer(4 * m * m)
+    for b_ in (ba, bb2):
+        N.check(L.spinn_hip_fill_u32(b_.ptr, 0x3c23d70a, b_.nbytes, None), "fill")
+    gd = N.GemmDesc(m, m, m, 0, 0, 0, 1.0, 0.0, 1, 0, 0, 0, 0)
+    out = {}
+    for t in (64, 128):
+        L.spinn_hip_tune_force_tiles(t, t, 0)
+        try:
+            ms = time_graph(lambda st: L.spinn_hip_gemm(C.byref(gd), ba.ptr, bb2.ptr, None, by2.ptr, None, 0, st), 2,
+                            replays=2)
+        finally:
+            L.spinn_hip_tune_force_tiles(0, 0, 0)
+        out[f"{t}x{t}"] = {"us": round(ms * 1e3, 1), "tflops": round(2.0 * m ** 3 / ms / 1e9, 1)}
+    print(json.dumps({"engine_scan": "tile edge, Gemm 8192^3", **out}), flush=True)
+    for b_ in (ba, bb2, by2):
+        b_.free()
+
+
 def time_steps(sess, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         sess.run_resident()
@@ -762,6 +937,13 @@ def main() -> int:
                     help="only run the known-size fill/copy kernels that scale the HBM byte counters")
     ap.add_argument("--traffic-summary", metavar="DIR",
                     help="reduce rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE CSVs in DIR to the traffic file (no GPU)")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="print markdown tables of a rocprofv3 kernel-trace CSV (no GPU)")
+    ap.add_argument("--passes", type=int, default=1, help="passes in the traced run, for --trace-summary")
+    ap.add_argument("--pmc-summary", metavar="DIR",
+                    help="print per-dispatch averages of the rocprofv3 --pmc CSVs in DIR (no GPU)")
+    ap.add_argument("--engine-scan", action="store_true",
+                    help="time 1x1 convs at batch 32 over K to split fixed cost from the K loop's rate")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
@@ -775,6 +957,15 @@ def main() -> int:
         return 0
     if a.gemm_compare:
         gemm_compare()
+        return 0
+    if a.trace_summary:
+        print(trace_summary(Path(a.trace_summary), a.passes))
+        return 0
+    if a.pmc_summary:
+        print(pmc_summary(Path(a.pmc_summary)))
+        return 0
+    if a.engine_scan:
+        engine_scan()
         return 0
     if a.traffic_summary:
         cmds = [f"rocprofv3 --pmc {c} --output-format csv -d {a.traffic_summary} -o {o}_{c} -- python -u bench.py {f}"
