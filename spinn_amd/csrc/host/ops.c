@@ -88,6 +88,13 @@ static void note_workspace(size_t need) {
     if (need > g_spinn_exec.prepare_ws_need) g_spinn_exec.prepare_ws_need = need;
 }
 
+/* A float32 operand holding exactly `elems` elements with device memory behind
+ * it. The loader already holds elem_count to the product of the dims and size
+ * to elem_count * 4, so this ties a kernel's extents to the buffer it gets. */
+static int f32_operand(const SpinnTensor *t, uint64_t elems) {
+    return t && t->data && t->dtype == ENNF_TYPE_FLOAT32 && elems > 0 && (uint64_t)t->elem_count == elems;
+}
+
 /* ------------------------------------------------------------------------
  * Conv (SPINN/run_time/ops/conv/conv2d.c:92-232)
  * ---------------------------------------------------------------------- */
@@ -137,6 +144,17 @@ int spinn_conv_desc_from_tensors(SpinnTensor **in, int n_in, const void *params,
     }
     d->act = act;
     if (kc * d->group != d->c || (int)Y->dims[1] != d->oc || (int)Y->dims[0] != d->n) return -1;
+    /* The kernels size every read and write from the descriptor: the window must
+     * be the weight tensor's own (params cannot widen it), output channels must
+     * split evenly over the groups, and each operand must hold what the
+     * descriptor says it does. */
+    if (d->kh != (int)W->dims[2] || d->kw != (int)W->dims[3] || d->group <= 0 || d->oc % d->group) return -1;
+    if (d->n <= 0 || d->c <= 0 || d->h <= 0 || d->w <= 0 || d->oh <= 0 || d->ow <= 0 || d->ph < 0 || d->pw < 0)
+        return -1;
+    const uint64_t y_elems = (uint64_t)d->n * d->oc * d->oh * d->ow;
+    if (!f32_operand(X, (uint64_t)d->n * d->c * d->h * d->w) || !f32_operand(W, (uint64_t)d->oc * kc * d->kh * d->kw) ||
+        !f32_operand(Y, y_elems))
+        return -1;
     d->algo = SPINN_CONV_ALGO_AUTO;
     int algo = spinn_hip_conv_select_algo(d);
     if (algo < 0) return -1;
@@ -152,6 +170,8 @@ int spinn_conv_desc_from_tensors(SpinnTensor **in, int n_in, const void *params,
     *bias = (n_real > 2 && in[2] && in[2]->data) ? (const float *)in[2]->data : NULL;
     *res = has_res ? (const float *)in[n_in - 1]->data : NULL;
     if (has_res && !*res) return -1;
+    if (*bias && (in[2]->dtype != ENNF_TYPE_FLOAT32 || in[2]->elem_count < (uint32_t)d->oc)) return -1;
+    if (has_res && !f32_operand(in[n_in - 1], y_elems)) return -1;
     return 0;
 }
 
@@ -217,10 +237,14 @@ int op_gemm(SpinnTensor **in, int n_in, void *params, uint16_t params_size, Spin
     d.n = (int)(d.trans_b ? B->dims[0] : B->dims[1]);
     const int kb = (int)(d.trans_b ? B->dims[1] : B->dims[0]);
     if (kb != d.k) return -1;
+    if (!f32_operand(A, (uint64_t)d.m * d.k) || !f32_operand(B, (uint64_t)d.k * d.n) ||
+        !f32_operand(Y, (uint64_t)d.m * d.n))
+        return -1;
     d.batch = 1;
     /* C joins as beta*C only when beta != 0: an [N] vector broadcast over rows,
      * else a full [M,N] matrix (gemm.c:31,62-67). */
     if (Cb && d.beta != 0.0f) {
+        if (Cb->dtype != ENNF_TYPE_FLOAT32) return -1;
         if (Cb->elem_count == (uint32_t)d.n) d.c_mode = 1;
         else if (Cb->elem_count == (uint32_t)d.m * (uint32_t)d.n) d.c_mode = 2;
         else return -1;
@@ -260,6 +284,9 @@ int op_matmul(SpinnTensor **in, int n_in, void *params, uint16_t params_size, Sp
     for (int i = 0; i < bn - 2; i++) batch_b *= (int)B->dims[i];
     if (an == 2 && bn == 2) batch = batch_b = 1;
     if (batch != batch_b) return -1;
+    if (!f32_operand(A, (uint64_t)batch * d.m * d.k) || !f32_operand(B, (uint64_t)batch * d.k * d.n) ||
+        !f32_operand(Y, (uint64_t)batch * d.m * d.n))
+        return -1;
     d.batch = batch;
     d.stride_a = (int64_t)d.m * d.k;
     d.stride_b = (int64_t)d.k * d.n;
@@ -300,6 +327,9 @@ int op_maxpool(SpinnTensor **in, int n_in, void *params, uint16_t params_size, S
         d.ph = p->pads[0];
         d.pw = p->pads[1];
     }
+    if (Y->dims[0] != X->dims[0] || Y->dims[1] != X->dims[1] || !f32_operand(X, X->elem_count) ||
+        !f32_operand(Y, Y->elem_count))
+        return -1;
     if (g_spinn_exec.preparing) return 0;
     return spinn_hip_maxpool2d(&d, (const float *)X->data, (float *)Y->data, g_spinn_exec.stream);
 }
@@ -312,6 +342,7 @@ int op_global_avg_pool(SpinnTensor **in, int n_in, void *params, uint16_t params
     if (n_in < 1 || n_out < 1) return -1;
     SpinnTensor *X = in[0];
     if (X->ndim != 4) return -1;
+    if (!f32_operand(X, X->elem_count) || !f32_operand(out[0], (uint64_t)X->dims[0] * X->dims[1])) return -1;
     if (g_spinn_exec.preparing) return 0;
     return spinn_hip_reduce_mean((int64_t)X->dims[0] * X->dims[1], (int64_t)X->dims[2] * X->dims[3], 1,
                                  (const float *)X->data, (float *)out[0]->data, g_spinn_exec.stream);

@@ -52,6 +52,14 @@ SpinnContext *spinn_load(const char *path) {
     ctx->num_weights = ctx->header.num_weights;
     ctx->weight_base_offset = ctx->header.weight_data_offset;
     if (ctx->num_tensors == 0 || ctx->num_tensors > 65536) goto fail;
+    /* Table sizes the file cannot hold are rejected before anything is sized
+     * from them: a node takes at least its 8-byte base record, a tensor its
+     * 44-byte meta record. */
+    if (fseek(fp, 0, SEEK_END)) goto fail;
+    const long file_bytes = ftell(fp);
+    if (file_bytes < 0 || (uint64_t)ctx->num_nodes * sizeof(ENNF_NodeBase) > (uint64_t)file_bytes ||
+        (uint64_t)ctx->num_tensors * sizeof(ENNF_TensorMeta) > (uint64_t)file_bytes)
+        goto fail;
 
     /* graph meta: u16 n_in, u16 ids[n_in], u16 n_out, u16 ids[n_out] */
     if (fseek(fp, ctx->header.graph_meta_offset, SEEK_SET)) goto fail;
@@ -167,6 +175,13 @@ static int dispatch_node(SpinnContext *ctx, uint32_t i) {
     SpinnTensor *ins[SPINN_MAX_IO], *outs[SPINN_MAX_IO];
     for (int j = 0; j < node->num_inputs; j++) ins[j] = &ctx->tensors[node->input_ids[j]];
     for (int j = 0; j < node->num_outputs; j++) outs[j] = &ctx->tensors[node->output_ids[j]];
+    /* A non-empty operand without device memory (a weight whose file entry has
+     * no payload, a tensor the planner never placed) would reach a kernel as a
+     * null pointer: the node fails instead. */
+    for (int j = 0; j < node->num_inputs; j++)
+        if (ins[j]->size > 0 && !ins[j]->data) return -1;
+    for (int j = 0; j < node->num_outputs; j++)
+        if (outs[j]->size > 0 && !outs[j]->data) return -1;
     return spinn_dispatch_op(node->op_type, ins, node->num_inputs, node->params, node->params_size, outs,
                              node->num_outputs);
 }
@@ -205,9 +220,13 @@ int spinn_plan(SpinnContext *ctx, uint32_t max_arena_bytes) {
         /* the reference callocs its arena: start from zeros too */
         if (spinn_hip_fill_u32(base, 0u, (size_t)peak, ctx->stream) != 0) return -2; /* peak is a multiple of 16 */
     }
+    /* A tensor the planner never placed (neither a model input nor any node's
+     * output, in a malformed file) keeps offset 0: it gets device memory only
+     * if it fits inside the arena, else none, and a node using it fails. */
     for (uint32_t i = 0; i < ctx->num_tensors; i++) {
         SpinnTensor *t = &ctx->tensors[i];
-        if (!t->is_weight && t->size > 0) t->data = ctx->arena.base + t->offset;
+        if (!t->is_weight && t->size > 0 && (uint64_t)t->offset + t->size <= (uint64_t)peak)
+            t->data = ctx->arena.base + t->offset;
     }
 
     /* weights: one device pool, 256-byte aligned entries */
