@@ -279,6 +279,16 @@ const char *spinn_hip_error_string(int code);
  * depend on it, workspace sizes do. No counterpart in the reference. */
 void spinn_hip_tune_force_tiles(int bm, int bn, int split);
 
+/* Tuning hook: the data-parallel + stream-K split of the implicit-GEMM conv
+ * (whole tiles one workgroup each, the tiles left over after an even share
+ * per CU cut along K and finished in the same launch): -1 = per-shape choice
+ * (default, or SPINN_STREAMK=0|1 from the environment), 0 = never, 1 = for
+ * every grid of at least one tile per CU whose tile count is not a multiple
+ * of the CU count, 2 = as 1 with the parts' sums exchanged through memory
+ * even where spinn_hip_init found them sharing an L2. Change it only between
+ * plans: workspace sizes depend on it. No counterpart in the reference. */
+void spinn_hip_tune_streamk(int mode);
+
 /* Library version / build identification string. */
 const char *spinn_hip_version(void);
 

@@ -340,7 +340,10 @@ int spinn_hip_init(int device) {
     // resolve the device address of spinn_hip_conv_noalloc's scratch array here,
     // at set-up, rather than inside a caller's capture or serving loop
     void *scratch = nullptr;
-    return noalloc_scratch(device, &scratch);
+    rc = noalloc_scratch(device, &scratch);
+    if (rc) return rc;
+    probe_xcd_local(device);
+    return SPINN_HIP_OK;
 }
 
 int spinn_hip_device_count(int *count) {
@@ -452,6 +455,8 @@ const char *spinn_hip_error_string(int code) {
 }
 
 void spinn_hip_tune_force_tiles(int bm, int bn, int split) { force_tiles(bm, bn, split); }
+
+void spinn_hip_tune_streamk(int mode) { force_streamk(mode); }
 
 const char *spinn_hip_version(void) { return "spinn_amd 0.1 gfx950 fp32-mfma"; }
 

@@ -16,6 +16,7 @@
 // sums them in a fixed order and applies the epilogue (deterministic).
 #include "mfma_core.h"
 #include "spinn_hip_internal.h"
+#include "streamk.h"
 #include <type_traits>
 
 namespace spinn {
@@ -35,6 +36,81 @@ struct ConvKArgs {
     float *__restrict__ ws; // split-K partials [split][OC][ntot]
     int k_chunk;       // K per split (multiple of kBK)
 };
+
+// Accumulator start values of a conv output tile: bias + residual when
+// `terms` (their loads then overlap the K loop's prologue instead of arriving
+// as one burst of reads after it, and the epilogue only applies the activation
+// and stores; the sum is the reference's acc + bias + residual in another
+// order, within fp32 rounding), else zero.
+template <class WT>
+__device__ __forceinline__ void conv_acc_start(const ConvKArgs &a, int group, int m0, int n0, int wm0, int wn0,
+                                               int lane, bool terms, f32x16 (&c)[WT::TM][WT::TN]) {
+    if (!terms) {
+        ZeroAcc{}(c);
+        return;
+    }
+    // Unconditional buffer loads: a missing bias or residual is a zero-sized
+    // resource and rows or columns past the edge read at kOOB, all of which
+    // return 0.
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(a.bias ? a.bias + group * a.M : a.y, a.bias ? (uint32_t)a.M * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res ? a.res : a.y, a.res ? a.res_bytes : 0u);
+#pragma unroll
+    for (int j = 0; j < WT::TN; ++j) {
+        const int jcol = n0 + wn0 + j * 32 + l32;
+        const bool col_ok = jcol < a.geom.ntot;
+        const int img = jcol / a.OHW;
+        const int p = jcol - img * a.OHW;
+        const uint32_t ybase = ((uint32_t)img * a.OC + (uint32_t)(group * a.M)) * a.OHW + p;
+#pragma unroll
+        for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const bool ok = m < a.M;
+                const float bv = buf_f32(rb, ok ? (uint32_t)m * 4u : kOOB);
+                const float rv = buf_f32(rr, ok && col_ok ? (ybase + (uint32_t)m * a.OHW) * 4u : kOOB);
+                c[i][j][r] = bv + rv;
+            }
+    }
+}
+
+// Post-op and store of a finished conv output tile (accumulators already hold
+// bias + residual). Lane owns columns n0 + wn0 + j*32 + lane%32 and rows
+// m0 + wm0 + i*32 + 8*(r/4) + 4*(lane/32) + r%4.
+template <class WT, int AC>
+__device__ __forceinline__ void conv_store(const ConvKArgs &a, int group, int m0, int n0, int wm0, int wn0, int lane,
+                                           const f32x16 (&acc)[WT::TM][WT::TN]) {
+    const int h = lane >> 5;
+    const int l32 = lane & 31;
+    // A tile whose rows all exist (the usual case: OC a multiple of the tile)
+    // stores without a per-element row test.
+    const bool full_m = m0 + WT::WM * WT::WAVES_M <= a.M;
+#pragma unroll
+    for (int j = 0; j < WT::TN; ++j) {
+        const int jcol = n0 + wn0 + j * 32 + l32;
+        if (jcol >= a.geom.ntot) continue;
+        const int img = jcol / a.OHW;
+        const int p = jcol - img * a.OHW;
+        float *yp = a.y + ((int64_t)img * a.OC + (int64_t)group * a.M + m0 + wm0 + 4 * h) * a.OHW + p;
+        if (full_m) {
+#pragma unroll
+            for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    yp[(int64_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * a.OHW] = apply_act_c<AC>(acc[i][j][r]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < WT::TM; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int mo = i * 32 + 8 * (r >> 2) + (r & 3);
+                    if (m0 + wm0 + 4 * h + mo < a.M) yp[(int64_t)mo * a.OHW] = apply_act_c<AC>(acc[i][j][r]);
+                }
+        }
+    }
+}
 
 // AC: the post-op class (act_class), fixed at compile time so the epilogue has no
 // per-element branch on it.
@@ -65,46 +141,11 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
     BLoader bl;
     bl.init(a.geom, n0, group, tid, k_end);
 
-    // Lane owns columns jcol = n0 + wn0 + j*32 + lane%32 and rows
-    // m0 + wm0 + i*32 + 8*(r/4) + 4*(lane/32) + r%4 of the tile.
     const int h = lane >> 5;
     const int l32 = lane & 31;
     const int ntot = a.geom.ntot;
-
-    // Without split K the accumulators start from the epilogue's additive
-    // terms, bias + residual: their loads then overlap the K loop's prologue
-    // instead of arriving as one burst of reads after it, and the epilogue
-    // only applies the activation and stores. (The sum is the reference's
-    // acc + bias + residual in another order, within fp32 rounding.)
     auto init = [&](f32x16 (&c)[WT::TM][WT::TN]) {
-        if constexpr (SPLIT) {
-            ZeroAcc{}(c);
-        } else {
-            // Unconditional buffer loads: a missing bias or residual is a
-            // zero-sized resource and rows or columns past the edge read at
-            // kOOB, all of which return 0.
-            const __amdgpu_buffer_rsrc_t rb =
-                make_rsrc(a.bias ? a.bias + group * a.M : a.y, a.bias ? (uint32_t)a.M * 4u : 0u);
-            const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res ? a.res : a.y, a.res ? a.res_bytes : 0u);
-#pragma unroll
-            for (int j = 0; j < WT::TN; ++j) {
-                const int jcol = n0 + wn0 + j * 32 + l32;
-                const bool col_ok = jcol < ntot;
-                const int img = jcol / a.OHW;
-                const int p = jcol - img * a.OHW;
-                const uint32_t ybase = ((uint32_t)img * a.OC + (uint32_t)(group * a.M)) * a.OHW + p;
-#pragma unroll
-                for (int i = 0; i < WT::TM; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int m = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                        const bool ok = m < a.M;
-                        const float bv = buf_f32(rb, ok ? (uint32_t)m * 4u : kOOB);
-                        const float rv = buf_f32(rr, ok && col_ok ? (ybase + (uint32_t)m * a.OHW) * 4u : kOOB);
-                        c[i][j][r] = bv + rv;
-                    }
-            }
-        }
+        conv_acc_start<WT>(a, group, m0, n0, wm0, wn0, lane, !SPLIT, c);
     };
 
     f32x16 acc[WT::TM][WT::TN];
@@ -126,33 +167,122 @@ __global__ __launch_bounds__(kThreads, 2) void conv_igemm_kernel(ConvKArgs a) {
                 }
         }
     } else {
-        // A tile whose rows all exist (the usual case: OC a multiple of the tile)
-        // stores without a per-element row test.
-        const bool full_m = m0 + BM <= a.M;
-#pragma unroll
-        for (int j = 0; j < WT::TN; ++j) {
-            const int jcol = n0 + wn0 + j * 32 + l32;
-            if (jcol >= ntot) continue;
-            const int img = jcol / a.OHW;
-            const int p = jcol - img * a.OHW;
-            float *yp = a.y + ((int64_t)img * a.OC + (int64_t)group * a.M + m0 + wm0 + 4 * h) * a.OHW + p;
-            if (full_m) {
-#pragma unroll
-                for (int i = 0; i < WT::TM; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        yp[(int64_t)(i * 32 + 8 * (r >> 2) + (r & 3)) * a.OHW] = apply_act_c<AC>(acc[i][j][r]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < WT::TM; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int mo = i * 32 + 8 * (r >> 2) + (r & 3);
-                        if (m0 + wm0 + 4 * h + mo < a.M) yp[(int64_t)mo * a.OHW] = apply_act_c<AC>(acc[i][j][r]);
-                    }
-            }
-        }
+        conv_store<WT, AC>(a, group, m0, n0, wm0, wn0, lane, acc);
     }
+}
+
+// K slices [k0, k1) of output tile t of a group-1 conv into acc, through the
+// shared K loop; the accumulators start from bias + residual when k0 == 0.
+template <int BM, int BN, int BK, class BLoader>
+__device__ __forceinline__ void conv_segment(const ConvKArgs &a, int tiles_m, int t, int k0, int k1,
+                                             float (*As)[BK * LdsPad<BM>::stride],
+                                             float (*Bs)[BK * LdsPad<BN>::stride],
+                                             f32x16 (&acc)[WaveTiling<BM, BN>::TM][WaveTiling<BM, BN>::TN], int tid,
+                                             int lane, int wm0, int wn0, int &m0, int &n0) {
+    using WT = WaveTiling<BM, BN>;
+    m0 = (t % tiles_m) * BM;
+    n0 = (t / tiles_m) * BN;
+    const int mm0 = m0, nn0 = n0;
+    KMajorLoader<BM, BK, true> al;
+    al.init(a.wpk, (uint32_t)a.K * (uint32_t)a.ldw * 4u, (uint32_t)a.ldw, m0, a.ldw);
+    BLoader bl;
+    bl.init(a.geom, n0, 0, tid, min(a.K, k1 * BK));
+    auto init = [&](f32x16 (&c)[WT::TM][WT::TN]) { conv_acc_start<WT>(a, 0, mm0, nn0, wm0, wn0, lane, k0 == 0, c); };
+    gemm_mainloop<BM, BN, BK, kStages>(al, bl, As, Bs, acc, k0 * BK, k1 - k0, tid, lane, wm0, wn0, init);
+}
+
+// Data-parallel + stream-K launch of a group-1 conv (streamk.h). SPLIT_WGS:
+// block ids below 8 * s.W run a range of at most S slices of the remaining
+// tiles (the end of one tile and the start of the next), the rest one whole
+// tile each. PARTS_IN_DP: every block runs one whole tile, the first R * p of
+// them a part of a remaining tile before it. Segments are unrolled: a loop
+// would keep the second segment's set-up live across the first segment's K
+// loop and cost a wave per SIMD.
+template <int BM, int BN, int BK, class BLoader, int AC, int SCHEME>
+__global__ __launch_bounds__(kThreads, 2) void conv_igemm_sk_kernel(ConvKArgs a, SkSched s) {
+    using WT = WaveTiling<BM, BN>;
+    constexpr int SA = LdsPad<BM>::stride;
+    constexpr int SB = LdsPad<BN>::stride;
+    constexpr int NA = WT::TM * WT::TN * 16; // accumulators per thread
+    constexpr int TILE = BM * BN;            // floats of one partial tile
+    __shared__ __attribute__((aligned(16))) float As[2][BK * SA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK * SB];
+    __shared__ int sk_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = WT::origin_m(wave);
+    const int wn0 = WT::origin_n(wave);
+    const int id = blockIdx.x;
+    const int nsk = SCHEME == kSkSplitWgs ? kXcds * s.W : 0;
+    const int x = (id < nsk ? id : id - nsk) % kXcds;
+    int xstart, count;
+    sk_xcd_tiles(s, x, xstart, count);
+    const int tile_sk0 = kXcds * s.dp_per_xcd + xstart; // this XCD's first remaining tile
+    int m0, n0;
+
+    if (SCHEME == kSkSplitWgs && id < nsk) {
+        // SPLIT_WGS: one range of the XCD's remaining slices
+        const int I = count * s.S;
+        const int Wx = min(s.W, I);
+        const int w = id / kXcds;
+        if (w >= Wx) return; // no slices for this workgroup (uniform exit)
+        const int b = sk_begin(w, I, Wx);
+        const int e = sk_begin(w + 1, I, Wx);
+#pragma unroll
+        for (int seg = 0; seg < 2; ++seg) {
+            const int i = seg == 0 ? b : (b / s.S + 1) * s.S;
+            if (i >= e) break;
+            const int r = i / s.S;
+            const int k0 = i - r * s.S;
+            const int k1 = min(s.S, k0 + (e - i));
+            f32x16 acc[WT::TM][WT::TN];
+            conv_segment<BM, BN, BK, BLoader>(a, s.tiles_m, tile_sk0 + r, k0, k1, As, Bs, acc, tid, lane, wm0, wn0,
+                                              m0, n0);
+            if (k0 == 0 && k1 == s.S) {
+                conv_store<WT, AC>(a, 0, m0, n0, wm0, wn0, lane, acc);
+            } else {
+                const int w_first = sk_owner(r * s.S, I, Wx);
+                const int nparts = sk_owner((r + 1) * s.S - 1, I, Wx) - w_first + 1;
+                f32x16 sum[WT::TM][WT::TN];
+                auto slot_of = [&](int q) {
+                    const int wq = w_first + q;
+                    return (x * s.W + wq) * 2 + ((sk_begin(wq, I, Wx) / s.S == r) ? 0 : 1);
+                };
+                if (sk_finish_part<NA, TILE>(s, kXcds * s.W * 2, (x * s.W + w) * 2 + seg, xstart + r, nparts,
+                                             reinterpret_cast<const float *>(&acc), reinterpret_cast<float *>(&sum),
+                                             tid, sk_last, slot_of))
+                    conv_store<WT, AC>(a, 0, m0, n0, wm0, wn0, lane, sum);
+            }
+            __syncthreads(); // the next segment's prologue rewrites the LDS buffers
+        }
+        return;
+    }
+
+    const int l = (id - nsk) / kXcds; // XCD-local index of this whole-tile workgroup
+    if (SCHEME == kSkPartsInDp && l < count * s.p) {
+        // PARTS_IN_DP: part j of remaining tile r first
+        const int r = l / s.p;
+        const int j = l - r * s.p;
+        const int k0 = j * s.S / s.p;
+        const int k1 = (j + 1) * s.S / s.p;
+        f32x16 acc[WT::TM][WT::TN];
+        conv_segment<BM, BN, BK, BLoader>(a, s.tiles_m, tile_sk0 + r, k0, k1, As, Bs, acc, tid, lane, wm0, wn0, m0,
+                                          n0);
+        f32x16 sum[WT::TM][WT::TN];
+        const int base = (x * s.rx + r) * s.p;
+        auto slot_of = [&](int q) { return base + q; };
+        if (sk_finish_part<NA, TILE>(s, kXcds * s.rx * s.p, base + j, xstart + r, s.p,
+                                     reinterpret_cast<const float *>(&acc), reinterpret_cast<float *>(&sum), tid,
+                                     sk_last, slot_of))
+            conv_store<WT, AC>(a, 0, m0, n0, wm0, wn0, lane, sum);
+        __syncthreads(); // the whole tile's prologue rewrites the LDS buffers
+    }
+    f32x16 acc[WT::TM][WT::TN];
+    conv_segment<BM, BN, BK, BLoader>(a, s.tiles_m, x * s.dp_per_xcd + l, 0, s.S, As, Bs, acc, tid, lane, wm0, wn0,
+                                      m0, n0);
+    conv_store<WT, AC>(a, 0, m0, n0, wm0, wn0, lane, acc);
 }
 
 // Sum split-K partials in split order and apply the conv epilogue.
@@ -240,6 +370,52 @@ int launch_conv_tile(const ConvKArgs &a, int groups, int split, hipStream_t st) 
     return check_launch();
 }
 
+template <int BM, int BN, class BL>
+int launch_conv_sk_tile(const ConvKArgs &a, const SkPlan &sp, int S, void *ws, hipStream_t st) {
+    SkSched s{};
+    s.tiles_m = (a.M + BM - 1) / BM;
+    s.S = S;
+    s.dp_per_xcd = sp.dp_per_xcd;
+    s.R = sp.R;
+    s.scheme = sp.scheme;
+    s.W = sp.W;
+    s.p = sp.p;
+    s.rx = (sp.R + kXcds - 1) / kXcds;
+    s.local = xcd_local_parts() ? 1 : 0;
+    s.epoch = streamk_epoch();
+    s.cnt = (unsigned long long *)ws;
+    s.part = (float *)((char *)ws + sp.cnt_bytes);
+    const dim3 grid(sp.grid);
+    if (sp.scheme == kSkSplitWgs) {
+        if (act_class(a.act) == 1)
+            hipLaunchKernelGGL((conv_igemm_sk_kernel<BM, BN, kBK, BL, 1, kSkSplitWgs>), grid, dim3(kThreads), 0, st,
+                               a, s);
+        else if (act_class(a.act) == 3)
+            hipLaunchKernelGGL((conv_igemm_sk_kernel<BM, BN, kBK, BL, 3, kSkSplitWgs>), grid, dim3(kThreads), 0, st,
+                               a, s);
+        else
+            hipLaunchKernelGGL((conv_igemm_sk_kernel<BM, BN, kBK, BL, 0, kSkSplitWgs>), grid, dim3(kThreads), 0, st,
+                               a, s);
+    } else {
+        if (act_class(a.act) == 1)
+            hipLaunchKernelGGL((conv_igemm_sk_kernel<BM, BN, kBK, BL, 1, kSkPartsInDp>), grid, dim3(kThreads), 0, st,
+                               a, s);
+        else if (act_class(a.act) == 3)
+            hipLaunchKernelGGL((conv_igemm_sk_kernel<BM, BN, kBK, BL, 3, kSkPartsInDp>), grid, dim3(kThreads), 0, st,
+                               a, s);
+        else
+            hipLaunchKernelGGL((conv_igemm_sk_kernel<BM, BN, kBK, BL, 0, kSkPartsInDp>), grid, dim3(kThreads), 0, st,
+                               a, s);
+    }
+    return check_launch();
+}
+
+template <template <int> class BLT>
+int launch_conv_sk(const ConvKArgs &a, const TileChoice &tc, const SkPlan &sp, int S, void *ws, hipStream_t st) {
+    if (tc.bm == 32 && tc.bn == 128) return launch_conv_sk_tile<32, 128, BLT<128>>(a, sp, S, ws, st);
+    return launch_conv_sk_tile<64, 64, BLT<64>>(a, sp, S, ws, st);
+}
+
 template <template <int> class BLT>
 int launch_conv_bl(const ConvKArgs &a, const TileChoice &tc, int groups, hipStream_t st) {
     if (tc.bm == 128 && tc.bn == 128) return launch_conv_tile<128, 128, BLT<128>>(a, groups, tc.split, st);
@@ -313,6 +489,20 @@ static TileChoice igemm_tiles(const SpinnHipConvDesc *d) {
     return choose_tiles(OCg, ntot, K, d->group, d->group == 1);
 }
 
+// Data-parallel + stream-K split for a group-1 conv on 64 x 64 or 32 x 128
+// tiles whose tile count leaves the CUs unevenly loaded.
+static bool igemm_streamk(const SpinnHipConvDesc *d, const TileChoice &tc, SkPlan &sp) {
+    // A grid the tile rule already splits along K (long K, few tiles) keeps its
+    // split: several workgroups per CU hide the gather latency better than one
+    // or two whole tiles and an extra range.
+    if (d->group != 1 || tc.split > 1 || !((tc.bm == 64 && tc.bn == 64) || (tc.bm == 32 && tc.bn == 128)))
+        return false;
+    const int K = d->c * d->kh * d->kw;
+    const int ntot = d->n * d->oh * d->ow;
+    return plan_streamk((d->oc + tc.bm - 1) / tc.bm, (ntot + tc.bn - 1) / tc.bn, (K + kBK - 1) / kBK,
+                        tc.bm * tc.bn, sp);
+}
+
 static int igemm_wavek(const SpinnHipConvDesc *d) {
     const bool pointwise = d->kh == 1 && d->kw == 1 && d->sh == 1 && d->sw == 1 && d->ph == 0 && d->pw == 0 &&
                            d->oh == d->h && d->ow == d->w;
@@ -323,6 +513,13 @@ static int igemm_wavek(const SpinnHipConvDesc *d) {
 size_t igemm_workspace_bytes(const SpinnHipConvDesc *d) {
     if (igemm_wavek(d)) return 0;
     TileChoice tc = igemm_tiles(d);
+    SkPlan sp;
+    if (igemm_streamk(d, tc, sp)) {
+        // plan time: settle how the parts exchange sums on this device
+        int dev = 0;
+        if (hipGetDevice(&dev) == hipSuccess) probe_xcd_local(dev);
+        return sp.ws_bytes;
+    }
     if (tc.split <= 1) return 0;
     return (size_t)tc.split * d->oc * ((size_t)d->n * d->oh * d->ow) * sizeof(float);
 }
@@ -352,6 +549,17 @@ int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const 
     a.OC = d->oc;
     a.OHW = d->oh * d->ow;
     TileChoice tc = igemm_tiles(d);
+    SkPlan sp;
+    if (igemm_streamk(d, tc, sp)) {
+        if (!ws || ws_bytes < sp.ws_bytes || ((uintptr_t)ws & 15u)) return SPINN_HIP_EWORKSPACE;
+        const int S = (a.K + kBK - 1) / kBK;
+        if (conv_pointwise_vec(d, x)) return launch_conv_sk<PwBL>(a, tc, sp, S, ws, st);
+        if (conv_tap_order(d)) return launch_conv_sk<TapBL>(a, tc, sp, S, ws, st);
+        if (d->kh == 3 && d->kw == 3) return launch_conv_sk<Gen33BL>(a, tc, sp, S, ws, st);
+        if (d->kh == 7 && d->kw == 7) return launch_conv_sk<Gen77BL>(a, tc, sp, S, ws, st);
+        if (d->kh == 1 && d->kw == 1) return launch_conv_sk<Gen11BL>(a, tc, sp, S, ws, st);
+        return launch_conv_sk<GenBL>(a, tc, sp, S, ws, st);
+    }
     if (tc.split > 1) {
         const size_t need = (size_t)tc.split * d->oc * (size_t)a.geom.ntot * sizeof(float);
         if (!ws || ws_bytes < need) return SPINN_HIP_EWORKSPACE;

@@ -64,6 +64,24 @@ struct TileChoice {
 };
 TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split);
 void force_tiles(int bm, int bn, int split);
+// Data-parallel + stream-K split of one launch (streamk.h): dp_per_xcd whole
+// tiles per XCD, the R remaining tiles cut along K, either over W extra
+// workgroups per XCD (scheme kSkSplitWgs) or in p parts done by whole-tile
+// workgroups (kSkPartsInDp). Workspace: cnt_bytes of arrival counters, then
+// the partial-tile slots.
+struct SkPlan {
+    int dp_per_xcd, R, scheme, W, p, grid;
+    size_t cnt_bytes, ws_bytes;
+};
+// False when whole tiles are balanced enough (or the split is switched off).
+bool plan_streamk(int tiles_m, int tiles_n, int S, int tile_elems, SkPlan &p);
+void force_streamk(int mode);
+uint64_t streamk_epoch();
+// Check once per device that workgroup b runs on XCD b % 8 (so the parts of a
+// cut tile can exchange sums through one L2); xcd_local_parts() reports the
+// result for the current device, false until checked.
+void probe_xcd_local(int device);
+bool xcd_local_parts();
 // Output tile edge of the wave-K kernel (K split over a workgroup's waves) for
 // an (M x N x K) problem repeated `reps` times: 32 or 16, or 0 when it runs on the
 // 64/128-wide tiles of choose_tiles. `pointwise`: a 1x1 stride-1 unpadded conv.

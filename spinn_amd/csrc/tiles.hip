@@ -1,6 +1,10 @@
 // tiles.hip - output-tile and split-K choice shared by the MFMA GEMM launches.
 #include "spinn_hip_internal.h"
+#include "streamk.h"
+#include <atomic>
+#include <chrono>
 #include <cstdlib>
+#include <mutex>
 
 namespace spinn {
 
@@ -106,6 +110,135 @@ TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
         }
     }
     return tc;
+}
+
+static int g_force_streamk = -1;
+static bool g_force_sys_exchange = false;
+
+void force_streamk(int mode) {
+    g_force_streamk = mode < 0 ? -1 : (mode ? 1 : 0);
+    g_force_sys_exchange = mode == 2;
+}
+
+static int env_streamk() {
+    // SPINN_STREAMK=0 never splits the remainder tiles along K, 1 does it for
+    // every grid whose tile count is not a multiple of the CU count; unset =
+    // per-shape choice.
+    static int v = [] {
+        const char *e = std::getenv("SPINN_STREAMK");
+        if (!e || !*e) return -1;
+        return e[0] == '0' ? 0 : 1;
+    }();
+    return v;
+}
+
+bool plan_streamk(int tiles_m, int tiles_n, int S, int tile_elems, SkPlan &p) {
+    const int cus = device_cu_count();
+    if (cus % kXcds || tiles_m <= 0 || tiles_n <= 0 || S <= 0) return false;
+    const int64_t T = (int64_t)tiles_m * tiles_n;
+    const int64_t full = T / cus;
+    const int R = (int)(T % cus);
+    // Fewer tiles than CUs keep split-K or the wave-K kernel: every tile would
+    // be cut, and the last part's serial read-back of the others costs more
+    // than the reduction launch it saves (measured at batch 1).
+    if (R == 0 || full == 0 || T > (int64_t)INT32_MAX / 2) return false;
+    const int mode = g_force_streamk >= 0 ? g_force_streamk : env_streamk();
+    if (mode == 0 || g_force_split > 1) return false; // a forced K split keeps its grid
+    // Whole tiles alone leave full + 1 tiles on the busiest CU against T/C on
+    // average: split the remainder when that costs >= 10 % (below that the
+    // parts' write-back and read-back cost as much as they save; measured on
+    // ResNet-101's batch-32 layers).
+    if (mode < 0 && (double)(full + 1) * cus < 1.10 * (double)T) return false;
+    const int cx = cus / kXcds;
+    const int rx = (R + kXcds - 1) / kXcds;
+    p.dp_per_xcd = (int)(full * cx);
+    p.R = R;
+    p.cnt_bytes = ((size_t)R * 8 + 255) / 256 * 256;
+    size_t slots;
+    if (full <= 2 && 4 * R > cus) {
+        // One extra workgroup per CU (beside at most two whole ones) takes an
+        // equal range of the remaining slices; with at least one workgroup per
+        // remaining tile of an XCD a range spans at most two tiles.
+        p.scheme = kSkSplitWgs;
+        p.W = std::max(cx, rx);
+        p.p = 0;
+        slots = (size_t)kXcds * p.W * 2;
+    } else {
+        // Parts of >= 4 slices, at most one per CU, done by whole-tile
+        // workgroups before their own tile.
+        p.scheme = kSkPartsInDp;
+        p.W = 0;
+        p.p = std::min(std::min(cx / rx, S / 4), kSkMaxParts);
+        if (p.p < 2) return false;
+        slots = (size_t)kXcds * rx * p.p;
+    }
+    p.grid = kXcds * p.W + kXcds * p.dp_per_xcd;
+    p.ws_bytes = p.cnt_bytes + slots * (size_t)tile_elems * sizeof(float);
+    return true;
+}
+
+// One workgroup thread records the XCD it runs on (hardware register XCC_ID).
+__global__ void xcc_id_kernel(unsigned *out, int n) {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    if (threadIdx.x == 0 && (int)blockIdx.x < n) out[blockIdx.x] = v & 0xFu;
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+struct XcdState {
+    std::once_flag once;
+    std::atomic<int> local{0};
+};
+XcdState g_xcd[kMaxDevices];
+
+// Launch xcc_id_kernel over 4096 workgroups on a private stream and check that
+// block id b ran on XCD b % 8. Relaxed capture mode lets the check run even
+// while this thread captures a graph on another stream.
+int probe_xcd_mapping() {
+    constexpr int n = 4096;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return 0;
+    int ok = 0;
+    unsigned *d = nullptr;
+    hipStream_t st = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess &&
+        hipMalloc((void **)&d, n * sizeof(unsigned)) == hipSuccess) {
+        unsigned h[n];
+        hipLaunchKernelGGL(xcc_id_kernel, dim3(n), dim3(64), 0, st, d, n);
+        if (hipGetLastError() == hipSuccess &&
+            hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, st) == hipSuccess &&
+            hipStreamSynchronize(st) == hipSuccess) {
+            ok = 1;
+            for (int i = 0; i < n && ok; ++i) ok = h[i] == (unsigned)(i % kXcds);
+        }
+    }
+    if (d) hipFree(d);
+    if (st) hipStreamDestroy(st);
+    (void)hipGetLastError();
+    hipThreadExchangeStreamCaptureMode(&mode);
+    return ok;
+}
+} // namespace
+
+void probe_xcd_local(int device) {
+    if (device < 0 || device >= kMaxDevices) return;
+    XcdState &x = g_xcd[device];
+    std::call_once(x.once, [&x]() { x.local.store(probe_xcd_mapping()); });
+}
+
+bool xcd_local_parts() {
+    if (g_force_sys_exchange) return false;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+    return g_xcd[dev].local.load() != 0;
+}
+
+uint64_t streamk_epoch() {
+    // 48-bit launch tags, never 0; the start varies between processes.
+    static std::atomic<uint64_t> next{(uint64_t)std::chrono::steady_clock::now().time_since_epoch().count() * 2654435761u};
+    uint64_t e = next.fetch_add(1) & ((1ull << 48) - 1);
+    return e ? e : 1;
 }
 
 } // namespace spinn

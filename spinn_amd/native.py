@@ -178,6 +178,7 @@ _SIGS = {
     "spinn_hip_error_string": (C.c_char_p, [C.c_int]),
     "spinn_hip_version": (C.c_char_p, []),
     "spinn_hip_tune_force_tiles": (None, [C.c_int, C.c_int, C.c_int]),
+    "spinn_hip_tune_streamk": (None, [C.c_int]),
     # host runtime
     "spinn_load": (C.POINTER(SpinnContext), [C.c_char_p]),
     "spinn_plan": (C.c_int, [C.POINTER(SpinnContext), C.c_uint32]),
