@@ -591,6 +591,12 @@ def conv_layers_live(N, rows, algo_for, reps: int = 10) -> list:
             psz = L.spinn_hip_conv_packed_size(C.byref(d))
             pk = DeviceBuffer(psz) if psz else None
             wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
+            ksplit = ""
+            if wsz and algo == N.ALGO_IMPLICIT_GEMM:
+                # a workspace without the stream-K split means split-K partials
+                L.spinn_hip_tune_streamk(0)
+                ksplit = "split-K" if L.spinn_hip_conv_workspace_size(C.byref(d)) else "stream-K"
+                L.spinn_hip_tune_streamk(-1)
             ws = DeviceBuffer(wsz) if wsz else None
             if pk:
                 N.check(L.spinn_hip_conv_pack_weights(C.byref(d), dev["w"].ptr, pk.ptr, None), "pack")
@@ -603,7 +609,7 @@ def conv_layers_live(N, rows, algo_for, reps: int = 10) -> list:
             byts = (nbytes(r["n"], r["c"], r["h"], r["w"]) + nbytes(r["oc"], r["c"] // r["group"], r["kh"], r["kw"])
                     + nbytes(r["oc"]) + nbytes(r["n"], r["oc"], r["oh"], r["ow"]) * (2 if has_res else 1))
             out.append(dict(row=r, count=len(rs), algo=algo, ms=ms, flops=r["flops"],
-                            exec_flops=executed_flops(r, algo), bytes=byts, split=bool(wsz) and algo == 1))
+                            exec_flops=executed_flops(r, algo), bytes=byts, split=ksplit))
             for buf in (pk, ws):
                 if buf:
                     buf.free()
@@ -628,8 +634,10 @@ def layers_markdown(live: list, batch: int, policy: str) -> str:
              "replayed between HIP events "
              "(`bench.py`, conv_layers_live). GFLOP = direct-convolution count 2*N*OC*OH*OW*C*KH*KW; "
              "exec GFLOP = MFMA work actually issued (Winograd F(4x4,3x3): 36 GEMMs over 4x4 output tiles, "
-             "transforms not counted). % peak against 157.3 TFLOP/s fp32 MFMA.", "",
-             "| layer (C,H,W -> OC, k/s, act) | x | algo | split K | GFLOP | exec GFLOP | us / launch | "
+             "transforms not counted). K split: split-K (partials reduced by a second launch) or stream-K "
+             "(whole tiles plus the remaining tiles cut along K, finished in the same launch). "
+             "% peak against 157.3 TFLOP/s fp32 MFMA.", "",
+             "| layer (C,H,W -> OC, k/s, act) | x | algo | K split | GFLOP | exec GFLOP | us / launch | "
              "TFLOP/s direct | % peak direct | % peak executed |",
              "|---|---|---|---|---|---|---|---|---|---|"]
     tf = te = tt = 0.0
@@ -637,7 +645,7 @@ def layers_markdown(live: list, batch: int, policy: str) -> str:
         r = e["row"]
         t = e["ms"] * 1e-3
         lines.append(f"| {r['c']},{r['h']},{r['w']} -> {r['oc']}, {r['kh']}x{r['kw']}/s{r['sh']}, {r['act']} | "
-                     f"{e['count']} | {ALGO_NAMES.get(e['algo'], e['algo'])} | {'yes' if e['split'] else ''} | "
+                     f"{e['count']} | {ALGO_NAMES.get(e['algo'], e['algo'])} | {e['split']} | "
                      f"{e['flops'] / 1e9:.2f} | {e['exec_flops'] / 1e9:.2f} | {e['ms'] * 1e3:.1f} | "
                      f"{e['flops'] / t / 1e12:.1f} | {100 * e['flops'] / t / PEAK_FP32_MFMA:.1f} | "
                      f"{100 * e['exec_flops'] / t / PEAK_FP32_MFMA:.1f} |")
@@ -674,7 +682,8 @@ def igemm_algorithmic_bytes(batch: int, policy: str) -> float:
 def traffic_summary(d: Path, batch: int, policy: str, commands: list) -> dict:
     """Reduce the four rocprofv3 --pmc counter CSVs under `d` (calib_{FETCH,WRITE}_SIZE
     from the calibration kernels, r101_{FETCH,WRITE}_SIZE from --profile-pass) to
-    calibrated HBM-side bytes per conv_igemm_kernel dispatch."""
+    calibrated HBM-side bytes per implicit-GEMM conv dispatch (conv_igemm_kernel and its
+    data-parallel + stream-K form conv_igemm_sk_kernel; split-K reductions not counted)."""
     import csv
 
     def rows(name):
@@ -692,12 +701,13 @@ def traffic_summary(d: Path, batch: int, policy: str, commands: list) -> dict:
     f_write = kib / calib("WRITE_SIZE", "fill")
     per = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        v = [x for n, x in rows(f"r101_{counter}") if "conv_igemm_kernel" in n]
+        v = [x for n, x in rows(f"r101_{counter}") if "conv_igemm_kernel" in n or "conv_igemm_sk_kernel" in n]
         per[counter] = (len(v), sum(v) / len(v))
     fetch_b = per["FETCH_SIZE"][1] * 1024 * f_fetch
     write_b = per["WRITE_SIZE"][1] * 1024 * f_write
     return {
-        "kernel": f"conv_igemm_kernel (all tile instantiations), implicit-GEMM layers of ResNet-101 v1.5 fp32 "
+        "kernel": f"conv_igemm_kernel / conv_igemm_sk_kernel (all tile instantiations), implicit-GEMM layers of "
+                  f"ResNet-101 v1.5 fp32 "
                   f"batch {batch}",
         "conv_policy": policy, "batch": batch, "commands": commands,
         "calibration": {"method": "256 MiB fills (spinn_hip_fill_u32) and 256 MiB device copies (spinn_hip_copy) "
@@ -1137,7 +1147,8 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(ig_tflops, 3), "peak": PEAK_FP32_MFMA / 1e12,
                      "unit": "TFLOP/s", "frac": round(ig_tflops * 1e12 / PEAK_FP32_MFMA, 4),
                      "traffic": measured_traffic(a.batch, a.policy),
-                     "kernel": f"conv_igemm_kernel (implicit-GEMM conv, {n_ig} layers, batch {a.batch})",
+                     "kernel": f"conv_igemm_kernel / conv_igemm_sk_kernel (implicit-GEMM conv, {n_ig} layers, "
+                               f"batch {a.batch})",
                      "launch_us": round(ig_live_ms / max(n_ig, 1) * 1e3, 2),
                      "achieved_node_events": round(ig_node_tflops, 3),
                      "method": "direct-conv FLOPs of the implicit-GEMM layers / their kernel time, each "
