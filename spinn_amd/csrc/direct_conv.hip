@@ -245,6 +245,172 @@ __global__ __launch_bounds__(256) void dw_direct_kernel(const float *__restrict_
     }
 }
 
+// Depthwise convolution, one wave per (plane, run of row bands). The wave's
+// lanes split each output row of its plane into 4-pixel quads (owq lanes per
+// band) and take bpw = 64 / owq bands of RB output rows each, so the plane's
+// filter and bias are wave-uniform and sit in scalar registers. Each input row
+// of a band is one 16-byte load per lane (two for stride 2); the K/2 columns
+// on either side of a lane's quad are the neighbouring lanes' values, moved by
+// a lane permute (zero at the band's ends: the image edge, where the pad is
+// K/2). Every wave issues all its loads at once (the filter's scalar loads
+// beside them), computes and stores: short bands, many waves (measured on
+// YOLOv10n's batch-16 layers: 2- and 3-row bands beat 4- and 8-row ones, and
+// beat waves that loop over several bands with the next band's loads in
+// flight). Epilogue fused, float4 stores.
+constexpr int kDwWaveThreads = 256; // 4 waves per workgroup
+
+template <int K, int S, int RB, bool VEC>
+__global__ __launch_bounds__(kDwWaveThreads) void dw_wave_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                      const float *__restrict__ bias, const float *__restrict__ res,
+                                                      float *__restrict__ y, SpinnHipConvDesc d, int owq, int bands,
+                                                      int bpw, int wpp, int waves) {
+    static_assert(S == 1 || (S == 2 && K == 3), "stride 2 only for 3 x 3 filters");
+    constexpr int HL = S == 1 ? K / 2 : 1; // columns from the left neighbour
+    constexpr int HR = S == 1 ? K / 2 : 0; // columns from the right neighbour
+    constexpr int NV = HL + 4 * S + HR;     // window columns of one input row
+    constexpr int IR = (RB - 1) * S + K;    // input rows of a band
+    const int lane = threadIdx.x & 63;
+    // the scalar arguments fetched in one round trip before any use
+    uint64_t px = (uint64_t)x, pr = (uint64_t)res, py = (uint64_t)y;
+    asm volatile(""
+                 : "+s"(owq), "+s"(bands), "+s"(bpw), "+s"(wpp), "+s"(waves), "+s"(d.n), "+s"(d.c), "+s"(d.h),
+                   "+s"(d.w), "+s"(d.oh), "+s"(d.ow), "+s"(d.ph), "+s"(d.act), "+s"(px), "+s"(pr), "+s"(py));
+    typedef __attribute__((address_space(1))) const float gcf;
+    typedef __attribute__((address_space(1))) float gf;
+    x = (const float *)(gcf *)px;
+    res = (const float *)(gcf *)pr;
+    y = (float *)(gf *)py;
+    // 32-bit index math (the host keeps waves * 64 below 2^31); the waves past
+    // the last one of the grid's final workgroup run with every lane off, so
+    // no branch holds back the first loads.
+    const uint32_t wave =
+        blockIdx.x * (uint32_t)(kDwWaveThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t pl = wave / (uint32_t)wpp;
+    const int bg = (int)(wave - pl * (uint32_t)wpp);
+    const int c = (int)(pl % (uint32_t)d.c);
+    const int bl = lane / owq, q = lane - bl * owq;
+    const int b = bg * bpw + bl;
+    const bool on = wave < (uint32_t)waves && bl < bpw && b < bands;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(((int64_t)d.n * d.c) * d.h * d.w * 4));
+    const uint32_t plane_off = pl * (uint32_t)(d.h * d.w);
+    const int ih0 = b * RB * S - d.ph;
+    const int col0 = 4 * S * q;
+    const bool has_l = q > 0, has_r = q + 1 < owq; // neighbour lane in the same band
+    const int addr_l = (lane - 1) << 2, addr_r = (lane + 1) << 2;
+    f32x4 f[IR][S];
+#pragma unroll
+    for (int ir = 0; ir < IR; ++ir) {
+        const int ih = ih0 + ir;
+        const bool row_ok = on && (unsigned)ih < (unsigned)d.h;
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            const int col = col0 + 4 * u;
+            f[ir][u] = buf_f32x4(rx, (row_ok && col < d.w) ? (plane_off + (uint32_t)ih * d.w + col) * 4u : kOOB);
+        }
+    }
+    // residual rows and the filter, in flight with the input rows
+    const uint32_t out0 = (pl * (uint32_t)d.oh + (uint32_t)(b * RB)) * (uint32_t)d.ow + 4u * q;
+    f32x4 rv[RB];
+    if (VEC && res) {
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(res, (uint32_t)(((int64_t)d.n * d.c) * d.oh * d.ow * 4));
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+            rv[r] = buf_f32x4(rr, (on && b * RB + r < d.oh) ? (out0 + (uint32_t)(r * d.ow)) * 4u : kOOB);
+    } else {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) rv[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    float wk[K * K];
+#pragma unroll
+    for (int i = 0; i < K * K; ++i) wk[i] = w[c * K * K + i];
+    float bv = bias ? bias[c] : 0.f;
+    // Materialise the filter and bias here, while the input rows are in flight
+    // (left alone, the compiler sinks their loads below the wait for the rows).
+#pragma unroll
+    for (int i = 0; i < K * K; ++i) asm volatile("" : "+s"(wk[i]));
+    asm volatile("" : "+s"(bv));
+    int act = d.act;
+    asm volatile("" : "+s"(act));
+    float acc[RB][4];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[r][j] = 0.f;
+#pragma unroll
+    for (int ir = 0; ir < IR; ++ir) {
+        float v[NV];
+#pragma unroll
+        for (int u = 0; u < S; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[HL + 4 * u + e] = f[ir][u][e];
+#pragma unroll
+        for (int j = 0; j < HL; ++j) {
+            const float t =
+                __int_as_float(__builtin_amdgcn_ds_bpermute(addr_l, __float_as_int(f[ir][S - 1][4 - HL + j])));
+            v[j] = has_l ? t : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < HR; ++j) {
+            const float t = __int_as_float(__builtin_amdgcn_ds_bpermute(addr_r, __float_as_int(f[ir][0][j])));
+            v[HL + 4 * S + j] = has_r ? t : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int kh = ir - r * S;
+            if (kh >= 0 && kh < K) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int kw = 0; kw < K; ++kw) acc[r][j] = fmaf(wk[kh * K + kw], v[j * S + kw], acc[r][j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const int oh = b * RB + r;
+        if (!on || oh >= d.oh) break;
+        const int ow0 = 4 * q;
+        const uint32_t o = out0 + (uint32_t)(r * d.ow);
+        if constexpr (VEC) {
+            const f32x4 out = {apply_act(acc[r][0] + bv + rv[r][0], act), apply_act(acc[r][1] + bv + rv[r][1], act),
+                               apply_act(acc[r][2] + bv + rv[r][2], act), apply_act(acc[r][3] + bv + rv[r][3], act)};
+            // non-temporal: nothing in this launch reads the output again (measured on
+            // YOLOv10n's batch-16 80 x 80 layers: 15.7 -> 13.5 us)
+            __builtin_nontemporal_store(out, reinterpret_cast<f32x4 *>(y + o));
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (ow0 + j < d.ow) {
+                    float vv = acc[r][j] + bv;
+                    if (res) vv += res[o + j];
+                    y[o + j] = apply_act(vv, act);
+                }
+            }
+        }
+    }
+}
+
+template <int K, int S, int RB>
+static int launch_dw_wave(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias,
+                          const float *res, float *y, hipStream_t st) {
+    const int owq = (d->ow + 3) / 4;
+    const int bands = (d->oh + RB - 1) / RB;
+    const int bpw = 64 / owq;
+    const int wpp = (bands + bpw - 1) / bpw;
+    const int64_t waves = (int64_t)d->n * d->c * wpp;
+    constexpr int wpb = kDwWaveThreads / 64;
+    const int64_t blocks = (waves + wpb - 1) / wpb;
+    if (blocks * kDwWaveThreads > INT32_MAX) return SPINN_HIP_EUNSUPPORTED;
+    const bool vec = d->ow % 4 == 0 && ((uintptr_t)y & 15u) == 0 && (!res || ((uintptr_t)res & 15u) == 0);
+    if (vec)
+        hipLaunchKernelGGL((dw_wave_kernel<K, S, RB, true>), dim3((unsigned)blocks), dim3(kDwWaveThreads), 0, st, x,
+                           w, bias, res, y, *d, owq, bands, bpw, wpp, (int)waves);
+    else
+        hipLaunchKernelGGL((dw_wave_kernel<K, S, RB, false>), dim3((unsigned)blocks), dim3(kDwWaveThreads), 0, st, x,
+                           w, bias, res, y, *d, owq, bands, bpw, wpp, (int)waves);
+    return check_launch();
+}
+
 template <int K, int S, int RPT>
 static int launch_dw_direct(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias,
                             const float *res, float *y, hipStream_t st) {
@@ -370,6 +536,17 @@ int direct_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const
                 float *y, hipStream_t st) {
     const int ohw = d->oh * d->ow;
     const bool depthwise = d->group == d->c && d->group == d->oc && d->kh == d->kw && d->sh == d->sw;
+    if (depthwise && dw_direct_ok(d) && d->ow <= 256 && (d->kh == 3 || d->kh == 5 || d->kh == 7) &&
+        (d->sh == 1 || (d->sh == 2 && d->kh == 3)) && d->ph == d->kh / 2) {
+        // 3-row bands for rows of >= 64 pixels, 2-row bands below (measured on YOLOv10n's
+        // batch-16 layers: 80 x 80 planes 10.6 -> 9.9 us with 3 rows, 20 x 20 and 40 x 40
+        // planes slower by 0.4-0.8 us)
+        if (d->kh == 3 && d->sh == 1 && d->ow >= 64) return launch_dw_wave<3, 1, 3>(d, x, w, bias, res, y, st);
+        if (d->kh == 3 && d->sh == 1) return launch_dw_wave<3, 1, 2>(d, x, w, bias, res, y, st);
+        if (d->kh == 3) return launch_dw_wave<3, 2, 1>(d, x, w, bias, res, y, st);
+        if (d->kh == 5) return launch_dw_wave<5, 1, 2>(d, x, w, bias, res, y, st);
+        return launch_dw_wave<7, 1, 2>(d, x, w, bias, res, y, st);
+    }
     if (depthwise && dw_direct_ok(d) && (d->kh == 3 || d->kh == 5 || d->kh == 7) &&
         (d->sh == 1 || (d->sh == 2 && d->kh == 3))) {
         // Measured on YOLOv10n's 13 depthwise layers at batch 16: 114 us against 180 us for the

@@ -50,6 +50,15 @@ CASES = [
     ("depthwise_large_plane", 1, 4, 160, 161, 4, 3, 1, 1, 4, 1, 0),   # 5 x 6 tiles, ragged right edge
     ("depthwise_tiny_planes", 4, 96, 7, 5, 96, 3, 1, 1, 96, 4, 0),    # 384 planes of one partial tile, residual
     ("grouped_direct_cg2", 1, 16, 12, 12, 8, 3, 1, 1, 8, 1, 0),      # two input channels per group: general kernel
+    # one wave per plane and run of row bands (4-pixel quads across the row, neighbours by lane permute)
+    ("dw_wave_w256", 1, 8, 9, 256, 8, 3, 1, 1, 8, 3, 0),              # 64 quads: one band per wave
+    ("dw_wave_w252_rows_ragged", 2, 4, 14, 252, 4, 3, 1, 1, 4, 1, 0), # 63 quads, last band 2 rows
+    ("dw_wave_5x5_w36", 2, 16, 13, 36, 16, 5, 1, 2, 16, 0, 0),       # 9 quads: 7 bands per wave
+    ("dw_wave_7x7_w44_res", 2, 8, 11, 44, 8, 7, 1, 3, 8, 4, 0),      # 11 quads, residual fused
+    ("dw_wave_s2_w84", 3, 16, 27, 84, 16, 3, 2, 1, 16, 1, 0),        # 42-wide output: scalar stores, half-empty last quad
+    ("dw_wave_s2_w200_add_relu", 1, 8, 10, 200, 8, 3, 2, 1, 8, 5, 0),
+    ("dw_wave_80x80_silu", 2, 20, 80, 80, 20, 3, 1, 1, 20, 3, 0),    # YOLOv10n plane: 3 bands per wave
+    ("dw_fallback_w260", 1, 4, 6, 260, 4, 3, 1, 1, 4, 1, 0),         # 65 quads: per-thread kernel
     ("winograd_add_relu", 2, 64, 28, 28, 64, 3, 1, 1, 1, 5, 2),
     ("winograd_odd", 1, 16, 15, 13, 8, 3, 1, 1, 1, 1, 2),
     ("winograd_c256", 1, 256, 14, 14, 256, 3, 1, 1, 1, 1, 2),
