@@ -142,13 +142,17 @@ struct WkPointwise {
 };
 
 // Implicit-GEMM B operand, K in (kh, kw, c) order with Cg % 16 == 0: a block
-// of 8 or 16 k lies in one tap, so one bounds test per block.
+// of 8 or 16 k lies in one tap, so one bounds test per block. A wave fetches
+// its blocks in increasing k, one block at a time: the loader keeps the next
+// block's (kh, kw, c) position and steps it, instead of dividing k by Cg and
+// KW for every block.
 struct WkTap {
     __amdgpu_buffer_rsrc_t rsrc;
     PixelOrigin px;
     uint32_t hw;
     int Cg, KW, KH, H, W;
     int k_end;
+    int blk, c_cur, kh_cur, kw_cur; // block size and the next block's position
     __device__ __forceinline__ void init(const ConvGeom &g, int n, int group, int kend) {
         rsrc = make_rsrc(g.x, g.x_bytes);
         px.init(g, n, group);
@@ -160,17 +164,30 @@ struct WkTap {
         W = g.W;
         k_end = kend;
     }
-    __device__ __forceinline__ void fetch(int k0, int h, float (&v)[4]) const {
-        const int tap = k0 / Cg;
-        const int c0 = k0 - tap * Cg;
-        const int kh = tap / KW;
-        const int kw = tap - kh * KW;
-        const int ih = px.ih0 + kh;
-        const int iw = px.iw0 + kw;
+    // First block at k = kb (a multiple of `block`), blocks of `block` k.
+    __device__ __forceinline__ void start(int kb, int block) {
+        blk = block;
+        const int tap = kb / Cg;
+        c_cur = kb - tap * Cg;
+        kh_cur = tap / KW;
+        kw_cur = tap - kh_cur * KW;
+    }
+    // The block at k0, which is the block after the previous call's.
+    __device__ __forceinline__ void fetch(int k0, int h, float (&v)[4]) {
+        const int ih = px.ih0 + kh_cur;
+        const int iw = px.iw0 + kw_cur;
         const bool ok = px.valid && k0 < k_end && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
-        const uint32_t off0 = (px.base + (uint32_t)(c0 + 4 * h) * hw + (uint32_t)ih * W + iw) * 4u;
+        const uint32_t off0 = (px.base + (uint32_t)(c_cur + 4 * h) * hw + (uint32_t)ih * W + iw) * 4u;
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = buf_f32(rsrc, ok ? off0 + (uint32_t)q * hw * 4u : kOOB);
+        c_cur += blk;
+        if (c_cur >= Cg) {
+            c_cur = 0;
+            if (++kw_cur == KW) {
+                kw_cur = 0;
+                ++kh_cur;
+            }
+        }
     }
 };
 
@@ -212,7 +229,7 @@ struct WkGather {
 // ---- the K loop of one wave and the cross-wave sum ----
 
 template <int TS, class AF, class BF>
-__device__ __forceinline__ void wk_fetch(const AF &af, const BF &bf, int k0, int h, float (&a)[4][4],
+__device__ __forceinline__ void wk_fetch(const AF &af, BF &bf, int k0, int h, float (&a)[4][4],
                                          float (&b)[4][4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -250,7 +267,7 @@ __device__ __forceinline__ void wk_mfma_part(const float (&a)[4][4], const float
 // k_end (= ke), so chunks past the end need no branch; every fetch has a use
 // on every path, so none can be sunk below the MFMAs it is meant to overlap.
 template <int TS, int NB, class AF, class BF>
-__device__ __forceinline__ void wk_accumulate(const AF &af, const BF &bf, int kb, int ke, int h,
+__device__ __forceinline__ void wk_accumulate(const AF &af, BF &bf, int kb, int ke, int h,
                                               typename WkShape<TS>::Acc &acc) {
     static_assert(NB == 2 || NB == 4, "ring of 2 or 4 chunks");
     constexpr int kChunk = wk_chunk<TS>();
@@ -327,7 +344,8 @@ __global__ __launch_bounds__(64 * KG) void wavek_conv_kernel(WkConvArgs a) {
     using S = WkShape<TS>;
     __shared__ float red[KG][S::kAcc][64];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform: the K range and the tap / channel split of every block are scalar work
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = S::group(lane);
     int tm, tn;
     xcd_tile(gridDim.y, gridDim.x, tm, tn);
@@ -344,6 +362,7 @@ __global__ __launch_bounds__(64 * KG) void wavek_conv_kernel(WkConvArgs a) {
                 m0 + S::col(lane), a.M, ke);
     BF bf;
     bf.init(a.geom, n0 + S::col(lane), group, ke);
+    if constexpr (std::is_same<BF, WkTap>::value) bf.start(kb, S::kBlock);
     typename S::Acc acc;
     wk_accumulate<TS, NB>(af, bf, kb, ke, h, acc);
     const int ntot = a.geom.ntot;
@@ -378,7 +397,8 @@ __global__ __launch_bounds__(64 * KG) void wavek_gemm_kernel(WkGemmArgs a) {
     using S = WkShape<TS>;
     __shared__ float red[KG][S::kAcc][64];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform: the K range and the tap / channel split of every block are scalar work
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = S::group(lane);
     int tm, tn;
     xcd_tile(gridDim.y, gridDim.x, tm, tn);
