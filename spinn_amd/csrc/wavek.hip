@@ -86,11 +86,14 @@ struct WkTContig {
 };
 
 // Source [T][ld] with k contiguous: v = src[t * ld + k0 + 4h .. +3]; VEC: one
-// 16-byte load (ld % 4 == 0, aligned base, k_end % 4 == 0).
+// 16-byte load (ld % 4 == 0, aligned base, k_end % 4 == 0). The lane's row
+// offset is computed once, with the row test folded in (kOOB for rows past
+// t_total: adding a k offset below 2^31 keeps it out of range without
+// wrapping); a block then costs one add and the K-end test.
 template <bool VEC>
 struct WkKContig {
     __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t row;
+    uint32_t row, vrow;
     bool t_ok;
     int k_end;
     __device__ __forceinline__ void init(const float *base, uint32_t bytes, uint32_t ld, int t, int t_total,
@@ -98,12 +101,13 @@ struct WkKContig {
         rsrc = make_rsrc(base, bytes);
         t_ok = t < t_total;
         row = t_ok ? (uint32_t)t * ld : 0u;
+        vrow = t_ok ? row * 4u : kOOB;
         k_end = kend;
     }
     __device__ __forceinline__ void fetch(int k0, int h, float (&v)[4]) const {
         const int k = k0 + 4 * h;
         if constexpr (VEC) {
-            const f32x4 r = buf_f32x4(rsrc, (t_ok && k < k_end) ? (row + (uint32_t)k) * 4u : kOOB);
+            const f32x4 r = buf_f32x4(rsrc, k < k_end ? vrow + (uint32_t)k * 4u : kOOB);
             v[0] = r[0];
             v[1] = r[1];
             v[2] = r[2];
@@ -145,18 +149,26 @@ struct WkPointwise {
 // of 8 or 16 k lies in one tap, so one bounds test per block. A wave fetches
 // its blocks in increasing k, one block at a time: the loader keeps the next
 // block's (kh, kw, c) position and steps it, instead of dividing k by Cg and
-// KW for every block.
+// KW for every block. Each lane keeps the byte offset of its pixel's current
+// tap at channel 4h, or kOOB where the tap falls outside the image (adding a
+// channel offset, below 2^31, keeps it out of range without wrapping); the
+// channel offset of a block is wave-uniform, and a block at or past the K end
+// reads through a descriptor of size 0. A block's four loads then cost one add
+// each, and only a change of tap recomputes the lane's offset.
 struct WkTap {
-    __amdgpu_buffer_rsrc_t rsrc;
+    __amdgpu_buffer_rsrc_t rsrc, rnone;
     PixelOrigin px;
-    uint32_t hw;
+    uint32_t hw, hw4, lane_c; // lane_c: the lane's channel offset 4h * hw
     int Cg, KW, KH, H, W;
     int k_end;
     int blk, c_cur, kh_cur, kw_cur; // block size and the next block's position
+    uint32_t vtap;                  // byte offset of (pixel, current tap, channel 4h), or kOOB
     __device__ __forceinline__ void init(const ConvGeom &g, int n, int group, int kend) {
         rsrc = make_rsrc(g.x, g.x_bytes);
+        rnone = make_rsrc(g.x, 0u);
         px.init(g, n, group);
         hw = (uint32_t)(g.H * g.W);
+        hw4 = hw * 4u;
         Cg = g.Cg;
         KW = g.KW;
         KH = g.KH;
@@ -164,22 +176,28 @@ struct WkTap {
         W = g.W;
         k_end = kend;
     }
-    // First block at k = kb (a multiple of `block`), blocks of `block` k.
-    __device__ __forceinline__ void start(int kb, int block) {
+    __device__ __forceinline__ void set_tap() {
+        const int ih = px.ih0 + kh_cur;
+        const int iw = px.iw0 + kw_cur;
+        const bool ok = px.valid && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
+        vtap = ok ? (px.base + lane_c + (uint32_t)ih * W + iw) * 4u : kOOB;
+    }
+    // First block at k = kb (a multiple of `block`), blocks of `block` k; h: the lane's group.
+    __device__ __forceinline__ void start(int kb, int block, int h) {
         blk = block;
+        lane_c = (uint32_t)(4 * h) * hw;
         const int tap = kb / Cg;
         c_cur = kb - tap * Cg;
         kh_cur = tap / KW;
         kw_cur = tap - kh_cur * KW;
+        set_tap();
     }
     // The block at k0, which is the block after the previous call's.
-    __device__ __forceinline__ void fetch(int k0, int h, float (&v)[4]) {
-        const int ih = px.ih0 + kh_cur;
-        const int iw = px.iw0 + kw_cur;
-        const bool ok = px.valid && k0 < k_end && (unsigned)ih < (unsigned)H && (unsigned)iw < (unsigned)W;
-        const uint32_t off0 = (px.base + (uint32_t)(c_cur + 4 * h) * hw + (uint32_t)ih * W + iw) * 4u;
+    __device__ __forceinline__ void fetch(int k0, int, float (&v)[4]) {
+        const __amdgpu_buffer_rsrc_t r = k0 < k_end ? rsrc : rnone;
+        const uint32_t c_off = (uint32_t)c_cur * hw4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = buf_f32(rsrc, ok ? off0 + (uint32_t)q * hw * 4u : kOOB);
+        for (int q = 0; q < 4; ++q) v[q] = buf_f32(r, vtap + c_off + (uint32_t)q * hw4);
         c_cur += blk;
         if (c_cur >= Cg) {
             c_cur = 0;
@@ -187,6 +205,7 @@ struct WkTap {
                 kw_cur = 0;
                 ++kh_cur;
             }
+            set_tap();
         }
     }
 };
@@ -362,7 +381,7 @@ __global__ __launch_bounds__(64 * KG) void wavek_conv_kernel(WkConvArgs a) {
                 m0 + S::col(lane), a.M, ke);
     BF bf;
     bf.init(a.geom, n0 + S::col(lane), group, ke);
-    if constexpr (std::is_same<BF, WkTap>::value) bf.start(kb, S::kBlock);
+    if constexpr (std::is_same<BF, WkTap>::value) bf.start(kb, S::kBlock, h);
     typename S::Acc acc;
     wk_accumulate<TS, NB>(af, bf, kb, ke, h, acc);
     const int ntot = a.geom.ntot;
@@ -454,8 +473,11 @@ int launch_wk_conv_nb(const WkConvArgs &a, int kg, dim3 grid, hipStream_t st) {
     return check_launch();
 }
 
-// Waves with at most 2 chunks use the 2-deep ring, longer ones the 4-deep one.
-bool wk_deep(int kq, int chunk) { return kq > 2 * chunk; }
+// Waves with at most 4 chunks use the 2-deep ring, longer ones the 4-deep one:
+// the deep ring issues 4 chunks of loads before a wave's first MFMA, which for
+// a short K range only delays it (measured on the 1x64x56x56 3x3 layer, 72 k
+// per wave: 8.25 -> 7.85 us).
+bool wk_deep(int kq, int chunk) { return kq > 4 * chunk; }
 
 template <class AF, class BF>
 int launch_wk_conv(const WkConvArgs &a, int ts, int kg, dim3 grid, hipStream_t st) {
