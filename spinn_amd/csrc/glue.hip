@@ -31,6 +31,36 @@ __global__ __launch_bounds__(256) void maxpool_kernel(const float *__restrict__ 
     }
 }
 
+// The same pooling with the plane on grid.y (a stride of gridDim.y over the
+// planes) and one thread per output pixel of the plane on grid.x: 32-bit index
+// math instead of the 64-bit divisions of a flat output index (ResNet-101's
+// 3x3/2 pool at batch 32: 49 us before).
+__global__ __launch_bounds__(256) void maxpool_plane_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                            SpinnHipPoolDesc d, int planes) {
+    const int ohw = d.oh * d.ow;
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    if (p >= ohw) return;
+    const int oh = p / d.ow;
+    const int ow = p - oh * d.ow;
+    const int ih0 = oh * d.sh - d.ph, iw0 = ow * d.sw - d.pw;
+    const int hw = d.h * d.w;
+    for (int pl = blockIdx.y; pl < planes; pl += gridDim.y) {
+        const float *xp = x + (int64_t)pl * hw;
+        float m = -1e30f;
+        for (int kh = 0; kh < d.kh; ++kh) {
+            const int ih = ih0 + kh;
+            if ((unsigned)ih >= (unsigned)d.h) continue;
+            for (int kw = 0; kw < d.kw; ++kw) {
+                const int iw = iw0 + kw;
+                if ((unsigned)iw >= (unsigned)d.w) continue;
+                const float v = xp[ih * d.w + iw];
+                m = v > m ? v : m;
+            }
+        }
+        y[(int64_t)pl * ohw + p] = m;
+    }
+}
+
 // inner == 1: one wave per output, lanes stride the reduced axis, then a
 // wave-shuffle tree (SPINN/run_time/ops/reduce/reduce_mean.c:68-74).
 __global__ __launch_bounds__(256) void mean_rows_kernel(const float *__restrict__ x, float *__restrict__ y,
@@ -75,7 +105,13 @@ static int grid_for(int64_t n, int per_block = 256, int cap = 16384) {
 int maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, hipStream_t st) {
     const int64_t total = (int64_t)d->n * d->c * d->oh * d->ow;
     if (total == 0) return 0;
-    hipLaunchKernelGGL(maxpool_kernel, dim3(grid_for(total)), dim3(256), 0, st, x, y, *d);
+    const int64_t planes = (int64_t)d->n * d->c;
+    if ((int64_t)d->h * d->w <= INT32_MAX && (int64_t)d->oh * d->ow <= INT32_MAX - 256 && planes <= INT32_MAX) {
+        const dim3 grid((unsigned)((d->oh * d->ow + 255) / 256), (unsigned)std::min<int64_t>(planes, 65535));
+        hipLaunchKernelGGL(maxpool_plane_kernel, grid, dim3(256), 0, st, x, y, *d, (int)planes);
+    } else {
+        hipLaunchKernelGGL(maxpool_kernel, dim3(grid_for(total)), dim3(256), 0, st, x, y, *d);
+    }
     return check_launch();
 }
 
