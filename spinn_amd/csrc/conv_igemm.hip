@@ -510,8 +510,10 @@ static int igemm_wavek(const SpinnHipConvDesc *d) {
                       pointwise);
 }
 
+static bool igemm_stem(const SpinnHipConvDesc *d) { return stem_mfma_eligible(d) && !tiles_forced(); }
+
 size_t igemm_workspace_bytes(const SpinnHipConvDesc *d) {
-    if (igemm_wavek(d)) return 0;
+    if (igemm_stem(d) || igemm_wavek(d)) return 0;
     TileChoice tc = igemm_tiles(d);
     SkPlan sp;
     if (igemm_streamk(d, tc, sp)) {
@@ -526,6 +528,7 @@ size_t igemm_workspace_bytes(const SpinnHipConvDesc *d) {
 
 int igemm_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed, const float *bias,
                const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st) {
+    if (igemm_stem(d)) return stem_mfma_conv(d, x, packed, bias, res, y, st);
     if (const int ts = igemm_wavek(d)) return wavek_conv(d, ts, x, w, packed, bias, res, y, st);
     ConvKArgs a{};
     const int OCg = d->oc / d->group;

@@ -95,6 +95,14 @@ bool xcd_local_parts();
 // an (M x N x K) problem repeated `reps` times: 32 or 16, or 0 when it runs on the
 // 64/128-wide tiles of choose_tiles. `pointwise`: a 1x1 stride-1 unpadded conv.
 int wavek_tile(int M, int N, int K, int reps, bool pointwise);
+// true while spinn_hip_tune_force_tiles holds a tile shape or a K split
+bool tiles_forced();
+
+// 7x7 stride-2 stems (stem_mfma.hip): C <= 4, OC <= 64, output rows <= 128 pixels,
+// one workgroup per output row over an LDS-staged window; packed W^T as igemm_pack.
+bool stem_mfma_eligible(const SpinnHipConvDesc *d);
+int stem_mfma_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+                   const float *res, float *y, hipStream_t st);
 
 // wave-K kernels (wavek.hip): no workspace, packed conv weights as igemm_pack
 int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w, const float *packed, const float *bias,

@@ -19,6 +19,8 @@ void force_tiles(int bm, int bn, int split) {
     g_force_split = split;
 }
 
+bool tiles_forced() { return g_force_bm != 0 || g_force_split > 1; }
+
 static int env_wavek() {
     // SPINN_WAVEK=0 never runs the wave-K kernel, 1 runs it for every shape;
     // unset = per-shape choice.

@@ -34,6 +34,11 @@ CASES = [
     ("oc24_splitk", 1, 512, 7, 7, 24, 3, 1, 1, 1, 1, 0),
     ("stem3x3_direct", 2, 3, 64, 64, 16, 3, 2, 1, 1, 3, 3),        # few-input-channel stem kernel
     ("stem7x7_direct", 1, 3, 40, 40, 64, 7, 2, 3, 1, 1, 3),
+    # 7x7 stride-2 stems on the row-per-workgroup MFMA kernel (LDS-staged window)
+    ("stem7x7_224_res", 2, 3, 224, 224, 64, 7, 2, 3, 1, 5, 0),         # ResNet stem shape, residual + ReLU
+    ("stem7x7_c1_oc40_ragged", 3, 1, 37, 45, 40, 7, 2, 3, 1, 3, 0),   # one channel, 40 of 64 rows, 23-pixel rows
+    ("stem7x7_c4_ow128", 1, 4, 30, 256, 64, 7, 2, 3, 1, 1, 0),         # four channels, 128-pixel rows
+    ("stem7x7_ow129_fallback", 1, 3, 9, 258, 64, 7, 2, 3, 1, 1, 0),    # 129-pixel rows: generic implicit GEMM
     ("stem_c1_direct_oc20_res", 1, 1, 33, 35, 20, 3, 1, 1, 1, 5, 3),  # partial 16-channel chunk, residual
     ("direct_group1_general", 1, 6, 10, 12, 5, 3, 1, 1, 1, 1, 3),      # C > 4: general direct kernel
     ("conv3x3_s2", 2, 128, 28, 28, 128, 3, 2, 1, 1, 1, 0),
