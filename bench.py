@@ -682,8 +682,9 @@ def igemm_algorithmic_bytes(batch: int, policy: str) -> float:
 def traffic_summary(d: Path, batch: int, policy: str, commands: list) -> dict:
     """Reduce the four rocprofv3 --pmc counter CSVs under `d` (calib_{FETCH,WRITE}_SIZE
     from the calibration kernels, r101_{FETCH,WRITE}_SIZE from --profile-pass) to
-    calibrated HBM-side bytes per implicit-GEMM conv dispatch (conv_igemm_kernel and its
-    data-parallel + stream-K form conv_igemm_sk_kernel; split-K reductions not counted)."""
+    calibrated HBM-side bytes per implicit-GEMM conv dispatch (conv_igemm_kernel, its
+    data-parallel + stream-K form conv_igemm_sk_kernel and the 7x7 stem's stem7_mfma_kernel;
+    split-K reductions not counted)."""
     import csv
 
     def rows(name):
@@ -701,12 +702,13 @@ def traffic_summary(d: Path, batch: int, policy: str, commands: list) -> dict:
     f_write = kib / calib("WRITE_SIZE", "fill")
     per = {}
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        v = [x for n, x in rows(f"r101_{counter}") if "conv_igemm_kernel" in n or "conv_igemm_sk_kernel" in n]
+        v = [x for n, x in rows(f"r101_{counter}")
+             if "conv_igemm_kernel" in n or "conv_igemm_sk_kernel" in n or "stem7_mfma_kernel" in n]
         per[counter] = (len(v), sum(v) / len(v))
     fetch_b = per["FETCH_SIZE"][1] * 1024 * f_fetch
     write_b = per["WRITE_SIZE"][1] * 1024 * f_write
     return {
-        "kernel": f"conv_igemm_kernel / conv_igemm_sk_kernel (all tile instantiations), implicit-GEMM layers of "
+        "kernel": f"conv_igemm_kernel / conv_igemm_sk_kernel / stem7_mfma_kernel (all instantiations), implicit-GEMM layers of "
                   f"ResNet-101 v1.5 fp32 "
                   f"batch {batch}",
         "conv_policy": policy, "batch": batch, "commands": commands,
@@ -1147,7 +1149,7 @@ def main() -> int:
         "roofline": {"bound": "mfma", "achieved": round(ig_tflops, 3), "peak": PEAK_FP32_MFMA / 1e12,
                      "unit": "TFLOP/s", "frac": round(ig_tflops * 1e12 / PEAK_FP32_MFMA, 4),
                      "traffic": measured_traffic(a.batch, a.policy),
-                     "kernel": f"conv_igemm_kernel / conv_igemm_sk_kernel (implicit-GEMM conv, {n_ig} layers, "
+                     "kernel": f"conv_igemm_kernel / conv_igemm_sk_kernel / stem7_mfma_kernel (implicit-GEMM conv, {n_ig} layers, "
                                f"batch {a.batch})",
                      "launch_us": round(ig_live_ms / max(n_ig, 1) * 1e3, 2),
                      "achieved_node_events": round(ig_node_tflops, 3),
