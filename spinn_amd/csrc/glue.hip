@@ -1,5 +1,6 @@
 // glue.hip - bandwidth kernels around the conv/GEMM path: MaxPool2d,
 // mean reduction (ReduceMean / GlobalAveragePool) and a 32-bit fill.
+#include "mfma_core.h"
 #include "spinn_hip_internal.h"
 
 namespace spinn {
@@ -61,6 +62,115 @@ __global__ __launch_bounds__(256) void maxpool_plane_kernel(const float *__restr
     }
 }
 
+// Pools with a K/2 pad over 16-byte input rows and output rows of at most 256
+// pixels (3x3 stride 1 or 2, 5x5 stride 1: ResNet's stem pool, YOLO's SPPF):
+// one wave per (plane, run of bands of RB output rows), lanes over 4-pixel
+// quads of the row, each input row of a band one 16-byte load per lane (two at
+// stride 2), the K/2 neighbour columns from the adjacent lanes by a lane
+// permute. Taps outside the image read -inf, which never beats the running
+// maximum's start of -1e30: the same result as skipping them. Taps are taken
+// in the reference's (kh, kw) order with its `v > m` rule, so NaN is never
+// selected and the result is bit-identical to the per-output kernels above.
+template <int K, int S, int RB>
+__global__ __launch_bounds__(256) void maxpool_wave_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                           SpinnHipPoolDesc d, int owq, int bands, int bpw, int wpp,
+                                                           int waves) {
+    constexpr int HL = S == 1 ? K / 2 : 1;
+    constexpr int HR = S == 1 ? K / 2 : 0;
+    constexpr int NV = HL + 4 * S + HR;
+    constexpr int IR = (RB - 1) * S + K;
+    const float ninf = -__builtin_inff();
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t pl = wave / (uint32_t)wpp;
+    const int bg = (int)(wave - pl * (uint32_t)wpp);
+    const int bl = lane / owq, q = lane - bl * owq;
+    const int b = bg * bpw + bl;
+    const bool on = wave < (uint32_t)waves && bl < bpw && b < bands;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)(((int64_t)d.n * d.c) * d.h * d.w * 4));
+    const uint32_t plane_off = pl * (uint32_t)(d.h * d.w);
+    const int ih0 = b * RB * S - d.ph;
+    const int col0 = 4 * S * q;
+    const bool has_l = q > 0, has_r = q + 1 < owq;
+    const int addr_l = (lane - 1) << 2, addr_r = (lane + 1) << 2;
+    f32x4 f[IR][S];
+    bool rok[IR];
+#pragma unroll
+    for (int ir = 0; ir < IR; ++ir) {
+        const int ih = ih0 + ir;
+        rok[ir] = on && (unsigned)ih < (unsigned)d.h;
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+            const int col = col0 + 4 * u;
+            const bool ok = rok[ir] && col < d.w;
+            f[ir][u] = buf_f32x4(rx, ok ? (plane_off + (uint32_t)ih * d.w + col) * 4u : kOOB);
+            if (!ok) f[ir][u] = f32x4{ninf, ninf, ninf, ninf};
+        }
+    }
+    float m[RB][4];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m[r][j] = -1e30f;
+#pragma unroll
+    for (int ir = 0; ir < IR; ++ir) {
+        float v[NV];
+#pragma unroll
+        for (int u = 0; u < S; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[HL + 4 * u + e] = f[ir][u][e];
+#pragma unroll
+        for (int j = 0; j < HL; ++j) {
+            const float t =
+                __int_as_float(__builtin_amdgcn_ds_bpermute(addr_l, __float_as_int(f[ir][S - 1][4 - HL + j])));
+            v[j] = has_l ? t : ninf;
+        }
+#pragma unroll
+        for (int j = 0; j < HR; ++j) {
+            const float t = __int_as_float(__builtin_amdgcn_ds_bpermute(addr_r, __float_as_int(f[ir][0][j])));
+            v[HL + 4 * S + j] = has_r ? t : ninf;
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int kh = ir - r * S;
+            if (kh >= 0 && kh < K) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int kw = 0; kw < K; ++kw) {
+                        const float t = v[j * S + kw];
+                        m[r][j] = t > m[r][j] ? t : m[r][j];
+                    }
+            }
+        }
+    }
+    if (!on) return;
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        const int oh = b * RB + r;
+        if (oh >= d.oh) break;
+        const int ow0 = 4 * q;
+        const int64_t o = ((int64_t)pl * d.oh + oh) * d.ow + ow0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (ow0 + j < d.ow) y[o + j] = m[r][j];
+    }
+}
+
+template <int K, int S, int RB>
+static int launch_maxpool_wave(const SpinnHipPoolDesc *d, const float *x, float *y, hipStream_t st) {
+    const int owq = (d->ow + 3) / 4;
+    const int bands = (d->oh + RB - 1) / RB;
+    const int bpw = 64 / owq;
+    const int wpp = (bands + bpw - 1) / bpw;
+    const int64_t waves = (int64_t)d->n * d->c * wpp;
+    const int64_t blocks = (waves + 3) / 4;
+    if (blocks * 256 > INT32_MAX) return SPINN_HIP_EUNSUPPORTED;
+    hipLaunchKernelGGL((maxpool_wave_kernel<K, S, RB>), dim3((unsigned)blocks), dim3(256), 0, st, x, y, *d, owq,
+                       bands, bpw, wpp, (int)waves);
+    return check_launch();
+}
+
 // inner == 1: one wave per output, lanes stride the reduced axis, then a
 // wave-shuffle tree (SPINN/run_time/ops/reduce/reduce_mean.c:68-74).
 __global__ __launch_bounds__(256) void mean_rows_kernel(const float *__restrict__ x, float *__restrict__ y,
@@ -106,6 +216,12 @@ int maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, hipStream_t s
     const int64_t total = (int64_t)d->n * d->c * d->oh * d->ow;
     if (total == 0) return 0;
     const int64_t planes = (int64_t)d->n * d->c;
+    const bool wave_ok = d->kh == d->kw && d->sh == d->sw && d->ph == d->kh / 2 && d->pw == d->kw / 2 &&
+                         d->w % 4 == 0 && d->ow <= 256 && d->ow == (d->w + 2 * d->pw - d->kw) / d->sw + 1 &&
+                         d->oh == (d->h + 2 * d->ph - d->kh) / d->sh + 1 && (int64_t)planes * d->h * d->w * 4 <= (int64_t)kMaxOperandBytes;
+    if (wave_ok && d->kh == 3 && d->sh == 1) return launch_maxpool_wave<3, 1, 2>(d, x, y, st);
+    if (wave_ok && d->kh == 3 && d->sh == 2) return launch_maxpool_wave<3, 2, 1>(d, x, y, st);
+    if (wave_ok && d->kh == 5 && d->sh == 1) return launch_maxpool_wave<5, 1, 2>(d, x, y, st);
     if ((int64_t)d->h * d->w <= INT32_MAX && (int64_t)d->oh * d->ow <= INT32_MAX - 256 && planes <= INT32_MAX) {
         const dim3 grid((unsigned)((d->oh * d->ow + 255) / 256), (unsigned)std::min<int64_t>(planes, 65535));
         hipLaunchKernelGGL(maxpool_plane_kernel, grid, dim3(256), 0, st, x, y, *d, (int)planes);

@@ -175,7 +175,13 @@ def test_resize_and_sppf_pool(hip, torch_gpu):
     ((2, 4, 9, 11), 3, 1, 1),
     ((1, 2, 10, 9), 7, 3, 3),
     ((3, 2, 6, 7), 5, 1, 2),
-], ids=["r101-b32", "odd", "2x2", "3x3s1", "7x7s3", "5x5s1"])
+    ((16, 128, 20, 20), 5, 1, 2),   # YOLOv10n SPPF pool at batch 16 (band/quad kernel)
+    ((2, 3, 13, 12), 5, 1, 2),      # odd number of output rows per band pair
+    ((1, 2, 9, 256), 3, 1, 1),      # one band of 64 quads per wave
+    ((2, 3, 7, 12), 3, 2, 1),       # stride 2, last quad half past the row
+    ((1, 4, 11, 36), 3, 1, 1),      # 9 quads: 7 bands per wave, lanes 63 idle
+], ids=["r101-b32", "odd", "2x2", "3x3s1", "7x7s3", "5x5s1", "sppf-b16", "5x5-odd", "w256", "s2-w12",
+        "w36"])
 def test_maxpool_shapes(hip, torch_gpu, shape, k, s, p):
     """Bit-exact against the oracle, including NaN inputs (never selected: the reference keeps
     the running max unless val > max, SPINN/run_time/ops/pool/maxpool.c:36) and -inf."""
