@@ -188,6 +188,56 @@ __global__ __launch_bounds__(256) void mean_rows_kernel(const float *__restrict_
     }
 }
 
+// inner == 1 with rows of at most kMeanRowMax floats (GlobalAveragePool over a
+// 7x7 map): a one-wave workgroup stages 64 consecutive rows in LDS - one
+// contiguous run, moved with 16-byte loads all issued before the first LDS
+// store - then each lane sums its row in order from 0, as the reference's loop
+// does (SPINN/run_time/ops/reduce/reduce_mean.c:68-72), so the result is
+// bit-identical to it. Rows sit at an odd float stride in LDS (the row length
+// itself when odd, so the staging store needs no division; even rows get one
+// float of padding): the lanes read distinct banks.
+constexpr int kMeanRowMax = 63;
+constexpr int kMeanRows = 64;
+constexpr int kMeanVec = (kMeanRows * kMeanRowMax / 4 + 63) / 64; // 16-byte loads per lane, at most
+template <bool ODD> // ODD: stride == dim
+__global__ __launch_bounds__(64) void mean_rows_lds_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                           int64_t rows, int dim, int stride) {
+    __shared__ float rowbuf[kMeanRows * kMeanRowMax];
+    const int lane = threadIdx.x;
+    const int64_t r0 = (int64_t)blockIdx.x * kMeanRows;
+    const int nr = (int)min<int64_t>(kMeanRows, rows - r0);
+    const int n = nr * dim;
+    const float *xb = x + r0 * dim;
+    const int nv = n >> 2;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xb, (uint32_t)n * 4u);
+    f32x4 q[kMeanVec];
+#pragma unroll
+    for (int i = 0; i < kMeanVec; ++i) {
+        const int v = lane + 64 * i;
+        q[i] = buf_f32x4(rx, v < nv ? (uint32_t)v * 16u : kOOB);
+    }
+    const int et = 4 * nv + lane; // tail: n % 4 < 4 floats
+    const float t = et < n ? xb[et] : 0.f;
+#pragma unroll
+    for (int i = 0; i < kMeanVec; ++i) {
+        const int v = lane + 64 * i;
+        if (v < nv) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = 4 * v + u;
+                rowbuf[ODD ? e : e + e / dim] = q[i][u];
+            }
+        }
+    }
+    if (et < n) rowbuf[ODD ? et : et + et / dim] = t;
+    __syncthreads();
+    if (lane >= nr) return;
+    const float *rp = rowbuf + lane * stride;
+    float s = 0.f;
+    for (int j = 0; j < dim; ++j) s += rp[j];
+    y[r0 + lane] = s / (float)dim;
+}
+
 // inner > 1: one thread per (outer, inner), consecutive threads on inner.
 __global__ __launch_bounds__(256) void mean_strided_kernel(const float *__restrict__ x, float *__restrict__ y,
                                                            int64_t outer, int64_t dim, int64_t inner) {
@@ -233,6 +283,19 @@ int maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, hipStream_t s
 
 int reduce_mean(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, hipStream_t st) {
     if (outer * inner == 0) return 0;
+    if (inner == 1 && dim <= kMeanRowMax && ((uintptr_t)x & 15) == 0) {
+        const int stride = (int)dim | 1;
+        const int64_t blocks = (outer + kMeanRows - 1) / kMeanRows;
+        if (blocks <= INT32_MAX) {
+            if (dim & 1)
+                hipLaunchKernelGGL(mean_rows_lds_kernel<true>, dim3((unsigned)blocks), dim3(64), 0, st, x, y, outer,
+                                   (int)dim, stride);
+            else
+                hipLaunchKernelGGL(mean_rows_lds_kernel<false>, dim3((unsigned)blocks), dim3(64), 0, st, x, y, outer,
+                                   (int)dim, stride);
+            return check_launch();
+        }
+    }
     if (inner == 1) {
         hipLaunchKernelGGL(mean_rows_kernel, dim3(grid_for(outer * 64)), dim3(256), 0, st, x, y, outer, dim);
     } else {

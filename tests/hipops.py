@@ -187,6 +187,13 @@ def run_resize(N, torch, x, oh, ow):
     return _done(torch, yd)
 
 
+def run_reduce_mean(N, torch, x, outer, dim, inner, offset=0):
+    xd = _in(torch, x, offset)
+    yd = _out(torch, (outer * inner,))
+    N.check(N.lib().spinn_hip_reduce_mean(outer, dim, inner, _p(xd), _p(yd), None), "spinn_hip_reduce_mean")
+    return _done(torch, yd)
+
+
 def run_maxpool(N, torch, x, oh, ow, kh, kw, sh, sw, ph, pw):
     n, c, h, w = x.shape
     xd = _in(torch, x)

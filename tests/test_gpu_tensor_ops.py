@@ -10,8 +10,8 @@ import pytest
 
 from oracle import oracle as O
 from tests.conftest import assert_parity
-from tests.hipops import (run_batchnorm, run_binary, run_concat, run_maxpool, run_resize, run_softmax, run_split,
-                          run_transpose, run_unary)
+from tests.hipops import (run_batchnorm, run_binary, run_concat, run_maxpool, run_reduce_mean, run_resize, run_softmax,
+                          run_split, run_transpose, run_unary)
 from tests.test_oracle import _ROUNDED, _params_axis, _tensor_op_cases
 
 pytestmark = pytest.mark.gpu
@@ -194,6 +194,33 @@ def test_maxpool_shapes(hip, torch_gpu, shape, k, s, p):
     flat[5::89] = -np.inf
     np.testing.assert_array_equal(run_maxpool(hip, torch_gpu, x, oh, ow, k, k, s, s, p, p),
                                   O.maxpool(x, oh, ow, k, k, s, s, p, p))
+
+
+@pytest.mark.parametrize("outer,dim,inner,offset,exact", [
+    (32 * 2048, 49, 1, 0, True),  # ResNet-101 global average pool at batch 32 (7x7 map)
+    (2048, 49, 1, 0, True),       # batch 1
+    (300, 7, 1, 0, True),         # last block of 44 rows
+    (257, 62, 1, 0, True),        # even rows: padded LDS stride, one row in the last block
+    (5, 63, 1, 0, True),          # longest staged row
+    (9, 1, 1, 0, True),
+    (40, 64, 1, 0, False),        # one wave per row, shuffle-tree sum
+    (3, 1000, 1, 0, False),
+    (100, 49, 1, 1, False),       # input not 16-byte aligned: the wave kernel
+    (4, 9, 17, 0, True),          # inner > 1: one thread per output, sequential sum
+], ids=["gap-b32", "gap-b1", "ragged", "even", "d63", "d1", "wave64", "wave1000", "unaligned", "strided"])
+def test_reduce_mean(hip, torch_gpu, outer, dim, inner, offset, exact):
+    """The staged-row and strided kernels sum each row in the reference's order from 0
+    (SPINN/run_time/ops/reduce/reduce_mean.c:68-72): bit-exact. Rows longer than 63 floats
+    (or an unaligned input) take the wave kernel, whose shuffle tree reorders the additions:
+    within 1e-6 absolute on inputs in [-1, 1]."""
+    print(f"[tensor-op] reduce_mean outer={outer} dim={dim} inner={inner} offset={offset}", flush=True)
+    x = np.random.default_rng(outer + dim + inner).uniform(-1, 1, outer * dim * inner).astype(np.float32)
+    got = run_reduce_mean(hip, torch_gpu, x, outer, dim, inner, offset)
+    want = O.reduce_mean(x, outer, dim, inner)
+    if exact:
+        np.testing.assert_array_equal(got, want)
+    else:
+        np.testing.assert_allclose(got, want, rtol=0, atol=1e-6)
 
 
 def test_bad_arguments(hip, torch_gpu):
