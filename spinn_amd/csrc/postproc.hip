@@ -93,16 +93,209 @@ __device__ __forceinline__ uint32_t order_key(float v) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u); // larger float -> larger key
 }
 
+constexpr int kTopkWaves = kTopkThreads / 64;
+constexpr int kTopkBins = 257; // per-wave histograms, padded so equal bins of two waves sit in different banks
+
+// Radix-select state shared by the workgroup.
+struct TopkSel {
+    uint32_t whist[kTopkWaves * kTopkBins];
+    uint32_t hist[256];
+    uint32_t prefix, mask, need, gt, eq_base;
+    uint32_t wave_eq[kTopkWaves];
+};
+
+// Count this lane's element (when `match`) into its wave's histogram `wh`. When
+// every matching lane of the wave falls in one bin (the usual case for the
+// leading digit of scores in a narrow range) the wave adds its lane count with
+// one atomic instead of 64 serialised ones. The lead lane's bin is read with
+// readlane (the lane index is wave-uniform): no LDS round trip per element.
+__device__ __forceinline__ void topk_count(bool match, uint32_t bin, int lane, uint32_t *wh) {
+    const uint64_t act = __ballot(match);
+    if (act) {
+        const int lead = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)act) - 1);
+        const uint32_t lead_bin = (uint32_t)__builtin_amdgcn_readlane((int)bin, lead);
+        const uint64_t same = __ballot(match && bin == lead_bin);
+        if (same == act) {
+            if (lane == lead) atomicAdd(&wh[lead_bin], (uint32_t)__popcll(act));
+        } else if (match) {
+            atomicAdd(&wh[bin], 1u);
+        }
+    }
+}
+
+// After every element of the pass at `shift` is counted (a barrier behind the
+// counting): sum the wave histograms and fix the digit of the need-th largest
+// key. With above(b) the count of elements whose digit exceeds b, it is the one
+// digit b where above(b) < need <= above(b) + hist[b]; thread t < 256 holds bin
+// 255 - t, so above() is an exclusive prefix sum over t. Ends with a barrier.
+__device__ __forceinline__ void topk_pick_digit(TopkSel &sh, int shift, uint32_t prefix, uint32_t mask, int tid,
+                                                int lane, int wave) {
+    for (int b = tid; b < 256; b += kTopkThreads) {
+        uint32_t t = 0u;
+#pragma unroll
+        for (int w = 0; w < kTopkWaves; ++w) t += sh.whist[w * kTopkBins + b];
+        sh.hist[b] = t;
+    }
+    __syncthreads();
+    const uint32_t need = sh.need;
+    const int b = 255 - tid;
+    uint32_t v = 0u, incl = 0u;
+    if (tid < 256) {
+        v = sh.hist[b];
+        incl = v;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t o = (uint32_t)__shfl_up((int)incl, off);
+            if (lane >= off) incl += o;
+        }
+        if (lane == 63) sh.wave_eq[wave] = incl;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        for (int w = 0; w < wave; ++w) incl += sh.wave_eq[w];
+        const uint32_t above = incl - v;
+        if (above < need && above + v >= need) {
+            sh.need = need - above;
+            sh.prefix = prefix | ((uint32_t)b << shift);
+            sh.mask = mask | (255u << shift);
+        }
+    }
+    __syncthreads();
+}
+
+// Bitonic sort of cand[0, k) descending over the next power of two >= k (pads
+// sort last), then the row's values and indices in that order. A compare-exchange
+// stage with stride < 128 keeps every pair inside one 128-element block, which
+// one wave owns (64 pairs, one per lane): those stages need only the wave's own
+// ordering of its LDS accesses. Block-wide barriers surround only the stages of
+// stride >= 128 (5 of the 45 stages for k = 300).
+__device__ __forceinline__ void bitonic_pair(uint64_t *cand, int t, int stride, int size) {
+    const int i = ((t & ~(stride - 1)) << 1) | (t & (stride - 1)); // pair t: i has the stride bit clear
+    const int j = i + stride;
+    const bool desc = (i & size) == 0;
+    const uint64_t a = cand[i], b = cand[j];
+    if (desc ? (a < b) : (a > b)) {
+        cand[i] = b;
+        cand[j] = a;
+    }
+}
+
+__device__ __forceinline__ void topk_sort_store(uint64_t *cand, int k, int tid, const float *xr, float *values,
+                                                int64_t *indices) {
+    int p2 = 1;
+    while (p2 < k) p2 <<= 1;
+    for (int i = k + tid; i < p2; i += kTopkThreads) cand[i] = 0ull;
+    __syncthreads();
+    const int lane = tid & 63, wave = tid >> 6;
+    const bool in_wave = wave * 128 < p2 && 2 * lane < p2; // this lane's pair of its wave's block exists
+    for (int size = 2; size <= p2; size <<= 1) {
+        int stride = size >> 1;
+        if (stride >= 128) {
+            for (; stride >= 128; stride >>= 1) {
+                __syncthreads();
+                if (2 * tid < p2) bitonic_pair(cand, tid, stride, size);
+            }
+            __syncthreads();
+        }
+        for (; stride > 0; stride >>= 1) {
+            if (in_wave) bitonic_pair(cand, wave * 64 + lane, stride, size);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+    __syncthreads();
+    for (int j = tid; j < k; j += kTopkThreads) {
+        const uint32_t i = 0xffffffffu - (uint32_t)cand[j];
+        values[(int64_t)blockIdx.x * k + j] = xr[i];
+        indices[(int64_t)blockIdx.x * k + j] = (int64_t)i;
+    }
+}
+
+// Rows of at most R * 1024 elements: each thread loads its R keys (element
+// u * 1024 + tid) once, all loads in flight together, and every pass runs from
+// registers. The threshold-equal elements are ranked in index order from
+// per-(chunk, wave) counts with three barriers, instead of one block-wide count
+// per chunk. Same keys, threshold and sort as topk_rows_kernel: identical output.
+template <int R>
+__global__ __launch_bounds__(kTopkThreads) void topk_rows_reg_kernel(const float *__restrict__ x, int n, int k,
+                                                                     float *__restrict__ values,
+                                                                     int64_t *__restrict__ indices) {
+    __shared__ TopkSel sh;
+    __shared__ uint32_t ceq[R][kTopkWaves]; // threshold-equal elements per (chunk, wave)
+    __shared__ uint32_t cbase[R];           // ... in the chunks before this one
+    __shared__ uint64_t cand[SPINN_HIP_TOPK_MAX_K];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const float *xr = x + (int64_t)blockIdx.x * n;
+    uint32_t key[R];
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int i = u * kTopkThreads + tid;
+        key[u] = i < n ? order_key(xr[i]) : 0u;
+    }
+    if (tid == 0) {
+        sh.prefix = 0u;
+        sh.mask = 0u;
+        sh.need = (uint32_t)k;
+        sh.gt = 0u;
+    }
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int b = tid; b < kTopkWaves * kTopkBins; b += kTopkThreads) sh.whist[b] = 0u;
+        __syncthreads();
+        const uint32_t prefix = sh.prefix, mask = sh.mask;
+        uint32_t *wh = sh.whist + wave * kTopkBins;
+#pragma unroll
+        for (int u = 0; u < R; ++u)
+            if (u * kTopkThreads < n) // wave-uniform
+                topk_count(u * kTopkThreads + tid < n && (key[u] & mask) == prefix, (key[u] >> shift) & 255u, lane,
+                           wh);
+        __syncthreads();
+        topk_pick_digit(sh, shift, prefix, mask, tid, lane, wave);
+    }
+    const uint32_t thr = sh.prefix;   // key of the k-th largest element
+    const uint32_t take_eq = sh.need; // how many elements equal to it are kept: the lowest-index ones
+    const uint32_t n_gt = (uint32_t)k - take_eq;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int i = u * kTopkThreads + tid;
+        const bool valid = i < n;
+        if (valid && key[u] > thr) {
+            const uint32_t slot = atomicAdd(&sh.gt, 1u); // < n_gt by construction of thr
+            if (slot < n_gt) cand[slot] = ((uint64_t)key[u] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+        }
+        const uint64_t eqb = __ballot(valid && key[u] == thr);
+        if (lane == 0) ceq[u][wave] = (uint32_t)__popcll(eqb);
+    }
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t t = 0u;
+        for (int u = 0; u < R; ++u) {
+            cbase[u] = t;
+            for (int w = 0; w < kTopkWaves; ++w) t += ceq[u][w];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+        const int i = u * kTopkThreads + tid;
+        const bool eq = i < n && key[u] == thr;
+        const uint64_t eqb = __ballot(eq);
+        if (eq) {
+            uint32_t rank = cbase[u] + (uint32_t)__popcll(eqb & ((1ull << lane) - 1ull));
+            for (int w = 0; w < wave; ++w) rank += ceq[u][w];
+            if (rank < take_eq) cand[n_gt + rank] = ((uint64_t)key[u] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+        }
+    }
+    __syncthreads();
+    topk_sort_store(cand, k, tid, xr, values, indices);
+}
+
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__restrict__ x, int64_t n, int k,
                                                                  float *__restrict__ values,
                                                                  int64_t *__restrict__ indices) {
-    constexpr int kWaves = kTopkThreads / 64;
-    constexpr int kBins = 257; // per-wave histograms, padded so equal bins of two waves sit in different banks
-    __shared__ uint32_t whist[kWaves * kBins];
-    __shared__ uint32_t hist[256];
-    __shared__ uint32_t s_prefix, s_mask, s_need;
-    __shared__ uint32_t s_gt, s_eq_base;
-    __shared__ uint32_t s_wave_eq[kWaves];
+    __shared__ TopkSel sh;
     __shared__ uint64_t cand[SPINN_HIP_TOPK_MAX_K];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -118,19 +311,17 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     };
 
     if (tid == 0) {
-        s_prefix = 0u;
-        s_mask = 0u;
-        s_need = (uint32_t)k;
+        sh.prefix = 0u;
+        sh.mask = 0u;
+        sh.need = (uint32_t)k;
     }
-    // 1. radix select, most significant digit first. Each wave counts into its
-    // own histogram; when every counted lane of a wave falls in one bin (the
-    // usual case for the leading digit of scores in a narrow range) the wave adds
-    // its lane count with one atomic instead of 64 serialised ones.
+    // 1. radix select, most significant digit first, each wave counting into
+    // its own histogram.
     for (int shift = 24; shift >= 0; shift -= 8) {
-        for (int b = tid; b < kWaves * kBins; b += kTopkThreads) whist[b] = 0u;
+        for (int b = tid; b < kTopkWaves * kTopkBins; b += kTopkThreads) sh.whist[b] = 0u;
         __syncthreads();
-        const uint32_t prefix = s_prefix, mask = s_mask;
-        uint32_t *wh = whist + wave * kBins;
+        const uint32_t prefix = sh.prefix, mask = sh.mask;
+        uint32_t *wh = sh.whist + wave * kTopkBins;
         for (int64_t c0 = 0; c0 < nchunks; c0 += 4) {
             // four chunks' loads in flight before any is counted
             uint32_t kk[4];
@@ -138,64 +329,15 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
 #pragma unroll
             for (int u = 0; u < 4; ++u) kk[u] = key_at(c0 + u, vv[u]);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const uint32_t key = kk[u];
-                const bool match = vv[u] && (key & mask) == prefix;
-                const uint32_t bin = (key >> shift) & 255u;
-                const uint64_t act = __ballot(match);
-                if (act) {
-                    const int lead = __ffsll((unsigned long long)act) - 1;
-                    const uint32_t lead_bin = (uint32_t)__shfl((int)bin, lead);
-                    const uint64_t same = __ballot(match && bin == lead_bin);
-                    if (same == act) {
-                        if (lane == lead) atomicAdd(&wh[lead_bin], (uint32_t)__popcll(act));
-                    } else if (match) {
-                        atomicAdd(&wh[bin], 1u);
-                    }
-                }
-            }
+            for (int u = 0; u < 4; ++u) topk_count(vv[u] && (kk[u] & mask) == prefix, (kk[u] >> shift) & 255u, lane, wh);
         }
         __syncthreads();
-        for (int b = tid; b < 256; b += kTopkThreads) {
-            uint32_t t = 0u;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) t += whist[w * kBins + b];
-            hist[b] = t;
-        }
-        __syncthreads();
-        // digit selection, in parallel over the 256 bins: with above(b) the
-        // count of elements whose digit exceeds b, the k-th largest has the one
-        // digit b where above(b) < need <= above(b) + hist[b]. Thread t < 256
-        // holds bin 255 - t, so above() is an exclusive prefix sum over t.
-        const uint32_t need = s_need;
-        const int b = 255 - tid;
-        uint32_t v = 0u, incl = 0u;
-        if (tid < 256) {
-            v = hist[b];
-            incl = v;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t o = (uint32_t)__shfl_up((int)incl, off);
-                if (lane >= off) incl += o;
-            }
-            if (lane == 63) s_wave_eq[wave] = incl;
-        }
-        __syncthreads();
-        if (tid < 256) {
-            for (int w = 0; w < wave; ++w) incl += s_wave_eq[w];
-            const uint32_t above = incl - v;
-            if (above < need && above + v >= need) {
-                s_need = need - above;
-                s_prefix = prefix | ((uint32_t)b << shift);
-                s_mask = mask | (255u << shift);
-            }
-        }
-        __syncthreads();
+        topk_pick_digit(sh, shift, prefix, mask, tid, lane, wave);
     }
-    const uint32_t thr = s_prefix;     // key of the k-th largest element
-    const uint32_t take_eq = s_need;   // how many elements equal to it are kept
+    const uint32_t thr = sh.prefix;   // key of the k-th largest element
+    const uint32_t take_eq = sh.need; // how many elements equal to it are kept
     const uint32_t n_gt = (uint32_t)k - take_eq;
-    if (tid == 0) s_gt = 0u;
+    if (tid == 0) sh.gt = 0u;
 
     // 2. compaction. Slots only need to be distinct (step 3 orders by key and
     // index), so winners take slots with LDS atomics; what must follow index
@@ -203,7 +345,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     // take_eq. A block-wide count per chunk of 1024 elements tells whether a
     // chunk's equal elements are all in, all out, or (one chunk) split, and
     // only that chunk ranks its equal elements exactly.
-    if (tid == 0) s_eq_base = 0u;
+    if (tid == 0) sh.eq_base = 0u;
     __syncthreads();
     uint32_t cum = 0u; // equal elements in the chunks before this one (block-uniform)
     bool vnext;
@@ -218,18 +360,18 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
         const uint64_t packed = ((uint64_t)key << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
         const uint32_t cnt = (uint32_t)__syncthreads_count(eq);
         if (gt) {
-            const uint32_t slot = atomicAdd(&s_gt, 1u); // < n_gt by construction of thr
+            const uint32_t slot = atomicAdd(&sh.gt, 1u); // < n_gt by construction of thr
             if (slot < n_gt) cand[slot] = packed;
         }
         if (cum < take_eq) {
             if (cum + cnt <= take_eq) {
-                if (eq) cand[n_gt + atomicAdd(&s_eq_base, 1u)] = packed;
+                if (eq) cand[n_gt + atomicAdd(&sh.eq_base, 1u)] = packed;
             } else {
                 const uint64_t ball = __ballot(eq);
-                if (lane == 0) s_wave_eq[wave] = (uint32_t)__popcll(ball);
+                if (lane == 0) sh.wave_eq[wave] = (uint32_t)__popcll(ball);
                 __syncthreads();
                 uint32_t rank = cum + (uint32_t)__popcll(ball & ((1ull << lane) - 1ull));
-                for (int w = 0; w < wave; ++w) rank += s_wave_eq[w];
+                for (int w = 0; w < wave; ++w) rank += sh.wave_eq[w];
                 if (eq && rank < take_eq) cand[n_gt + rank] = packed;
             }
         }
@@ -237,32 +379,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     }
     __syncthreads();
 
-    // 3. bitonic sort, descending, over the next power of two >= k (pads sort last)
-    int p2 = 1;
-    while (p2 < k) p2 <<= 1;
-    for (int i = k + tid; i < p2; i += kTopkThreads) cand[i] = 0ull;
-    __syncthreads();
-    for (int size = 2; size <= p2; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < p2; i += kTopkThreads) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const bool desc = (i & size) == 0;
-                    const uint64_t a = cand[i], b = cand[j];
-                    if (desc ? (a < b) : (a > b)) {
-                        cand[i] = b;
-                        cand[j] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
-    for (int j = tid; j < k; j += kTopkThreads) {
-        const uint32_t i = 0xffffffffu - (uint32_t)cand[j];
-        values[(int64_t)blockIdx.x * k + j] = xr[i];
-        indices[(int64_t)blockIdx.x * k + j] = (int64_t)i;
-    }
+    // 3. bitonic sort, descending, and the output
+    topk_sort_store(cand, k, tid, xr, values, indices);
 }
 
 // ---------------------------------------------------------------------------
@@ -364,7 +482,15 @@ int reduce_max_rows(int64_t rows, int64_t block, const float *x, float *y, hipSt
 }
 
 int topk_rows(int64_t rows, int64_t n, int k, const float *x, float *values, int64_t *indices, hipStream_t st) {
-    hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, x, n, k, values, indices);
+    const dim3 grid((unsigned)rows), block(kTopkThreads);
+    if (n <= 8 * kTopkThreads)
+        hipLaunchKernelGGL(topk_rows_reg_kernel<8>, grid, block, 0, st, x, (int)n, k, values, indices);
+    else if (n <= 16 * kTopkThreads)
+        hipLaunchKernelGGL(topk_rows_reg_kernel<16>, grid, block, 0, st, x, (int)n, k, values, indices);
+    else if (n <= 32 * kTopkThreads)
+        hipLaunchKernelGGL(topk_rows_reg_kernel<32>, grid, block, 0, st, x, (int)n, k, values, indices);
+    else
+        hipLaunchKernelGGL(topk_rows_kernel, dim3((unsigned)rows), dim3(kTopkThreads), 0, st, x, n, k, values, indices);
     return check_launch();
 }
 

@@ -87,11 +87,14 @@ def test_postproc_matches_reference(hip, torch_gpu, case):
 
 @pytest.mark.parametrize("rows,n,k,grid", [(16, 8400, 300, 0.01), (2, 24000, 300, 0.05), (3, 1024, 1024, 0.25),
                                           (1, 97, 1, 0.0), (4, 5000, 700, 0.0), (1, 24000, 300, 0.5),
-                                          (3, 100003, 7, 0.001), (2, 9000, 1, 0.0)])
+                                          (3, 100003, 7, 0.001), (2, 9000, 1, 0.0), (2, 8192, 300, 0.01),
+                                          (1, 8193, 64, 0.01), (2, 16384, 300, 0.05), (1, 32768, 1024, 0.01),
+                                          (1, 32769, 300, 0.01)])
 def test_topk_detector_sizes(hip, torch_gpu, rows, n, k, grid):
     """Sizes of the detector tail (8400 anchors, 300 x 80 candidates, batch 16),
     k = n, k = 1 and k > 512, long rows, with values on a grid so ties are everywhere (a
-    0.5 grid leaves five distinct values)."""
+    0.5 grid leaves five distinct values); rows of 8, 16 and 32 chunks of 1024 and one
+    element past each (the register-resident kernels and the streaming one beyond)."""
     print(f"[topk] rows={rows} n={n} k={k}", flush=True)
     rng = np.random.default_rng(n + k)
     x = rng.uniform(-1, 1, (rows, n)).astype(np.float32)
