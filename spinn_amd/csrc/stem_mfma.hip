@@ -32,13 +32,14 @@ __host__ __device__ constexpr int stem_koff(int k) {
     return ((k / (kStemK * kStemK)) * kStemK + (k % (kStemK * kStemK)) / kStemK) * kStemPW + k % kStemK;
 }
 
-template <int C>
+template <int C, bool RES>
 __global__ __launch_bounds__(256) void stem7_mfma_kernel(const float *__restrict__ x, const float *__restrict__ wpk,
                                                          const float *__restrict__ bias, const float *__restrict__ res,
                                                          float *__restrict__ y, SpinnHipConvDesc d, int ldw) {
     constexpr int K = C * kStemK * kStemK;
     constexpr int STEPS = (K + 1) / 2; // lane group h supplies k = 2s + h
     __shared__ float patch[C * kStemK * kStemPW]; // [c][kh][col]
+    __shared__ float bsh[kStemOC];                // bias, 0 past OC or without one
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, l32 = lane & 31;
@@ -75,6 +76,7 @@ __global__ __launch_bounds__(256) void stem7_mfma_kernel(const float *__restrict
     const uint32_t a_lane0 = l32 < ldw ? (uint32_t)(h * ldw + l32) * 4u : kOOB;
     const uint32_t a_lane1 = l32 + 32 < ldw ? (uint32_t)(h * ldw + l32 + 32) * 4u : kOOB;
     const uint32_t a_step = (uint32_t)(2 * ldw) * 4u;
+    if (tid < kStemOC) bsh[tid] = (bias && tid < d.oc) ? bias[tid] : 0.f;
     __syncthreads();
     const int n = wave * 32 + l32;        // this lane's pixel of the row
     const float *pb = patch + kStemS * n; // B[k][n] = pb[stem_koff(k)]
@@ -93,22 +95,49 @@ __global__ __launch_bounds__(256) void stem7_mfma_kernel(const float *__restrict
         acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b, acc1, 0, 0, 0);
     }
     if (n >= d.ow) return;
+    // The bias comes from LDS and every residual load is issued before the first
+    // store: one wait per lane instead of a global round trip per output.
+    // (acc + bias) + residual, the epilogue's order.
     const int64_t ohw = (int64_t)d.oh * d.ow;
-    const int64_t pix = (int64_t)oh * d.ow + n;
+    const int64_t base = (int64_t)img * d.oc * ohw + (int64_t)oh * d.ow + n;
+    if constexpr (!RES) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m < d.oc) y[base + (int64_t)m * ohw] = apply_act((mb ? acc1[r] : acc0[r]) + bsh[m], d.act);
+            }
+        return;
+    }
+    float v[2][16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int mr = 8 * (r >> 2) + 4 * h + (r & 3);
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-            const int m = mb * 32 + mr;
-            if (m >= d.oc) continue;
-            const int64_t idx = ((int64_t)img * d.oc + m) * ohw + pix;
-            float v = mb ? acc1[r] : acc0[r];
-            if (bias) v += bias[m];
-            if (res) v += res[idx];
-            y[idx] = apply_act(v, d.act);
-        }
+        v[0][r] = acc0[r] + bsh[mr];
+        v[1][r] = acc1[r] + bsh[32 + mr];
     }
+    {
+        float rv[2][16];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                rv[mb][r] = m < d.oc ? res[base + (int64_t)m * ohw] : 0.f;
+            }
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v[mb][r] += rv[mb][r];
+    }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            if (m < d.oc) y[base + (int64_t)m * ohw] = apply_act(v[mb][r], d.act);
+        }
 }
 
 } // namespace
@@ -126,11 +155,20 @@ int stem_mfma_conv(const SpinnHipConvDesc *d, const float *x, const float *packe
     if (!packed) return SPINN_HIP_EINVAL;
     const int ldw = (d->oc + 3) / 4 * 4;
     const dim3 grid((unsigned)(d->n * d->oh));
-    switch (d->c) {
-    case 1: hipLaunchKernelGGL(stem7_mfma_kernel<1>, grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-    case 2: hipLaunchKernelGGL(stem7_mfma_kernel<2>, grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-    case 3: hipLaunchKernelGGL(stem7_mfma_kernel<3>, grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-    default: hipLaunchKernelGGL(stem7_mfma_kernel<4>, grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+    if (res) {
+        switch (d->c) {
+        case 1: hipLaunchKernelGGL((stem7_mfma_kernel<1, true>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+        case 2: hipLaunchKernelGGL((stem7_mfma_kernel<2, true>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+        case 3: hipLaunchKernelGGL((stem7_mfma_kernel<3, true>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+        default: hipLaunchKernelGGL((stem7_mfma_kernel<4, true>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+        }
+    } else {
+        switch (d->c) {
+        case 1: hipLaunchKernelGGL((stem7_mfma_kernel<1, false>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+        case 2: hipLaunchKernelGGL((stem7_mfma_kernel<2, false>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+        case 3: hipLaunchKernelGGL((stem7_mfma_kernel<3, false>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+        default: hipLaunchKernelGGL((stem7_mfma_kernel<4, false>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
+        }
     }
     return check_launch();
 }
