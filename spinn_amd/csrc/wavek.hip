@@ -319,8 +319,26 @@ __device__ __forceinline__ void wk_range(int K, int kq, int wave, int &kb, int &
     ke = min(K, kb + kq);
 }
 
+// Outputs of the tile per thread in the cross-wave sum: output i of a thread is
+// element e = threadIdx.x + 64 KG i (e < TS * TS) of the wave-order layout.
+template <int TS, int KG>
+constexpr int wk_outs() { return (TS * TS + 64 * KG - 1) / (64 * KG); }
+
+// Call `f(i, m_local, n_local)` for each output i of this thread.
+template <int TS, int KG, class F>
+__device__ __forceinline__ void wk_for_outputs(const F &f) {
+#pragma unroll
+    for (int i = 0; i < wk_outs<TS, KG>(); ++i) {
+        const int e = threadIdx.x + 64 * KG * i;
+        if (e < TS * TS) f(i, WkShape<TS>::row(e >> 6, e & 63), WkShape<TS>::col(e & 63));
+    }
+}
+
 // Sum the KG partial tiles in wave order and hand each output (m, n) to
-// `store(m_local, n_local, v)`; consecutive threads take consecutive columns.
+// `store(i, m_local, n_local, v)`; consecutive threads take consecutive columns.
+// The kernels load what the epilogue adds (bias, residual, C) for the same
+// outputs i before their K loop, so those loads are in flight during it
+// instead of one round trip per output after the sum.
 template <int TS, int KG, class Store>
 __device__ __forceinline__ void wk_reduce_store(const typename WkShape<TS>::Acc &acc,
                                                 float (*red)[WkShape<TS>::kAcc][64], const Store &store) {
@@ -329,13 +347,16 @@ __device__ __forceinline__ void wk_reduce_store(const typename WkShape<TS>::Acc 
 #pragma unroll
     for (int r = 0; r < WkShape<TS>::kAcc; ++r) red[wave][r][lane] = acc[r];
     __syncthreads();
-    for (int e = threadIdx.x; e < TS * TS; e += 64 * KG) {
+#pragma unroll
+    for (int i = 0; i < wk_outs<TS, KG>(); ++i) {
+        const int e = threadIdx.x + 64 * KG * i;
+        if (e >= TS * TS) break;
         const int r = e >> 6;
         const int l = e & 63;
         float v = 0.f;
 #pragma unroll
         for (int w = 0; w < KG; ++w) v += red[w][r][l];
-        store(WkShape<TS>::row(r, l), WkShape<TS>::col(l), v);
+        store(i, WkShape<TS>::row(r, l), WkShape<TS>::col(l), v);
     }
 }
 
@@ -382,20 +403,32 @@ __global__ __launch_bounds__(64 * KG) void wavek_conv_kernel(WkConvArgs a) {
     BF bf;
     bf.init(a.geom, n0 + S::col(lane), group, ke);
     if constexpr (std::is_same<BF, WkTap>::value) bf.start(kb, S::kBlock, h);
-    typename S::Acc acc;
-    wk_accumulate<TS, NB>(af, bf, kb, ke, h, acc);
+    // output index, bias and residual of each of this thread's outputs (idx < 0: outside the
+    // problem; y is at most 2 GiB, so an element index fits 32 bits)
     const int ntot = a.geom.ntot;
-    wk_reduce_store<TS, KG>(acc, red, [&](int ml, int nl, float v) {
+    constexpr int NO = wk_outs<TS, KG>();
+    int oidx[NO];
+    float ob[NO], orr[NO];
+    wk_for_outputs<TS, KG>([&](int i, int ml, int nl) {
         const int m = m0 + ml, n = n0 + nl;
+        oidx[i] = -1;
+        ob[i] = orr[i] = 0.f;
         if (m >= a.M || n >= ntot) return;
         const int img = n / a.OHW;
         const int p = n - img * a.OHW;
         const int oc = group * a.M + m;
-        const int64_t idx = ((int64_t)img * a.OC + oc) * a.OHW + p;
+        oidx[i] = (int)(((int64_t)img * a.OC + oc) * a.OHW + p);
+        if (a.bias) ob[i] = a.bias[oc];
+        if (a.res) orr[i] = a.res[oidx[i]];
+    });
+    typename S::Acc acc;
+    wk_accumulate<TS, NB>(af, bf, kb, ke, h, acc);
+    wk_reduce_store<TS, KG>(acc, red, [&](int i, int, int, float v) {
+        if (oidx[i] < 0) return;
         // the reference's order: acc + bias, then + residual (gemm_kernel.c:316-338)
-        if (a.bias) v += a.bias[oc];
-        if (a.res) v += a.res[idx];
-        a.y[idx] = apply_act(v, a.act);
+        if (a.bias) v += ob[i];
+        if (a.res) v += orr[i];
+        a.y[oidx[i]] = apply_act(v, a.act);
     });
 }
 
@@ -439,14 +472,23 @@ __global__ __launch_bounds__(64 * KG) void wavek_gemm_kernel(WkGemmArgs a) {
         bf.init(bbase, (uint32_t)(a.K * a.ldb * 4), (uint32_t)a.ldb, n0 + S::col(lane), a.N, ke);
     else
         bf.init(bbase, (uint32_t)(a.N * a.ldb * 4), (uint32_t)a.ldb, n0 + S::col(lane), a.N, ke);
+    // C value of each of this thread's outputs, loaded before the K loop
+    constexpr int NO = wk_outs<TS, KG>();
+    float oc_[NO];
+    wk_for_outputs<TS, KG>([&](int i, int ml, int nl) {
+        const int m = m0 + ml, n = n0 + nl;
+        oc_[i] = 0.f;
+        if (m >= a.M || n >= a.N) return;
+        if (a.c_mode == 1) oc_[i] = a.c[n];
+        else if (a.c_mode == 2) oc_[i] = a.c[(int64_t)m * a.N + n];
+    });
     typename S::Acc acc;
     wk_accumulate<TS, NB>(af, bf, kb, ke, h, acc);
-    wk_reduce_store<TS, KG>(acc, red, [&](int ml, int nl, float v) {
+    wk_reduce_store<TS, KG>(acc, red, [&](int i, int ml, int nl, float v) {
         const int m = m0 + ml, n = n0 + nl;
         if (m >= a.M || n >= a.N) return;
         v *= a.alpha;
-        if (a.c_mode == 1) v += a.beta * a.c[n];
-        else if (a.c_mode == 2) v += a.beta * a.c[(int64_t)m * a.N + n];
+        if (a.c_mode == 1 || a.c_mode == 2) v += a.beta * oc_[i];
         a.y[batch * a.stride_y + (int64_t)m * a.N + n] = v;
     });
 }
