@@ -70,14 +70,16 @@ int spinn_hip_conv(const SpinnHipConvDesc *d, const float *x, const float *w, co
  * SPINN_HIP_NOALLOC_SCRATCH_BYTES held by the library. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc), and
- * it calls no allocating routine. The caller still passes inputs (including
+ * once spinn_hip_init has run for its device it calls no allocating routine.
+ * The caller still passes inputs (including
  * packed_w from spinn_hip_conv_pack_weights) and the output; results are those
  * of spinn_hip_conv. A descriptor whose spinn_hip_conv_workspace_size exceeds
  * the array returns SPINN_HIP_EWORKSPACE without launching. Every call on one
  * GPU shares that GPU's array: calls that overlap on one GPU (other streams,
- * other host threads) race. Nothing in the array needs to start at zero. The
- * array's device address is resolved by spinn_hip_init for its device, else by
- * the first call on a device.
+ * other host threads) race. Nothing in the array needs to start at zero.
+ * spinn_hip_init resolves the array's device address and runs the
+ * once-per-device XCD placement check the stream-K plan reads (a 16 KB
+ * allocation, freed); without it the first call on a device does both.
  */
 #define SPINN_HIP_NOALLOC_SCRATCH_BYTES (128u << 20) /* every conv of ResNet-101 b32, VGG b8, YOLOv10n b16 */
 int spinn_hip_conv_noalloc(const SpinnHipConvDesc *d, const float *x, const float *w, const float *packed_w,
