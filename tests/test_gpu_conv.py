@@ -39,10 +39,10 @@ CASES = [
     ("stem7x7_c1_oc40_ragged", 3, 1, 37, 45, 40, 7, 2, 3, 1, 3, 0),   # one channel, 40 of 64 rows, 23-pixel rows
     ("stem7x7_c4_ow128", 1, 4, 30, 256, 64, 7, 2, 3, 1, 1, 0),         # four channels, 128-pixel rows
     ("stem7x7_ow129_fallback", 1, 3, 9, 258, 64, 7, 2, 3, 1, 1, 0),    # 129-pixel rows: generic implicit GEMM
-    # weight-stationary persistent stem (at least two rows per resident workgroup)
-    ("stem7x7_ws_224_b8", 8, 3, 224, 224, 64, 7, 2, 3, 1, 1, 0),       # 896 rows: 3 or 4 per workgroup
-    ("stem7x7_ws_c2_res_ragged", 24, 2, 48, 90, 48, 7, 2, 3, 1, 5, 0), # 576 rows of 45 pixels, 48 channels
-    ("stem7x7_ws_c1_oc40", 34, 1, 64, 64, 40, 7, 2, 3, 1, 3, 0),       # 1088 rows of 32 pixels, SiLU
+    # stem epilogue: bias from LDS, residual loads batched (no-residual and residual variants)
+    ("stem7x7_224_b8", 8, 3, 224, 224, 64, 7, 2, 3, 1, 1, 0),          # 896 rows
+    ("stem7x7_c2_res_ragged", 24, 2, 48, 90, 48, 7, 2, 3, 1, 5, 0),    # 576 rows of 45 pixels, 48 channels
+    ("stem7x7_c1_oc40_silu", 34, 1, 64, 64, 40, 7, 2, 3, 1, 3, 0),     # 1088 rows of 32 pixels, SiLU
     ("stem_c1_direct_oc20_res", 1, 1, 33, 35, 20, 3, 1, 1, 1, 5, 3),  # partial 16-channel chunk, residual
     ("direct_group1_general", 1, 6, 10, 12, 5, 3, 1, 1, 1, 1, 3),      # C > 4: general direct kernel
     ("conv3x3_s2", 2, 128, 28, 28, 128, 3, 2, 1, 1, 1, 0),
