@@ -494,6 +494,61 @@ def small_launches(reps: int = 20) -> None:
     print("[bench] small-config launches done", flush=True)
 
 
+def clock_probe(reps: int = 200) -> None:
+    """Launches for a clock comparison under rocprofv3 --pmc GRBM_GUI_ACTIVE GRBM_COUNT
+    --kernel-trace: the 1024 -> 256 1x1 conv at 14x14, batch 32 (implicit GEMM), `reps`
+    times on zero-filled operands, then `reps` times on random ones. Cycles per
+    dispatch over the dispatch's duration compare the clock the chip holds on each."""
+    import ctypes as C
+    from spinn_amd import native as N
+    from spinn_amd.devbuf import DeviceBuffer
+    L = N.lib()
+    N.check(L.spinn_hip_init(0), "spinn_hip_init")
+    n, c, hw, oc = 32, 1024, 14, 256
+    d = N.ConvDesc(n, c, hw, hw, oc, hw, hw, 1, 1, 1, 1, 0, 0, 1, 1, N.ALGO_IMPLICIT_GEMM, 0)
+    bufs = [DeviceBuffer(4 * v) for v in (n * c * hw * hw, oc * c, oc, n * oc * hw * hw)]
+    bx, bw, bb, by = bufs
+    bp = DeviceBuffer(L.spinn_hip_conv_packed_size(C.byref(d)))
+    wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
+    ws = DeviceBuffer(wsz) if wsz else None
+    for label in ("zeros", "random"):
+        for i, b_ in enumerate(bufs):
+            if label == "zeros":
+                N.check(L.spinn_hip_fill_u32(b_.ptr, 0, b_.nbytes, None), "fill")
+            else:
+                fill_random(b_, seed=5 + i, scale=0.05 if i == 1 else 1.0)
+        N.check(L.spinn_hip_conv_pack_weights(C.byref(d), bw.ptr, bp.ptr, None), "pack")
+        N.check(L.spinn_hip_stream_sync(None), "sync")
+        print(f"[bench] clock probe: {reps} launches on {label} operands", flush=True)
+        for _ in range(reps):
+            N.check(L.spinn_hip_conv(C.byref(d), bx.ptr, bw.ptr, bp.ptr, bb.ptr, None, by.ptr,
+                                     ws.ptr if ws else None, wsz, None), "conv")
+        N.check(L.spinn_hip_stream_sync(None), "sync")
+    for b_ in bufs + [bp] + ([ws] if ws else []):
+        b_.free()
+
+
+def clock_summary(d: Path) -> str:
+    """Per-dispatch GRBM_COUNT cycles and kernel-trace durations of a --clock-probe run
+    (the first 20 launches of each half dropped)."""
+    import csv
+    cc = list(csv.DictReader(open(next(d.glob("*_counter_collection.csv")))))
+    kt = list(csv.DictReader(open(next(d.glob("*_kernel_trace.csv")))))
+    dur = {r["Dispatch_Id"]: (int(r["End_Timestamp"]) - int(r["Start_Timestamp"]), r["Kernel_Name"]) for r in kt}
+    cyc = {}
+    for r in cc:
+        if r["Counter_Name"] == "GRBM_COUNT":
+            cyc[r["Dispatch_Id"]] = float(r["Counter_Value"])
+    rows = sorted((int(k), dur[k][0], v) for k, v in cyc.items() if k in dur and "conv_igemm" in dur[k][1])
+    half = len(rows) // 2
+    lines = ["| operands | dispatches | mean duration us | mean GRBM_COUNT cycles | cycles / ns |", "|---|---|---|---|---|"]
+    for name, part in (("zeros", rows[:half][20:]), ("random", rows[half:][20:])):
+        du = sum(p[1] for p in part) / len(part)
+        cy = sum(p[2] for p in part) / len(part)
+        lines.append(f"| {name} | {len(part)} | {du / 1e3:.2f} | {cy:.0f} | {cy / du:.3f} |")
+    return "\n".join(lines) + "\n"
+
+
 COMPARE_LAYERS = [  # (n, c, h, w, oc, k, stride, pad, act): ResNet-101 batch-32 layers
     (32, 256, 14, 14, 1024, 1, 1, 0, 5),
     (32, 1024, 14, 14, 256, 1, 1, 0, 1),
@@ -970,6 +1025,10 @@ def main() -> int:
     ap.add_argument("--small-launches", action="store_true",
                     help="only launch the config-0 conv, the Gemm sweep and the YOLOv10n b16 depthwise layers "
                          "20x each (for rocprofv3 --kernel-trace --stats)")
+    ap.add_argument("--clock-probe", action="store_true",
+                    help="one conv launched 200x on zero then on random operands (run under rocprofv3 --pmc "
+                         "GRBM_GUI_ACTIVE GRBM_COUNT --kernel-trace)")
+    ap.add_argument("--clock-summary", metavar="DIR", help="table of a --clock-probe run's counters (no GPU)")
     ap.add_argument("--calibration-kernels", action="store_true",
                     help="only run the known-size fill/copy kernels that scale the HBM byte counters")
     ap.add_argument("--traffic-summary", metavar="DIR",
@@ -986,6 +1045,12 @@ def main() -> int:
         print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
               "(the path shards by batch with no collective; see DESIGN.md)", file=sys.stderr)
         return 2
+    if a.clock_summary:
+        print(clock_summary(Path(a.clock_summary)), end="")
+        return 0
+    if a.clock_probe:
+        clock_probe()
+        return 0
     if a.calibration_kernels:
         calibration_kernels()
         return 0
