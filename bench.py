@@ -5,8 +5,9 @@
 
 A step is one forward pass of ResNet-101 (batch 32, 224x224, random-init with
 BN folded) through spinn_run over a single HBM arena, with the input already
-resident in HBM (spinn_run_resident; the node loop is replayed from a HIP
-graph). Prints ONE JSON line:
+in HBM (spinn_run_resident: each step copies the staged input into its arena
+region device to device, as the reference's spinn_run copies its host input on
+every call, then replays the node loop from a HIP graph). Prints ONE JSON line:
 
   value             images/s at batch 32 (whole job = the one GPU)
   images_per_s_b1   images/s at batch 1 (same protocol)
@@ -271,14 +272,16 @@ def suite(N, Session, models, reps: int = 100, yolo_cpu: dict | None = None) -> 
     outs = {}
     for name, pol in (("implicit_gemm", N.POLICY_IGEMM), ("winograd", N.POLICY_WINOGRAD)):
         with Session(pv, policy=pol, graph=True) as sv:
+            yv = sv.run(xv)
             sv.upload_input(xv)
-            msv = time_steps(sv, max(10, reps // 10), 3)
-            outs[name] = sv.download(sv.output_id)
+            msv = time_steps(sv, max(10, reps // 10), 3, ref=yv)
+            outs[name] = yv
         res[name] = {"ms": round(msv, 4), "images_per_s": round(8 / (msv * 1e-3), 1),
                      "tflops_direct_equiv": round(vgg_flops / (msv * 1e-3) / 1e12, 2)}
     dv = outs["winograd"].astype(np.float64) - outs["implicit_gemm"]
     res["winograd_vs_igemm_rel_l2"] = float(np.linalg.norm(dv) / np.linalg.norm(outs["implicit_gemm"]))
     res["winograd_vs_igemm_max_abs"] = float(np.abs(dv).max())
+    res["output_max_abs"] = float(np.abs(outs["implicit_gemm"]).max())
     res["gflop_direct_equiv"] = round(vgg_flops / 1e9, 2)
     out["vgg3x3_stack_b8"] = res
     out["yolov10n"] = yolo_bench(N, Session, models, tmp, reps)
@@ -369,8 +372,9 @@ def yolo_bench(N, Session, models, tmp: Path, reps: int) -> dict:
         g, x = models.yolov10n(batch=b, seed=0, postprocess=True)
         path = g.write(tmp / f"y10_b{b}.ennf")
         with Session(path, graph=True) as s:
+            yh = s.run(x)
             s.upload_input(x)
-            ms = time_steps(s, max(20, reps // 2) if b == 1 else max(10, reps // 10), 3)
+            ms = time_steps(s, max(20, reps // 2) if b == 1 else max(10, reps // 10), 3, ref=yh)
         gf = sum(f for _, f in models.conv_flops(g))
         ent = {"ms": round(ms, 4), "images_per_s": round(b / (ms * 1e-3), 1),
                "conv_tflops_direct_equiv": round(gf / (ms * 1e-3) / 1e12, 2), "conv_gflop": round(gf / 1e9, 3)}
@@ -993,13 +997,30 @@ def engine_scan(reps: int = 10) -> None:
         b_.free()
 
 
-def time_steps(sess, steps: int, warmup: int) -> float:
+class StepMismatch(RuntimeError):
+    pass
+
+
+def time_steps(sess, steps: int, warmup: int, ref: np.ndarray | None = None) -> float:
+    """Mean wall time of one resident step (ms). Every step restores input 0 into its
+    arena region from the staged device copy (spinn_run_resident) and runs the node
+    loop. The output of the first step (and `ref`, the host-copy path's output for
+    the same input, when given) must equal the output after the timed steps bit for
+    bit, so every timed step computed the stated input."""
+    sess.run_resident()
+    first = sess.download(sess.output_id)
+    if ref is not None and not np.array_equal(first.view(np.uint32), np.asarray(ref).view(np.uint32)):
+        raise StepMismatch("resident step output differs from spinn_run with host copies")
     for _ in range(warmup):
         sess.run_resident()
     t0 = time.perf_counter()
     for _ in range(steps):
         sess.run_resident()  # returns after the runtime's stream is idle
-    return (time.perf_counter() - t0) / steps * 1e3
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    last = sess.download(sess.output_id)
+    if not np.array_equal(first.view(np.uint32), last.view(np.uint32)):
+        raise StepMismatch("output after the timed steps differs from the first step's")
+    return ms
 
 
 def main() -> int:
@@ -1139,8 +1160,9 @@ def main() -> int:
 
     # ---- batch B, graph replay, input resident ----
     sB = Session(pB, policy=policy, graph=not a.no_graph)
+    yB_host = sB.run(xB)  # host in, host out: the reference's spinn_run protocol
     sB.upload_input(xB)
-    ms_B = time_steps(sB, a.steps, a.warmup)
+    ms_B = time_steps(sB, a.steps, a.warmup, ref=yB_host)
     print(f"[bench] b{a.batch}: {ms_B:.3f} ms/step", file=sys.stderr, flush=True)
     # PCIe-inclusive rate (host input in, logits out) for reference
     t0 = time.perf_counter()
@@ -1154,8 +1176,9 @@ def main() -> int:
 
     # ---- batch 1 ----
     s1 = Session(p1, policy=policy, graph=not a.no_graph)
+    y1_host = s1.run(x1)
     s1.upload_input(x1)
-    ms_1 = time_steps(s1, max(a.steps, 50), a.warmup)
+    ms_1 = time_steps(s1, max(a.steps, 50), a.warmup, ref=y1_host)
     s1.close()
     print(f"[bench] b1: {ms_1:.3f} ms/step", file=sys.stderr, flush=True)
 
@@ -1218,9 +1241,12 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded random-init ResNet-101, BN folded; input U[-1,1])",
         "config": {"workload": f"ResNet-101 v1.5 fp32 forward, batch {a.batch}, 3x224x224, ENNF through "
-                               f"spinn_run over one HBM arena, input resident, "
+                               f"spinn_run over one HBM arena, input staged in HBM and copied into the arena "
+                               f"each step (device to device, counted in the step), "
                                f"{'per-node launches' if a.no_graph else 'HIP-graph replay'}",
                    "batch": a.batch, "image": [3, 224, 224], "conv_layers": len(rows), "conv_policy": a.policy},
+        "step_check": "each timed loop's output after its last step equals its first step's and spinn_run's "
+                      "with host copies, bit for bit (b32, b1, VGG and YOLOv10n loops)",
         "images_per_s_b1": round(1e3 / ms_1, 2),
         "ms_per_step_b1": round(ms_1, 4),
         "images_per_s_with_host_copies": round(a.batch / (ms_B_h2d * 1e-3), 2),

@@ -24,6 +24,7 @@ extern "C" {
 #define SPINN_HIP_EINVAL (-1)      /* bad arity / shape / argument (reference ops return -1) */
 #define SPINN_HIP_EUNSUPPORTED (-2) /* valid request this layer does not implement */
 #define SPINN_HIP_EWORKSPACE (-3)   /* workspace missing or too small */
+#define SPINN_HIP_EDEVICE (-4)      /* a kernel reported an internal failure (spinn_hip_device_status) */
 #define SPINN_HIP_ERUNTIME (-100)   /* HIP runtime error: code = -100 - hipError_t */
 
 /* Convolution algorithms. AUTO picks per shape (see spinn_hip_conv_select_algo). */
@@ -290,6 +291,21 @@ void spinn_hip_tune_force_tiles(int bm, int bn, int split);
  * even where spinn_hip_init found them sharing an L2. Change it only between
  * plans: workspace sizes depend on it. No counterpart in the reference. */
 void spinn_hip_tune_streamk(int mode);
+
+/* Test hook: arrival rounds of the stream-K parts (default 4; < 0 restores
+ * it). 0 makes every arrival fail, so the cut tiles stay unwritten and the
+ * status word reports it, while every kernel still exits normally. No
+ * counterpart in the reference. */
+void spinn_hip_tune_streamk_tries(int tries);
+
+/* Device-side failure report: SPINN_HIP_EDEVICE when a kernel launched since
+ * the last call could not finish its work (a stream-K tile whose parts' arrival
+ * protocol broke, leaving the tile unwritten), else 0; clears the report. Call
+ * after synchronising the streams the launches ran on; spinn_run does. The
+ * word is host memory the kernels write, allocated by spinn_hip_init or the
+ * first workspace query of a stream-K conv. No counterpart in the reference
+ * (its operators run on the calling thread and return their errors). */
+int spinn_hip_device_status(void);
 
 /* Library version / build identification string. */
 const char *spinn_hip_version(void);

@@ -92,6 +92,8 @@ typedef struct {
     int use_graph;
     void *prof_state;        /* per-node HIP events and times when SPINN_PROFILE=1 */
     int conv_policy;         /* SPINN_CONV_POLICY_* fixed at plan time */
+    void *input_stage;       /* device copy of input 0 that spinn_run_resident restores from */
+    int input_staged;        /* 1 once spinn_stage_input has filled input_stage */
 } SpinnContext;
 
 /* Which algorithm eligible 3x3 stride-1 convolutions use (spinn_set_conv_policy). */
@@ -128,9 +130,25 @@ int spinn_plan_memory(SpinnContext *ctx, uint32_t max_arena_bytes);
 int spinn_tensor_upload(SpinnContext *ctx, uint16_t tensor_id, const void *host, size_t bytes);
 int spinn_tensor_download(SpinnContext *ctx, uint16_t tensor_id, void *host, size_t bytes);
 
-/* Run the node loop with inputs already resident in the arena and leave the
- * outputs there; returns after the stream is idle. Equivalent to
- * spinn_run(ctx, NULL, NULL). */
+/* Copy input 0 from the host into the context's device staging buffer (a
+ * separate allocation made by spinn_plan, outside the arena); synchronous.
+ * The staged copy stays untouched by the node loop. */
+int spinn_stage_input(SpinnContext *ctx, const void *host, size_t bytes);
+
+/* Device address of the staging buffer (NULL before spinn_plan), for callers
+ * that produce input 0 on the device themselves; after writing it they call
+ * spinn_stage_input(ctx, NULL, 0) to mark it filled. */
+void *spinn_input_stage_ptr(SpinnContext *ctx);
+
+/* One step with the input resident in HBM: copy the staged input 0 into its
+ * arena region (device to device, on the runtime's stream), run the node loop
+ * and leave the outputs in the arena; returns after the stream is idle.
+ * The copy is what the reference's spinn_run does with its host input on
+ * every call (SPINN/run_time/spinn_runtime.c:302-306): the planner hands the
+ * input's arena region to later activations once its last consumer has run,
+ * so a run that skips it computes on the previous run's activations.
+ * Returns -1 when nothing has been staged. spinn_run(ctx, NULL, NULL) keeps
+ * the reference's meaning (no copy at all). */
 int spinn_run_resident(SpinnContext *ctx);
 
 /* Capture the node loop into a HIP graph and replay it on later runs (1) or

@@ -343,8 +343,11 @@ int spinn_hip_init(int device) {
     rc = noalloc_scratch(device, &scratch);
     if (rc) return rc;
     probe_xcd_local(device);
+    init_device_status();
     return SPINN_HIP_OK;
 }
+
+int spinn_hip_device_status(void) { return take_device_status() ? SPINN_HIP_EDEVICE : SPINN_HIP_OK; }
 
 int spinn_hip_device_count(int *count) {
     if (!count) return SPINN_HIP_EINVAL;
@@ -450,6 +453,7 @@ const char *spinn_hip_error_string(int code) {
     if (code == SPINN_HIP_EINVAL) return "invalid argument";
     if (code == SPINN_HIP_EUNSUPPORTED) return "unsupported configuration";
     if (code == SPINN_HIP_EWORKSPACE) return "workspace missing or too small";
+    if (code == SPINN_HIP_EDEVICE) return "a kernel reported an internal failure (stream-K tile left unfinished)";
     if (code <= SPINN_HIP_ERUNTIME) return hipGetErrorString((hipError_t)(SPINN_HIP_ERUNTIME - code));
     return "unknown error";
 }
@@ -457,6 +461,8 @@ const char *spinn_hip_error_string(int code) {
 void spinn_hip_tune_force_tiles(int bm, int bn, int split) { force_tiles(bm, bn, split); }
 
 void spinn_hip_tune_streamk(int mode) { force_streamk(mode); }
+
+void spinn_hip_tune_streamk_tries(int tries) { force_streamk_tries(tries); }
 
 const char *spinn_hip_version(void) { return "spinn_amd 0.1 gfx950 fp32-mfma"; }
 

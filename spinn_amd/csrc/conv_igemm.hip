@@ -385,6 +385,8 @@ int launch_conv_sk_tile(const ConvKArgs &a, const SkPlan &sp, int S, void *ws, h
     s.epoch = streamk_epoch();
     s.cnt = (unsigned long long *)ws;
     s.part = (float *)((char *)ws + sp.cnt_bytes);
+    s.status = device_status_word();
+    s.tries = streamk_tries();
     const dim3 grid(sp.grid);
     if (sp.scheme == kSkSplitWgs) {
         if (act_class(a.act) == 1)
@@ -520,6 +522,7 @@ size_t igemm_workspace_bytes(const SpinnHipConvDesc *d) {
         // plan time: settle how the parts exchange sums on this device
         int dev = 0;
         if (hipGetDevice(&dev) == hipSuccess) probe_xcd_local(dev);
+        init_device_status();
         return sp.ws_bytes;
     }
     if (tc.split <= 1) return 0;

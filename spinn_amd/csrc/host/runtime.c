@@ -276,6 +276,12 @@ int spinn_plan(SpinnContext *ctx, uint32_t max_arena_bytes) {
         if (spinn_hip_malloc(&ctx->workspace, need) != 0) rc = -2;
         else ctx->workspace_bytes = need;
     }
+    /* staging copy of input 0 for resident runs: outside the arena, whose
+     * input region later activations reuse */
+    SpinnTensor *tin = &ctx->tensors[ctx->input_ids[0]];
+    if (rc == 0 && !ctx->input_stage && tin->size > 0 && tin->data) {
+        if (spinn_hip_malloc(&ctx->input_stage, tin->size) != 0) rc = -2;
+    }
     if (rc == 0 && spinn_hip_stream_sync(ctx->stream) != 0) rc = -2;
     return rc;
 }
@@ -376,7 +382,7 @@ static int run_nodes(SpinnContext *ctx, ProfState *ps) {
     return first;
 }
 
-int spinn_run(SpinnContext *ctx, void *input_data, void *output_data) {
+static int run_impl(SpinnContext *ctx, void *input_data, void *output_data, int restore_stage) {
     if (!ctx || !ctx->stream) return -1;
     prof_init_once();
     ctx->last_error = 0;
@@ -385,6 +391,10 @@ int spinn_run(SpinnContext *ctx, void *input_data, void *output_data) {
     SpinnTensor *tin = &ctx->tensors[ctx->input_ids[0]];
     if (input_data && tin->data) {
         rc = spinn_hip_memcpy_h2d(tin->data, input_data, tin->size, ctx->stream);
+        if (rc) return rc;
+    } else if (restore_stage && tin->data) {
+        /* ordered on the stream before the node loop (eager or graph replay) */
+        rc = spinn_hip_copy(tin->data, ctx->input_stage, tin->size, ctx->stream);
         if (rc) return rc;
     }
     g_spinn_exec.conv_policy = ctx->conv_policy;
@@ -418,6 +428,7 @@ int spinn_run(SpinnContext *ctx, void *input_data, void *output_data) {
     if (rc == 0 && output_data && tout->data) rc = spinn_hip_memcpy_d2h(output_data, tout->data, tout->size, ctx->stream);
     int s = spinn_hip_stream_sync(ctx->stream);
     if (rc == 0) rc = s;
+    if (rc == 0) rc = spinn_hip_device_status(); /* a kernel that could not finish its work */
     if (ps && rc == 0) {
         for (uint32_t i = 0; i < ctx->num_nodes; i++) {
             float ms = 0.f;
@@ -435,7 +446,31 @@ int spinn_run(SpinnContext *ctx, void *input_data, void *output_data) {
     return rc;
 }
 
-int spinn_run_resident(SpinnContext *ctx) { return spinn_run(ctx, NULL, NULL); }
+int spinn_run(SpinnContext *ctx, void *input_data, void *output_data) {
+    return run_impl(ctx, input_data, output_data, 0);
+}
+
+int spinn_run_resident(SpinnContext *ctx) {
+    if (!ctx || !ctx->input_stage || !ctx->input_staged) return -1;
+    return run_impl(ctx, NULL, NULL, 1);
+}
+
+int spinn_stage_input(SpinnContext *ctx, const void *host, size_t bytes) {
+    if (!ctx || !ctx->input_stage) return -1;
+    SpinnTensor *tin = &ctx->tensors[ctx->input_ids[0]];
+    if (host) {
+        if (bytes != tin->size) return -1;
+        int rc = spinn_hip_memcpy_h2d(ctx->input_stage, host, bytes, ctx->stream);
+        if (rc == 0) rc = spinn_hip_stream_sync(ctx->stream);
+        if (rc) return rc;
+    } else if (bytes != 0) {
+        return -1;
+    }
+    ctx->input_staged = 1;
+    return 0;
+}
+
+void *spinn_input_stage_ptr(SpinnContext *ctx) { return ctx ? ctx->input_stage : NULL; }
 
 int spinn_set_graph_mode(SpinnContext *ctx, int enable) {
     if (!ctx) return -1;
@@ -489,6 +524,7 @@ static void ctx_release(SpinnContext *ctx) {
     if (ctx->graph_exec) spinn_hip_graph_destroy(ctx->graph_exec);
     spinn_free_packed(ctx);
     if (ctx->workspace) spinn_hip_free(ctx->workspace);
+    if (ctx->input_stage) spinn_hip_free(ctx->input_stage);
     if (ctx->weight_pool) spinn_hip_free(ctx->weight_pool);
     if (ctx->arena.base) spinn_hip_free(ctx->arena.base);
     if (ctx->stream) spinn_hip_stream_destroy(ctx->stream);

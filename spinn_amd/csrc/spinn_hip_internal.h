@@ -86,6 +86,17 @@ struct SkPlan {
 bool plan_streamk(int tiles_m, int tiles_n, int S, int tile_elems, SkPlan &p);
 void force_streamk(int mode);
 uint64_t streamk_epoch();
+// Host-visible status word that kernels set when an internal protocol fails
+// (a stream-K arrival that cannot complete): allocated once per process at
+// set-up (spinn_hip_init, or the plan-time workspace query); null before.
+void init_device_status();
+unsigned *device_status_word();
+// Read and clear the word (the caller has synchronised the streams).
+int take_device_status();
+// Arrival rounds of the stream-K parts (4; a test hook sets 0 to force the
+// failure report with every kernel still exiting normally).
+void force_streamk_tries(int tries);
+int streamk_tries();
 // Check once per device that workgroup b runs on XCD b % 8 (so the parts of a
 // cut tile can exchange sums through one L2); xcd_local_parts() reports the
 // result for the current device, false until checked.

@@ -29,14 +29,17 @@
 // epilogue's bias + residual, like a whole tile.
 //
 // Arrival counters are 64-bit: the launch's 48-bit epoch in the high bits and
-// the arrival count in the low 16. A counter holding another epoch (left by an
-// earlier launch, or any scratch contents) counts as zero, so the workspace
-// needs no clearing; the last arrival resets the count to zero under its own
-// epoch, so a graph replaying the same launch (same epoch) starts from zero.
+// the arrival count in the low 16 (protocol in sk_arrive.h). A counter holding
+// another epoch (left by an earlier launch, or any scratch contents) counts as
+// zero, so the workspace needs no clearing; the last arrival resets the count
+// to zero under its own epoch, so a graph replaying the same launch (same
+// epoch) starts from zero. An arrival that cannot complete the protocol sets
+// the host-visible status word instead of leaving the tile silently unwritten.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "mfma_core.h"
+#include "sk_arrive.h"
 
 namespace spinn {
 
@@ -59,6 +62,8 @@ struct SkSched {
     uint64_t epoch;  // 48-bit tag of this launch's counters, nonzero
     unsigned long long *cnt; // R arrival counters
     float *part;     // partial tiles in the per-thread layout, one slot per part
+    unsigned *status; // host-visible status word: set to 1 when an arrival fails (may be null)
+    int tries;       // arrival rounds before giving up (2 always suffice; see sk_arrive.h)
 };
 
 // Contiguous share of XCD x in the remaining tiles: [start, start + count).
@@ -73,39 +78,54 @@ __device__ __forceinline__ void sk_xcd_tiles(const SkSched &s, int x, int &start
 __device__ __forceinline__ int sk_begin(int w, int I, int Wx) { return (int)((int64_t)w * I / Wx); }
 __device__ __forceinline__ int sk_owner(int i, int I, int Wx) { return (int)(((int64_t)(i + 1) * Wx - 1) / I); }
 
-// Register the arrival of one part of a tile; true for the last part. Thread
-// 0 only; the caller has made its partial stores complete before calling.
-// The first arrival of a launch finds another epoch (or garbage) and installs
-// its own with one exchange; every other arrival adds 1 with one atomic, so
-// parts arriving together do not retry against each other.
-__device__ __forceinline__ bool sk_arrive(unsigned long long *c, uint64_t epoch, int nparts) {
-    const unsigned long long tag = (unsigned long long)epoch << 16;
-    unsigned long long v = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    int count = -1;
-    // A failed exchange can only have seen another part install this epoch,
-    // so the second round adds; the bound guards a corrupted counter.
-    for (int tries = 0; tries < 4 && count < 0; ++tries) {
-        if ((v >> 16) == epoch) {
-            const unsigned long long old =
-                __hip_atomic_fetch_add(c, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            count = (int)(old & 0xFFFFu) + 1;
-        } else if (__hip_atomic_compare_exchange_strong(c, &v, tag | 1ull, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_SYSTEM)) {
-            count = 1;
-        }
+// System-scope atomics on one arrival counter (the operations sk_arrive_count needs).
+struct SkDeviceCounter {
+    unsigned long long *p;
+    __device__ uint64_t load() const { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); }
+    __device__ uint64_t fetch_add(uint64_t d) const {
+        return __hip_atomic_fetch_add(p, (unsigned long long)d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    const bool last = count == nparts;
-    if (last) __hip_atomic_store(c, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    return last;
+    __device__ bool cas(uint64_t &exp, uint64_t desired) const {
+        unsigned long long e = exp;
+        const bool ok = __hip_atomic_compare_exchange_strong(p, &e, (unsigned long long)desired, __ATOMIC_RELAXED,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        exp = e;
+        return ok;
+    }
+};
+
+// Register the arrival of one part of a tile; true for the last part, which
+// resets the counter to a zero count under this epoch (so a graph replaying
+// the launch starts from zero). Thread 0 only; the caller has made its partial
+// stores complete before calling. A broken protocol (sk_arrive_outcome -1)
+// leaves the tile unfinished, so it is reported through the status word, which
+// the host reads after synchronising (spinn_hip_device_status).
+__device__ __forceinline__ bool sk_arrive(const SkSched &s, int cnt_idx, int nparts) {
+    SkDeviceCounter c{s.cnt + cnt_idx};
+    const int outcome = sk_arrive_outcome(sk_arrive_count(c, s.epoch, s.tries), nparts);
+    if (outcome < 0) {
+        if (s.status) __hip_atomic_store(s.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return false;
+    }
+    if (outcome == 1)
+        __hip_atomic_store(c.p, (unsigned long long)s.epoch << 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return outcome == 1;
 }
 
 // Partial sums move between the parts of a tile in one of two ways. All parts
 // of a tile have the same block id modulo 8, so when that is the XCD (checked
 // once per device at set-up, xcd_local_parts) they share one L2, the
-// coherence point of an XCD: plain stores (the L1 writes through) and loads
-// that bypass the L1 (sc0) suffice. Otherwise system-scope stores and loads
-// (sc0 + sc1: written through to / read from memory, past every L2) make the
-// exchange correct whatever the placement, at a longer round trip.
+// coherence point of an XCD: plain stores (the L1 writes through to the L2)
+// and loads marked sc0 suffice. Correctness there does not rest on sc0 alone
+// (the compiler's memory model counts sc0 as workgroup scope, which may hit in
+// the CU's L1) but on no L1 holding a line of a part slot when the last part
+// reads it: every L1 is invalidated when a launch starts, slots are 64x64x4 B
+// (whole cache lines, one slot per part), and within a launch each slot's lines
+// are read once, by the tile's last part, after every part's stores completed
+// (s_waitcnt before the arrival); the only earlier access from any CU is the
+// owning part's own store, which writes through. Otherwise system-scope stores
+// and loads (sc0 + sc1: written through to / read from memory, past every L2)
+// make the exchange correct whatever the placement, at a longer round trip.
 constexpr int kAuxL2Load = 1;  // sc0
 constexpr int kAuxSys = 17;    // sc0 + sc1
 __device__ __forceinline__ void part_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v, bool local) {
@@ -137,7 +157,7 @@ __device__ __forceinline__ bool sk_finish_part(const SkSched &s, int nslots, int
                     s.local);
     wait_stores();
     __syncthreads();
-    if (tid == 0) flag = sk_arrive(s.cnt + cnt_idx, s.epoch, nparts) ? 1 : 0;
+    if (tid == 0) flag = sk_arrive(s, cnt_idx, nparts) ? 1 : 0;
     __syncthreads();
     if (!flag) return false;
 #pragma unroll

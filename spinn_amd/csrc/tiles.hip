@@ -215,10 +215,10 @@ int probe_xcd_mapping() {
             for (int i = 0; i < n && ok; ++i) ok = h[i] == (unsigned)(i % kXcds);
         }
     }
-    if (d) hipFree(d);
-    if (st) hipStreamDestroy(st);
+    if (d) (void)hipFree(d);
+    if (st) (void)hipStreamDestroy(st);
     (void)hipGetLastError();
-    hipThreadExchangeStreamCaptureMode(&mode);
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
     return ok;
 }
 } // namespace
@@ -235,6 +235,44 @@ bool xcd_local_parts() {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
     return g_xcd[dev].local.load() != 0;
 }
+
+namespace {
+std::once_flag g_status_once;
+unsigned *g_status_host = nullptr; // pinned host word
+unsigned *g_status_dev = nullptr;  // its device address
+std::atomic<int> g_sk_tries{4};
+} // namespace
+
+void init_device_status() {
+    std::call_once(g_status_once, []() {
+        void *h = nullptr;
+        if (hipHostMalloc(&h, sizeof(unsigned), hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            return;
+        }
+        *(volatile unsigned *)h = 0u;
+        void *d = nullptr;
+        if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+            (void)hipGetLastError();
+            d = h;
+        }
+        g_status_host = (unsigned *)h;
+        g_status_dev = (unsigned *)d;
+    });
+}
+
+unsigned *device_status_word() { return g_status_dev; }
+
+int take_device_status() {
+    if (!g_status_host) return 0;
+    volatile unsigned *w = g_status_host;
+    const unsigned v = *w;
+    if (v) *w = 0u;
+    return (int)v;
+}
+
+void force_streamk_tries(int tries) { g_sk_tries.store(tries < 0 ? 4 : tries); }
+int streamk_tries() { return g_sk_tries.load(); }
 
 uint64_t streamk_epoch() {
     // 48-bit launch tags, never 0; the start varies between processes.

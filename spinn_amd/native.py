@@ -24,6 +24,7 @@ SPINN_HIP_OK = 0
 SPINN_HIP_EINVAL = -1
 SPINN_HIP_EUNSUPPORTED = -2
 SPINN_HIP_EWORKSPACE = -3
+SPINN_HIP_EDEVICE = -4
 NOALLOC_SCRATCH_BYTES = 128 << 20  # SPINN_HIP_NOALLOC_SCRATCH_BYTES
 
 ALGO_AUTO, ALGO_IMPLICIT_GEMM, ALGO_WINOGRAD, ALGO_DIRECT, ALGO_WINOGRAD_F43 = 0, 1, 2, 3, 4
@@ -117,6 +118,7 @@ class SpinnContext(C.Structure):
         ("last_error", C.c_int), ("last_error_node", C.c_int),
         ("graph_exec", C.c_void_p), ("use_graph", C.c_int), ("prof_state", C.c_void_p),
         ("conv_policy", C.c_int),
+        ("input_stage", C.c_void_p), ("input_staged", C.c_int),
     ]
 
 
@@ -138,6 +140,8 @@ _SIGS = {
     "spinn_hip_maxpool2d": (C.c_int, [C.POINTER(PoolDesc), C.c_void_p, C.c_void_p, C.c_void_p]),
     "spinn_hip_reduce_mean": (C.c_int, [C.c_int64, C.c_int64, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]),
     "spinn_hip_copy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "spinn_hip_device_status": (C.c_int, []),
+    "spinn_hip_tune_streamk_tries": (None, [C.c_int]),
     "spinn_hip_binary": (C.c_int, [C.c_int, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
                                    C.c_void_p]),
     "spinn_hip_unary": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),
@@ -192,6 +196,8 @@ _SIGS = {
     "spinn_tensor_upload": (C.c_int, [C.POINTER(SpinnContext), C.c_uint16, C.c_void_p, C.c_size_t]),
     "spinn_tensor_download": (C.c_int, [C.POINTER(SpinnContext), C.c_uint16, C.c_void_p, C.c_size_t]),
     "spinn_run_resident": (C.c_int, [C.POINTER(SpinnContext)]),
+    "spinn_stage_input": (C.c_int, [C.POINTER(SpinnContext), C.c_void_p, C.c_size_t]),
+    "spinn_input_stage_ptr": (C.c_void_p, [C.POINTER(SpinnContext)]),
     "spinn_set_graph_mode": (C.c_int, [C.POINTER(SpinnContext), C.c_int]),
     "spinn_node_times": (C.c_int, [C.POINTER(SpinnContext), C.POINTER(C.c_float), C.c_int]),
     "spinn_op_registered": (C.c_int, [C.c_uint16]),

@@ -2,8 +2,9 @@
 
     with Session("model.ennf") as s:
         y = s.run(x)              # host in, host out (H2D + nodes + D2H + sync)
-        s.upload_input(x)         # keep the input resident in HBM ...
-        s.run_resident()          # ... and time only the node loop
+        s.upload_input(x)         # stage the input in HBM once ...
+        s.run_resident()          # ... then each step copies it into the arena (device to
+                                  # device) and runs the node loop, outputs left in HBM
 """
 from __future__ import annotations
 
@@ -74,8 +75,10 @@ class Session:
         return y
 
     def upload_input(self, x: np.ndarray) -> None:
+        """Stage input 0 in the context's device staging buffer; every later
+        run_resident() restores the arena's input region from it."""
         x = np.ascontiguousarray(x, np.float32)
-        N.check(self.L.spinn_tensor_upload(self.ctx, self.input_id, x.ctypes.data, x.nbytes), "upload")
+        N.check(self.L.spinn_stage_input(self.ctx, x.ctypes.data, x.nbytes), "spinn_stage_input")
 
     _NP = {1: np.float32, 6: np.int32, 7: np.int64}
 

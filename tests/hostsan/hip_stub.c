@@ -36,6 +36,7 @@ int spinn_hip_copy(void *dst, const void *src, size_t bytes, void *stream) {
     if (bytes) memmove(dst, src, bytes);
     return 0;
 }
+int spinn_hip_device_status(void) { return 0; }
 int spinn_hip_fill_u32(void *dst, uint32_t value, size_t bytes, void *stream) {
     (void)stream;
     uint32_t *p = (uint32_t *)dst;

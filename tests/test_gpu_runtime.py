@@ -101,6 +101,52 @@ def test_resnet101_b1_graph_replay(hip, tmp_path):
         assert np.array_equal(o, y_eager)
 
 
+def _input_region_reused(s) -> bool:
+    """Whether the plan places another tensor inside input 0's arena region (the
+    reference planner frees it after its last consumer,
+    SPINN/run_time/spinn_memory_planner.c:231-238)."""
+    t_in = s.tensor(s.input_id)
+    lo, hi = t_in.offset, t_in.offset + t_in.size
+    return any(tid != s.input_id and off < hi and off + s.tensor(tid).size > lo
+               for tid, off in s.offsets().items())
+
+
+@pytest.mark.parametrize("graph", [False, True], ids=["eager", "graph"])
+@pytest.mark.parametrize("model", ["resnet50_96_b2", "yolov10n_320_b2_tail"])
+def test_resident_runs_restore_input(hip, tmp_path, model, graph):
+    """Input staged once, then three spinn_run_resident steps: each step restores
+    input 0 into its arena region before the node loop (the reference copies the
+    input on every spinn_run, SPINN/run_time/spinn_runtime.c:302-306), so runs 2
+    and 3 equal run 1 bit for bit and the oracle within the bar, although the plan
+    hands the input's region to later activations."""
+    if model == "resnet50_96_b2":
+        g, x = models.resnet(batch=2, seed=11, blocks=models.RESNET50_BLOCKS, hw=96)
+    else:
+        g, x = models.yolov10n(batch=2, seed=12, hw=320, postprocess=True)
+    path = g.write(tmp_path / f"{model}.ennf")
+    print(f"[resident] {model} graph={graph}", flush=True)
+    with Session(path, graph=graph) as s:
+        assert _input_region_reused(s), "the plan must reuse the input region for this test to mean anything"
+        with pytest.raises(N.SpinnError):
+            s.run_resident()  # nothing staged yet
+        y_host = s.run(x)
+        s.upload_input(x)
+        outs = []
+        for _ in range(3):
+            s.run_resident()
+            outs.append(s.download(s.output_id))
+        # a host-copy run in between must not disturb the staged input
+        s.run(np.zeros_like(x))
+        s.run_resident()
+        outs.append(s.download(s.output_id))
+    for i, o in enumerate(outs):
+        assert np.array_equal(o.view(np.uint32), y_host.view(np.uint32)), f"resident run {i + 1} differs"
+    if model == "resnet50_96_b2":
+        ref = O.Model(path).run(x, g.dims(g.outputs[0]))
+        assert_parity(outs[1], ref, what=f"{model} resident run 2", scale_by_ref=True)
+        assert_parity(outs[2], ref, what=f"{model} resident run 3", scale_by_ref=True)
+
+
 @pytest.mark.parametrize("batch,hw", [(1, 640), (2, 320)], ids=["b1_640", "b2_320"])
 def test_yolov10n(hip, tmp_path, batch, hw):
     """The detector: fused Conv+SiLU / Conv+Add, depthwise, unfused Add / Split /

@@ -86,6 +86,7 @@ def streamk_mode(hip):
     L = hip.lib()
     yield L.spinn_hip_tune_streamk
     L.spinn_hip_tune_streamk(-1)
+    L.spinn_hip_tune_streamk_tries(-1)
     L.spinn_hip_tune_force_tiles(0, 0, 0)
 
 
@@ -127,6 +128,40 @@ def test_streamk_parity_and_repeats(hip, torch_gpu, streamk_mode, case, exchange
         assert_parity(outs[-1], ref, what=f"{case[0]} stream-K call {i} vs oracle")
     assert np.array_equal(outs[0], outs[1]), "repeated stream-K launches differ"
     assert np.array_equal(outs[0], outs[2]), "stream-K launch over a garbage workspace differs"
+    assert hip.lib().spinn_hip_device_status() == 0, "an arrival reported a failure"
+
+
+def test_streamk_arrival_failure_is_reported(hip, torch_gpu, streamk_mode):
+    """With the arrival rounds set to 0 from the host (every kernel still exits
+    normally), no part of a cut tile can claim its counter: those tiles stay
+    unwritten and spinn_hip_device_status reports it once; whole tiles are
+    still right. Restored, the same launch is complete and reports nothing."""
+    torch = torch_gpu
+    L = hip.lib()
+    streamk_mode(1)
+    cv = _Conv(hip, torch, CASES[0])
+    ref = cv.oracle()
+    wsz = cv.ws_bytes()
+    assert wsz > 0
+    ws = torch.zeros(wsz // 4, device="cuda")
+    assert L.spinn_hip_device_status() == 0
+    L.spinn_hip_tune_streamk_tries(0)
+    try:
+        y = cv.run(ws)  # output pre-filled with NaN
+        torch.cuda.synchronize()
+    finally:
+        L.spinn_hip_tune_streamk_tries(-1)
+    assert L.spinn_hip_device_status() == hip.SPINN_HIP_EDEVICE
+    assert L.spinn_hip_device_status() == 0, "the report is cleared once read"
+    yb = y.cpu().numpy()
+    unwritten = np.isnan(yb)
+    assert unwritten.any(), "cut tiles must stay unwritten when no arrival completes"
+    written = ~unwritten
+    assert np.abs(yb[written] - ref[written]).max() <= 1e-3, "whole tiles are unaffected"
+    y = cv.run(ws)
+    torch.cuda.synchronize()
+    assert L.spinn_hip_device_status() == 0
+    assert_parity(y.cpu().numpy(), ref, what="stream-K after the failure report")
 
 
 def test_streamk_rule_picks_remainder_split(hip, torch_gpu, streamk_mode):

@@ -22,6 +22,11 @@ PAIRS = [
     ("f43_b32_then_f43_b2", (32, 256, 14, 14, 256, 3, 1, 1, 1, 1, 4), (2, 128, 28, 28, 128, 3, 1, 1, 1, 5, 4)),
     ("f23_then_splitk", (8, 128, 28, 28, 128, 3, 1, 1, 1, 3, 2), (1, 2048, 7, 7, 512, 1, 1, 0, 1, 1, 1)),
     ("auto_stem_then_depthwise", (4, 3, 224, 224, 64, 7, 2, 3, 1, 1, 0), (1, 32, 20, 20, 32, 3, 2, 1, 32, 3, 0)),
+    # stream-K under the per-shape rule: the 392-tile layer takes extra workgroups, the
+    # 1568-tile one has whole-tile workgroups do the parts; arrival counters and partial
+    # slots stay in the shared scratch between the calls
+    ("streamk_wgs_then_streamk_parts", (32, 1024, 14, 14, 256, 1, 1, 0, 1, 1, 1),
+     (32, 256, 14, 14, 1024, 1, 1, 0, 1, 5, 1)),
 ]
 
 
@@ -45,15 +50,22 @@ def _operands(torch, L, hip, case, seed):
     return d, (xd, wd, pk, bd, rd), ref
 
 
-@pytest.mark.parametrize("pair", PAIRS, ids=[p[0] for p in PAIRS])
-def test_noalloc_matches_workspace_entry_point(hip, torch_gpu, pair):
+CASES = [(p, -1) for p in PAIRS] + [(p, 2) for p in PAIRS if p[0].startswith("streamk")]
+
+
+@pytest.mark.parametrize("pair,streamk", CASES,
+                         ids=[p[0] + ("_exchange_memory" if m == 2 else "") for p, m in CASES])
+def test_noalloc_matches_workspace_entry_point(hip, torch_gpu, pair, streamk):
     L = hip.lib()
     if "splitk" in pair[0]:
         L.spinn_hip_tune_force_tiles(64, 64, 4)
+    L.spinn_hip_tune_streamk(streamk)  # 2: parts' sums through memory even where they share an L2
     try:
         _compare_pair(hip, torch_gpu, L, pair)
     finally:
         L.spinn_hip_tune_force_tiles(0, 0, 0)
+        L.spinn_hip_tune_streamk(-1)
+    assert L.spinn_hip_device_status() == 0
 
 
 def _compare_pair(hip, torch, L, pair):
@@ -63,8 +75,8 @@ def _compare_pair(hip, torch, L, pair):
         wsz = L.spinn_hip_conv_workspace_size(C.byref(d))
         print(f"[noalloc] {name} call {i}: algo={d.algo} scratch={wsz}", flush=True)
         assert wsz <= hip.NOALLOC_SCRATCH_BYTES
-        if "splitk" in name:
-            assert wsz > 0, "the split-K pair must use the scratch"
+        if "splitk" in name or name.startswith("streamk"):
+            assert wsz > 0, "the split-K / stream-K pair must use the scratch"
         ws = torch.empty(max(wsz // 4, 1), device="cuda") if wsz else None
         y_ws = torch.full((d.n, d.oc, d.oh, d.ow), float("nan"), device="cuda")
         y_na = torch.full((d.n, d.oc, d.oh, d.ow), float("nan"), device="cuda")
