@@ -913,6 +913,84 @@ def pmc_summary(d: Path) -> str:
     return "\n".join(out)
 
 
+FAMILY_COUNTERS = ("SQ_WAVES", "SQ_BUSY_CU_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_MFMA", "SQ_INSTS_VALU",
+                   "SQ_INSTS_LDS", "SQ_INSTS_VMEM_RD", "SQ_LDS_BANK_CONFLICT")
+
+
+def family_counters_summary(d: Path, tags: list) -> str:
+    """Per kernel family of each workload tag: rocprofv3 runs `{tag}_sq` (--pmc with the
+    FAMILY_COUNTERS), `{tag}_FETCH_SIZE` and `{tag}_WRITE_SIZE` (each with --kernel-trace),
+    plus `calib_FETCH_SIZE` / `calib_WRITE_SIZE` (bench.py --calibration-kernels) for the
+    byte scale. Reports, per dispatch: mean duration, executed MFMA rate (busy cycles x 64
+    fp32 flops per cycle and SIMD: v_mfma_f32_32x32x2f32 is 4096 flops in 64 cycles,
+    16x16x4f32 2048 in 32) against the 157.3 TFLOP/s peak, non-MFMA VALU / LDS / vector-memory
+    instructions per MFMA, LDS bank conflicts, and calibrated fetched / written MB and their
+    rate (L2-to-fabric traffic: Infinity Cache hits count as memory traffic)."""
+    import collections
+    import csv
+
+    def load(name):
+        p = d / f"{name}_counter_collection.csv"
+        if not p.exists():
+            return None
+        per = collections.defaultdict(dict)
+        with open(p) as f:
+            for r in csv.DictReader(f):
+                if "spinn::" not in r["Kernel_Name"] and "rocclr" not in r["Kernel_Name"]:
+                    continue
+                e = per[r["Dispatch_Id"]]
+                e["name"] = _kernel_label(r["Kernel_Name"]).split("<")[0]
+                e["us"] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                e[r["Counter_Name"]] = float(r["Counter_Value"])
+        return per
+
+    def calib(counter, kind):
+        per = load(f"calib_{counter}")
+        v = [e[counter] for _, e in sorted(per.items(), key=lambda kv: int(kv[0])) if kind in e["name"].lower()]
+        v = v[1:] if len(v) > 1 else v
+        return (CALIB_BYTES / 1024) / (sum(v) / len(v))
+
+    f_fetch, f_write = calib("FETCH_SIZE", "copy"), calib("WRITE_SIZE", "fill")
+    out = [f"Byte scale from the 256 MiB copy / fill calibration: FETCH_SIZE x {f_fetch:.3f}, "
+           f"WRITE_SIZE x {f_write:.3f}.", ""]
+    for tag in tags:
+        fam = collections.defaultdict(lambda: collections.defaultdict(list))
+        for part in ("sq", "FETCH_SIZE", "WRITE_SIZE"):
+            per = load(f"{tag}_{part}")
+            if per is None:
+                continue
+            for e in per.values():
+                for k, v in e.items():
+                    if k != "name":
+                        fam[e["name"]][f"{part}:{k}"].append(v)
+        out += [f"### {tag}", "",
+                "| kernel family | dispatches | mean us | MFMA TFLOP/s executed | % of MFMA peak | VALU / MFMA | "
+                "LDS / MFMA | VMEM rd / MFMA | LDS bank conflicts / dispatch | fetched MB | written MB | GB/s |",
+                "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+        rows = []
+        for name, cs in fam.items():
+            m = lambda k: (sum(cs[k]) / len(cs[k])) if cs.get(k) else None  # noqa: E731
+            us = m("sq:us") or m("FETCH_SIZE:us")
+            if not us:
+                continue
+            busy, mf = m("sq:SQ_VALU_MFMA_BUSY_CYCLES"), m("sq:SQ_INSTS_MFMA")
+            tf = busy * 64 / (us * 1e-6) / 1e12 if busy else 0.0
+            fmb = m("FETCH_SIZE:FETCH_SIZE")
+            wmb = m("WRITE_SIZE:WRITE_SIZE")
+            fmb = fmb * 1024 * f_fetch / 1e6 if fmb is not None else None
+            wmb = wmb * 1024 * f_write / 1e6 if wmb is not None else None
+            rate = (fmb + wmb) / us * 1e3 if fmb is not None and wmb is not None else None
+            per_mf = lambda k: f"{(m(k) - (mf if k.endswith('VALU') else 0)) / mf:.2f}" if mf and m(k) is not None else "-"  # noqa: E731,E501
+            rows.append((us * len(cs.get("sq:us", cs.get("FETCH_SIZE:us", []))),
+                         f"| {name} | {len(cs.get('sq:us', []))} | {us:.2f} | {tf:.1f} | {100 * tf / 157.3:.1f} | "
+                         f"{per_mf('sq:SQ_INSTS_VALU')} | {per_mf('sq:SQ_INSTS_LDS')} | {per_mf('sq:SQ_INSTS_VMEM_RD')} | "
+                         f"{(m('sq:SQ_LDS_BANK_CONFLICT') or 0):.0f} | "
+                         f"{'-' if fmb is None else f'{fmb:.2f}'} | {'-' if wmb is None else f'{wmb:.2f}'} | "
+                         f"{'-' if rate is None else f'{rate:.0f}'} |"))
+        out += [r for _, r in sorted(rows, key=lambda x: -x[0])] + [""]
+    return "\n".join(out)
+
+
 ENGINE_SCAN_SHAPES = [(1024, 14), (256, 14), (256, 56)]  # (output channels, plane edge) at batch 32
 ENGINE_SCAN_K = [64, 128, 256, 512, 1024, 2048]
 
@@ -1059,6 +1137,10 @@ def main() -> int:
     ap.add_argument("--passes", type=int, default=1, help="passes in the traced run, for --trace-summary")
     ap.add_argument("--pmc-summary", metavar="DIR",
                     help="print per-dispatch averages of the rocprofv3 --pmc CSVs in DIR (no GPU)")
+    ap.add_argument("--family-counters", metavar="DIR",
+                    help="per-kernel-family counter table of the rocprofv3 runs in DIR (no GPU; see "
+                         "family_counters_summary)")
+    ap.add_argument("--tags", default="r101b32,r101b1,y10b16", help="workload tags for --family-counters")
     ap.add_argument("--engine-scan", action="store_true",
                     help="time 1x1 convs at batch 32 over K to split fixed cost from the K loop's rate")
     a = ap.parse_args()
@@ -1086,6 +1168,9 @@ def main() -> int:
         return 0
     if a.pmc_summary:
         print(pmc_summary(Path(a.pmc_summary)))
+        return 0
+    if a.family_counters:
+        print(family_counters_summary(Path(a.family_counters), a.tags.split(",")))
         return 0
     if a.engine_scan:
         engine_scan()

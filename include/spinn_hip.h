@@ -292,6 +292,14 @@ void spinn_hip_tune_force_tiles(int bm, int bn, int split);
  * plans: workspace sizes depend on it. No counterpart in the reference. */
 void spinn_hip_tune_streamk(int mode);
 
+/* Tuning hook: how F(4x4,3x3) Winograd layers run. -1 = per-shape choice (default,
+ * or SPINN_WINOGRAD_FUSED=0|1 from the environment), 0 = always three launches
+ * (input transform, 36 batched GEMMs, output transform, V and M in the workspace),
+ * 1 = one fused launch wherever it fits (transforms and GEMMs on chip, no workspace).
+ * Change it only between plans: workspace sizes depend on it. No counterpart in the
+ * reference. */
+void spinn_hip_tune_winograd_fused(int mode);
+
 /* Test hook: arrival rounds of the stream-K parts (default 4; < 0 restores
  * it). 0 makes every arrival fail, so the cut tiles stay unwritten and the
  * status word reports it, while every kernel still exits normally. No

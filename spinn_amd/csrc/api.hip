@@ -50,6 +50,8 @@ static bool winograd_pays(const SpinnHipConvDesc *d, int m) {
     // and at 64 channels with >= 256 tiles (64@56x56 batch 32: 72 against 92 us for the
     // implicit GEMM; at batch 1, 196 tiles, it loses).
     if (m == 4) {
+        // the one-launch form (winograd_fused.hip) where it applies: few channels, many tiles
+        if (wino4_fused_selected(d)) return true;
         const int64_t tiles = (int64_t)d->n * ((d->oh + 3) / 4) * ((d->ow + 3) / 4);
         const bool wide = d->c >= 128 && d->oc >= 128;
         return d->c >= 64 && d->oc >= 64 && tiles >= (wide ? 128 : 256);
@@ -463,6 +465,8 @@ void spinn_hip_tune_force_tiles(int bm, int bn, int split) { force_tiles(bm, bn,
 void spinn_hip_tune_streamk(int mode) { force_streamk(mode); }
 
 void spinn_hip_tune_streamk_tries(int tries) { force_streamk_tries(tries); }
+
+void spinn_hip_tune_winograd_fused(int mode) { force_winograd_fused(mode); }
 
 const char *spinn_hip_version(void) { return "spinn_amd 0.1 gfx950 fp32-mfma"; }
 

@@ -415,6 +415,9 @@ int launch_conv_sk_tile(const ConvKArgs &a, const SkPlan &sp, int S, void *ws, h
 template <template <int> class BLT>
 int launch_conv_sk(const ConvKArgs &a, const TileChoice &tc, const SkPlan &sp, int S, void *ws, hipStream_t st) {
     if (tc.bm == 32 && tc.bn == 128) return launch_conv_sk_tile<32, 128, BLT<128>>(a, sp, S, ws, st);
+    if (tc.bm == 128 && tc.bn == 128) return launch_conv_sk_tile<128, 128, BLT<128>>(a, sp, S, ws, st);
+    if (tc.bm == 128 && tc.bn == 64) return launch_conv_sk_tile<128, 64, BLT<64>>(a, sp, S, ws, st);
+    if (tc.bm == 64 && tc.bn == 128) return launch_conv_sk_tile<64, 128, BLT<128>>(a, sp, S, ws, st);
     return launch_conv_sk_tile<64, 64, BLT<64>>(a, sp, S, ws, st);
 }
 
@@ -491,14 +494,13 @@ static TileChoice igemm_tiles(const SpinnHipConvDesc *d) {
     return choose_tiles(OCg, ntot, K, d->group, d->group == 1);
 }
 
-// Data-parallel + stream-K split for a group-1 conv on 64 x 64 or 32 x 128
-// tiles whose tile count leaves the CUs unevenly loaded.
+// Data-parallel + stream-K split for a group-1 conv whose tile count leaves
+// the CUs unevenly loaded (any tile shape).
 static bool igemm_streamk(const SpinnHipConvDesc *d, const TileChoice &tc, SkPlan &sp) {
     // A grid the tile rule already splits along K (long K, few tiles) keeps its
     // split: several workgroups per CU hide the gather latency better than one
     // or two whole tiles and an extra range.
-    if (d->group != 1 || tc.split > 1 || !((tc.bm == 64 && tc.bn == 64) || (tc.bm == 32 && tc.bn == 128)))
-        return false;
+    if (d->group != 1 || tc.split > 1) return false;
     const int K = d->c * d->kh * d->kw;
     const int ntot = d->n * d->oh * d->ow;
     return plan_streamk((d->oc + tc.bm - 1) / tc.bm, (ntot + tc.bn - 1) / tc.bn, (K + kBK - 1) / kBK,

@@ -143,6 +143,12 @@ int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const fl
 
 // Winograd F(2x2,3x3) / F(4x4,3x3) (winograd.hip); m = output tile edge, 2 or 4
 bool winograd_eligible(const SpinnHipConvDesc *d);
+// F(4x4,3x3) in one launch (winograd_fused.hip): transforms and the 36 GEMMs on chip,
+// no workspace; chosen per shape (few input channels) unless forced.
+bool wino4_fused_selected(const SpinnHipConvDesc *d);
+int wino4_fused_conv(const SpinnHipConvDesc *d, const float *x, const float *U, const float *bias,
+                     const float *res, float *y, hipStream_t st);
+void force_winograd_fused(int mode);
 int64_t winograd_packed_floats(const SpinnHipConvDesc *d, int m);
 int winograd_pack(const SpinnHipConvDesc *d, int m, const float *w, float *packed, hipStream_t st);
 size_t winograd_workspace_bytes(const SpinnHipConvDesc *d, int m);

@@ -19,6 +19,7 @@
 // U (packed weights) is [P][C][OC], OC contiguous, so the GEMM reads both
 // operands k-major with 16-byte loads.
 #include "spinn_hip_internal.h"
+#include "winograd_tf.h"
 
 namespace spinn {
 
@@ -47,33 +48,6 @@ WinoGeom wino_geom(const SpinnHipConvDesc *d, int m) {
     g.TW = (d->ow + g.m - 1) / g.m;
     g.T = (int64_t)g.N * g.TH * g.TW;
     return g;
-}
-
-// 1-D transforms of F(4,3) (Lavin & Gray 2015, points 0, 1, -1, 2, -2, inf).
-__device__ __forceinline__ void bt6(const float d[6], float o[6]) {   // B^T (6x6)
-    o[0] = 4.f * d[0] - 5.f * d[2] + d[4];
-    o[1] = -4.f * d[1] - 4.f * d[2] + d[3] + d[4];
-    o[2] = 4.f * d[1] - 4.f * d[2] - d[3] + d[4];
-    o[3] = -2.f * d[1] - d[2] + 2.f * d[3] + d[4];
-    o[4] = 2.f * d[1] - d[2] - 2.f * d[3] + d[4];
-    o[5] = 4.f * d[1] - 5.f * d[3] + d[5];
-}
-
-__device__ __forceinline__ void g6(const float g[3], float o[6]) {    // G (6x3)
-    o[0] = 0.25f * g[0];
-    o[1] = (g[0] + g[1] + g[2]) * (-1.f / 6.f);
-    o[2] = (g[0] - g[1] + g[2]) * (-1.f / 6.f);
-    o[3] = g[0] * (1.f / 24.f) + g[1] * (1.f / 12.f) + g[2] * (1.f / 6.f);
-    o[4] = g[0] * (1.f / 24.f) - g[1] * (1.f / 12.f) + g[2] * (1.f / 6.f);
-    o[5] = g[2];
-}
-
-__device__ __forceinline__ void at6(const float m[6], float o[4]) {   // A^T (4x6)
-    const float p12 = m[1] + m[2], m12 = m[1] - m[2], p34 = m[3] + m[4], m34 = m[3] - m[4];
-    o[0] = m[0] + p12 + p34;
-    o[1] = m12 + 2.f * m34;
-    o[2] = p12 + 4.f * p34;
-    o[3] = m12 + 8.f * m34 + m[5];
 }
 
 } // namespace
@@ -235,7 +209,10 @@ constexpr int kW4Threads = 6 * kW4Tiles;
 // V[a][c][t] = (B^T d B)[a] over the 6x6 input patch of tile t. Grid: (ceil(T / 64), C).
 __global__ __launch_bounds__(kW4Threads) void wino4_input_kernel(const float *__restrict__ x,
                                                                  float *__restrict__ V, WinoGeom g) {
-    __shared__ float tt[kW4Tiles][6][7]; // [tile][row i][column j], padded
+    // [tile][row i][column j]; a tile's 42 words padded to an odd stride, so the 64
+    // lanes of a wave (64 tiles) fall in 64 different banks
+    constexpr int kTS = 43;
+    __shared__ float tt[kW4Tiles * kTS];
     const int lane_t = threadIdx.x % kW4Tiles;
     const int q = threadIdx.x / kW4Tiles; // phase 1: patch column j; phase 2: transform row i
     const int c = blockIdx.y;
@@ -260,13 +237,13 @@ __global__ __launch_bounds__(kW4Threads) void wino4_input_kernel(const float *__
         float o[6];
         bt6(col, o);
 #pragma unroll
-        for (int i = 0; i < 6; ++i) tt[lane_t][i][q] = o[i];
+        for (int i = 0; i < 6; ++i) tt[lane_t * kTS + i * 7 + q] = o[i];
     }
     __syncthreads();
     if (live) {
         float row[6];
 #pragma unroll
-        for (int j = 0; j < 6; ++j) row[j] = tt[lane_t][q][j];
+        for (int j = 0; j < 6; ++j) row[j] = tt[lane_t * kTS + q * 7 + j];
         float o[6];
         bt6(row, o);
         const int64_t plane = (int64_t)g.C * g.T;
@@ -283,7 +260,9 @@ __global__ __launch_bounds__(kW4Threads) void wino4_output_kernel(const float *_
                                                                   const float *__restrict__ bias,
                                                                   const float *__restrict__ res, int act,
                                                                   float *__restrict__ y, WinoGeom g) {
-    __shared__ float tt[kW4Tiles][4][7]; // [tile][row i][column j], padded
+    // [tile][row i][column j]; a tile's 28 words padded to an odd stride (conflict-free)
+    constexpr int kTS = 29;
+    __shared__ float tt[kW4Tiles * kTS];
     const int lane_t = threadIdx.x % kW4Tiles;
     const int q = threadIdx.x / kW4Tiles;
     const int oc = blockIdx.y;
@@ -298,13 +277,13 @@ __global__ __launch_bounds__(kW4Threads) void wino4_output_kernel(const float *_
         float o[4];
         at6(col, o);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) tt[lane_t][i][q] = o[i];
+        for (int i = 0; i < 4; ++i) tt[lane_t * kTS + i * 7 + q] = o[i];
     }
     __syncthreads();
     if (live && q < 4) {
         float row[6];
 #pragma unroll
-        for (int j = 0; j < 6; ++j) row[j] = tt[lane_t][q][j];
+        for (int j = 0; j < 6; ++j) row[j] = tt[lane_t * kTS + q * 7 + j];
         float o[4];
         at6(row, o);
         const int per_img = g.TH * g.TW;
@@ -366,12 +345,14 @@ static SpinnHipGemmDesc wino_gemm_desc(const WinoGeom &g) {
 }
 
 size_t winograd_workspace_bytes(const SpinnHipConvDesc *d, int m) {
+    if (m == 4 && wino4_fused_selected(d)) return 0; // V and M stay on chip
     WinoGeom g = wino_geom(d, m);
     return ((size_t)g.P * g.C * g.T + (size_t)g.P * g.OC * g.T) * sizeof(float);
 }
 
 int winograd_conv(const SpinnHipConvDesc *d, int m, const float *x, const float *packed, const float *bias,
                   const float *res, float *y, void *ws, size_t ws_bytes, hipStream_t st) {
+    if (m == 4 && wino4_fused_selected(d)) return wino4_fused_conv(d, x, packed, bias, res, y, st);
     WinoGeom g = wino_geom(d, m);
     if (g.T > INT32_MAX) return SPINN_HIP_EUNSUPPORTED;
     if (m == 4 && (g.C > 65535 || g.OC > 65535)) return SPINN_HIP_EUNSUPPORTED; // channels on grid y

@@ -142,6 +142,7 @@ _SIGS = {
     "spinn_hip_copy": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "spinn_hip_device_status": (C.c_int, []),
     "spinn_hip_tune_streamk_tries": (None, [C.c_int]),
+    "spinn_hip_tune_winograd_fused": (None, [C.c_int]),
     "spinn_hip_binary": (C.c_int, [C.c_int, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64, C.c_void_p, C.c_int64,
                                    C.c_void_p]),
     "spinn_hip_unary": (C.c_int, [C.c_int, C.c_void_p, C.c_void_p, C.c_int64, C.c_void_p]),

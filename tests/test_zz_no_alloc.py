@@ -93,8 +93,9 @@ def _compare_pair(hip, torch, L, pair):
 def test_noalloc_rejects_oversized_scratch(hip, torch_gpu):
     """A conv whose scratch exceeds the fixed array is refused before any launch."""
     L = hip.lib()
-    # F(4x4,3x3) at 16 x 64 x 112 x 112: V and M are 2 x 115.6 MB
-    d = conv_desc(hip, 16, 64, 112, 112, 64, 3, 3, 1, 1, 1, 1, 1, 1, 4)
+    # F(4x4,3x3) in three launches at 16 x 128 x 112 x 112: V and M are 2 x 231 MB
+    # (128 channels stay off the one-launch form, which needs no scratch)
+    d = conv_desc(hip, 16, 128, 112, 112, 128, 3, 3, 1, 1, 1, 1, 1, 1, 4)
     assert L.spinn_hip_conv_workspace_size(C.byref(d)) > hip.NOALLOC_SCRATCH_BYTES
     rc = L.spinn_hip_conv_noalloc(C.byref(d), C.c_void_p(256), C.c_void_p(256), C.c_void_p(256), None, None,
                                   C.c_void_p(256), None)
