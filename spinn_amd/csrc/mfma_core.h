@@ -315,18 +315,30 @@ struct Im2colTapLoader {
     PixelOrigin px;
     uint32_t hw;
     float r[NV];
+    // k0 of the previous fetch and its decomposition k_last = (kh * KW + kw) * Cg + c0
+    // (wave-uniform): each loader copy sees k0 only grow, by a fixed step of one
+    // or two slices, so the tap follows by carries instead of two integer
+    // divisions per slice (k0 < KH * KW * Cg bounds the carries of a first fetch).
+    int k_last, c0, kh, kw;
 
     __device__ __forceinline__ void init(const ConvGeom &geom, int n0, int group, int tid, int /*kend*/) {
         g = geom;
         rsrc = make_rsrc(g.x, g.x_bytes);
         hw = (uint32_t)(g.H * g.W);
         px.init(g, n0 + (tid % BN), group);
+        k_last = c0 = kh = kw = 0;
     }
     __device__ __forceinline__ void fetch(int k0, int tid) {
-        const int tap = k0 / g.Cg;
-        const int c0 = k0 - tap * g.Cg;
-        const int kh = tap / g.KW;
-        const int kw = tap - kh * g.KW;
+        if (k0 < k_last) c0 = kh = kw = k_last = 0;
+        c0 += k0 - k_last;
+        while (c0 >= g.Cg) {
+            c0 -= g.Cg;
+            if (++kw == g.KW) {
+                kw = 0;
+                ++kh;
+            }
+        }
+        k_last = k0;
         const int ih = px.ih0 + kh;
         const int iw = px.iw0 + kw;
         // taps past the window (fetches beyond the end of K) read zeros too
