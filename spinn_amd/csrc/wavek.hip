@@ -121,27 +121,33 @@ struct WkKContig {
 };
 
 // Implicit-GEMM B operand, 1x1 stride-1 unpadded conv: column n = (img, p)
-// reads x[img][g*Cg + k][p].
+// reads x[img][g*Cg + k][p]. The lane's pixel is a byte offset with the column
+// test folded in (kOOB past ntot: adding a channel offset below 2^31 keeps it
+// out of range without wrapping), so a load costs one add. K is a multiple of
+// the k block (the caller's condition; the per-wave ranges are block multiples),
+// so a block is wholly inside or past the wave's K end and the test is a
+// wave-uniform choice of descriptor, one of size 0 past the end.
 struct WkPointwise {
-    __amdgpu_buffer_rsrc_t rsrc;
-    uint32_t base, hw;
-    bool ok;
+    __amdgpu_buffer_rsrc_t rsrc, rnone;
+    uint32_t vbase, hw4;
     int k_end;
     __device__ __forceinline__ void init(const ConvGeom &g, int n, int group, int kend) {
         rsrc = make_rsrc(g.x, g.x_bytes);
-        hw = (uint32_t)(g.OH * g.OW);
-        ok = n < g.ntot;
+        rnone = make_rsrc(g.x, 0u);
+        const uint32_t hw = (uint32_t)(g.OH * g.OW);
+        hw4 = hw * 4u;
+        const bool ok = n < g.ntot;
         const int nn = ok ? n : 0;
         const int img = nn / (int)hw;
-        base = ((uint32_t)img * g.C + (uint32_t)group * g.Cg) * hw + (uint32_t)(nn - img * (int)hw);
+        vbase = ok ? (((uint32_t)img * g.C + (uint32_t)group * g.Cg) * hw + (uint32_t)(nn - img * (int)hw)) * 4u
+                   : kOOB;
         k_end = kend;
     }
     __device__ __forceinline__ void fetch(int k0, int h, float (&v)[4]) const {
+        const __amdgpu_buffer_rsrc_t r = k0 < k_end ? rsrc : rnone;
+        const uint32_t off = vbase + (uint32_t)(k0 + 4 * h) * hw4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int k = k0 + 4 * h + q;
-            v[q] = buf_f32(rsrc, (ok && k < k_end) ? (base + (uint32_t)k * hw) * 4u : kOOB);
-        }
+        for (int q = 0; q < 4; ++q) v[q] = buf_f32(r, off + (uint32_t)q * hw4);
     }
 };
 
@@ -565,6 +571,9 @@ int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w
     // of 4 and W is 16-byte aligned; the B gather then follows W's (c, kh, kw) order.
     const bool pointwise = d->kh == 1 && d->kw == 1 && d->sh == 1 && d->sw == 1 && d->ph == 0 && d->pw == 0 &&
                            d->oh == d->h && d->ow == d->w;
+    // WkPointwise tests the K end once per k block: K a multiple of the block
+    // (every wave's range is a multiple of it); other 1x1 shapes take WkGather<1, 1>.
+    const bool pw_blocks = pointwise && a.K % (ts == 16 ? WkShape<16>::kBlock : WkShape<32>::kBlock) == 0;
     // Raw weights need the B gather in (c, kh, kw) order, whose per-element index
     // arithmetic costs more than the 16-byte A loads save for windows larger than 1x1
     // when the packed layout is tap-ordered (16-channel multiples): there the packed
@@ -594,7 +603,7 @@ int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w
     a.kq = wavek_kq(a.K, kg, ts == 16 ? WkShape<16>::kBlock : WkShape<32>::kBlock);
     if (raw) {
         using RA = WkKContig<true>;
-        if (pointwise) return launch_wk_conv<RA, WkPointwise>(a, ts, kg, grid, st);
+        if (pw_blocks) return launch_wk_conv<RA, WkPointwise>(a, ts, kg, grid, st);
         if (d->kh == 3 && d->kw == 3) return launch_wk_conv<RA, WkGather<3, 3>>(a, ts, kg, grid, st);
         if (d->kh == 7 && d->kw == 7) return launch_wk_conv<RA, WkGather<7, 7>>(a, ts, kg, grid, st);
         if (d->kh == 1 && d->kw == 1) return launch_wk_conv<RA, WkGather<1, 1>>(a, ts, kg, grid, st);
@@ -602,7 +611,7 @@ int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w
     }
     if (tap_k) return launch_wk_conv<WkKContig<true>, WkTap>(a, ts, kg, grid, st);
     if (!packed) return SPINN_HIP_EINVAL;
-    if (pointwise) return launch_wk_conv<WkTContig, WkPointwise>(a, ts, kg, grid, st);
+    if (pw_blocks) return launch_wk_conv<WkTContig, WkPointwise>(a, ts, kg, grid, st);
     if (Cg % kBK == 0) return launch_wk_conv<WkTContig, WkTap>(a, ts, kg, grid, st); // the pack's tap order
     if (d->kh == 3 && d->kw == 3) return launch_wk_conv<WkTContig, WkGather<3, 3>>(a, ts, kg, grid, st);
     if (d->kh == 7 && d->kw == 7) return launch_wk_conv<WkTContig, WkGather<7, 7>>(a, ts, kg, grid, st);
