@@ -563,6 +563,11 @@ int direct_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const
         if (d->kh == 7 && d->sh == 1) return launch_dw<7, 1>(d, x, w, bias, res, y, st);
     }
     if (stem_conv_eligible(d)) {
+        // Measured on YOLOv10n's 3 -> 16 stem at 640x640: 50.1 us against 53.5-55 us at batch 16
+        // (5120 rows), 9.2 against 9.0 us at batch 1 (320 rows: too few workgroups to hide the
+        // staging loads), so the MFMA kernel takes grids of at least 4 rows per CU.
+        if (stem3_mfma_eligible(d) && (int64_t)d->n * d->oh >= 4 * (int64_t)device_cu_count())
+            return stem3_mfma_conv(d, x, w, bias, res, y, st);
         const int64_t total = (int64_t)d->n * ohw;
         dim3 grid((unsigned)std::min<int64_t>((total + 255) / 256, 1 << 16), (unsigned)((d->oc + kStemOcb - 1) / kStemOcb));
         if (d->kh == 3)

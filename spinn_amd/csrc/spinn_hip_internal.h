@@ -114,6 +114,11 @@ bool tiles_forced();
 bool stem_mfma_eligible(const SpinnHipConvDesc *d);
 int stem_mfma_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
                    const float *res, float *y, hipStream_t st);
+// 3x3 stride-2 stems (stem_mfma.hip): C <= 4, OC <= 16, output rows <= 320 pixels, begin
+// pads <= 1, one workgroup per output row on 16x16x4 MFMAs; raw weights W [OC][C][3][3].
+bool stem3_mfma_eligible(const SpinnHipConvDesc *d);
+int stem3_mfma_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias, const float *res,
+                    float *y, hipStream_t st);
 
 // wave-K kernels (wavek.hip): no workspace, packed conv weights as igemm_pack
 int wavek_conv(const SpinnHipConvDesc *d, int ts, const float *x, const float *w, const float *packed, const float *bias,

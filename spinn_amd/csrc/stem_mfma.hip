@@ -140,6 +140,102 @@ __global__ __launch_bounds__(256) void stem7_mfma_kernel(const float *__restrict
         }
 }
 
+
+// ---- 3x3 stride-2 stems on v_mfma_f32_16x16x4f32 ----
+// Up to 4 input channels, up to 16 output channels, output rows of up to 320
+// pixels (YOLOv10n's 3 -> 16 stem at 640x640), begin pads 0 or 1; raw weights
+// W [OC][K], K = C*9 in the reference's (c, kh, kw) im2col order
+// (SPINN/run_time/ops/conv/conv2d.c:58-76). One workgroup computes one output
+// row, all output channels x the row's pixels, from the row's 3 input rows
+// staged in LDS (zero outside the image); staged column iw + pw holds input
+// column iw, so output pixel ow reads columns 2*ow + kw. 16x16x4 MFMA register
+// layout: A lane l = W[oc = l%16][k = 4s + l/16], B lane l = patch[k][pixel l%16],
+// accumulator r of lane l = D[oc = 4*(l/16) + r][pixel l%16]: the 16 output
+// channels fill the tile's rows exactly, where a 32-row MFMA would leave half
+// of them empty. A wave takes every fourth 16-pixel block of the row; its A
+// operands (7 steps for 3 channels) and B offsets stay in registers.
+constexpr int kS3OC = 16;
+constexpr int kS3PX = 320;            // output pixels per row, at most
+constexpr int kS3PW = 2 * kS3PX + 2;  // staged columns per input row
+
+template <int C, bool RES>
+__global__ __launch_bounds__(256) void stem3_mfma_kernel(const float *__restrict__ x, const float *__restrict__ w,
+                                                         const float *__restrict__ bias, const float *__restrict__ res,
+                                                         float *__restrict__ y, SpinnHipConvDesc d) {
+    constexpr int K = C * 9;
+    constexpr int STEPS = (K + 3) / 4;
+    constexpr int PN = C * 3 * kS3PW;
+    constexpr int PIT = (PN + 255) / 256;
+    __shared__ float patch[PN]; // [c][kh][col]
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, j = lane & 15;
+    const int row = blockIdx.x; // img * OH + oh
+    const int img = row / d.oh;
+    const int oh = row - img * d.oh;
+    const int ih0 = 2 * oh - d.ph;
+    // Input rows, every load issued before the first LDS store.
+    const uint32_t img_off = (uint32_t)img * (uint32_t)(C * d.h * d.w);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)d.n * C * d.h * d.w * 4));
+    float pv[PIT];
+#pragma unroll
+    for (int i = 0; i < PIT; ++i) {
+        const int e = tid + i * 256;
+        const int rr = e / kS3PW; // c * 3 + kh
+        const int col = e - rr * kS3PW;
+        const int c = rr / 3, kh = rr - 3 * c;
+        const int ih = ih0 + kh, iw = col - d.pw;
+        const bool ok = e < PN && (unsigned)ih < (unsigned)d.h && (unsigned)iw < (unsigned)d.w;
+        pv[i] = buf_f32(rx, ok ? (img_off + (uint32_t)(c * d.h + ih) * d.w + iw) * 4u : kOOB);
+    }
+    // A operands and B offsets of the K steps: k = 4s + g; past K the weight is 0
+    // and the B offset points at a staged (finite) value
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)(d.oc * K * 4));
+    float a[STEPS];
+    int boff[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+        const int k = 4 * s + g;
+        const bool ok = k < K;
+        a[s] = buf_f32(rw, ok && j < d.oc ? (uint32_t)(j * K + k) * 4u : kOOB);
+        const int c = k / 9, kh = (k - 9 * c) / 3, kw = k - 9 * c - 3 * kh;
+        boff[s] = ok ? (c * 3 + kh) * kS3PW + kw : 0;
+    }
+    float bv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bv[q] = (bias && 4 * g + q < d.oc) ? bias[4 * g + q] : 0.f;
+#pragma unroll
+    for (int i = 0; i < PIT; ++i) {
+        const int e = tid + i * 256;
+        if (e < PN) patch[e] = pv[i];
+    }
+    __syncthreads();
+    const int64_t ohw = (int64_t)d.oh * d.ow;
+    const int nblk = (d.ow + 15) >> 4;
+    for (int pb = wave; pb < nblk; pb += 4) {
+        const int ow = pb * 16 + j;
+        const float *pp = patch + 2 * ow; // ow < 320: columns up to 2*319 + 2 < kS3PW
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], pp[boff[s]], acc, 0, 0, 0);
+        if (ow >= d.ow) continue;
+        const int64_t base = (int64_t)img * d.oc * ohw + (int64_t)oh * d.ow + ow;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = acc[q] + bv[q]; // (acc + bias) + residual, the epilogue's order
+        if constexpr (RES) {
+            float rv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) rv[q] = 4 * g + q < d.oc ? res[base + (int64_t)(4 * g + q) * ohw] : 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] += rv[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (4 * g + q < d.oc) y[base + (int64_t)(4 * g + q) * ohw] = apply_act(v[q], d.act);
+    }
+}
+
 } // namespace
 
 bool stem_mfma_eligible(const SpinnHipConvDesc *d) {
@@ -171,6 +267,36 @@ int stem_mfma_conv(const SpinnHipConvDesc *d, const float *x, const float *packe
         }
     }
     return check_launch();
+}
+
+template <int C>
+static int launch_stem3(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias,
+                        const float *res, float *y, hipStream_t st) {
+    const dim3 grid((unsigned)(d->n * d->oh));
+    if (res)
+        hipLaunchKernelGGL((stem3_mfma_kernel<C, true>), grid, dim3(256), 0, st, x, w, bias, res, y, *d);
+    else
+        hipLaunchKernelGGL((stem3_mfma_kernel<C, false>), grid, dim3(256), 0, st, x, w, bias, res, y, *d);
+    return check_launch();
+}
+
+bool stem3_mfma_eligible(const SpinnHipConvDesc *d) {
+    return d->group == 1 && d->c >= 1 && d->c <= 4 && d->kh == 3 && d->kw == 3 && d->sh == 2 && d->sw == 2 &&
+           d->ph >= 0 && d->ph <= 1 && d->pw >= 0 && d->pw <= 1 && d->oc >= 1 && d->oc <= kS3OC && d->ow >= 1 &&
+           d->ow <= kS3PX && d->oh >= 1 && (int64_t)d->n * d->oh <= INT32_MAX &&
+           (int64_t)d->n * d->c * d->h * d->w * 4 <= (int64_t)kMaxOperandBytes;
+}
+
+// w: the raw weights W [OC][C][3][3].
+int stem3_mfma_conv(const SpinnHipConvDesc *d, const float *x, const float *w, const float *bias, const float *res,
+                    float *y, hipStream_t st) {
+    if (!stem3_mfma_eligible(d)) return SPINN_HIP_EUNSUPPORTED;
+    switch (d->c) {
+    case 1: return launch_stem3<1>(d, x, w, bias, res, y, st);
+    case 2: return launch_stem3<2>(d, x, w, bias, res, y, st);
+    case 3: return launch_stem3<3>(d, x, w, bias, res, y, st);
+    default: return launch_stem3<4>(d, x, w, bias, res, y, st);
+    }
 }
 
 } // namespace spinn

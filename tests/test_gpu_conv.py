@@ -44,6 +44,14 @@ CASES = [
     ("stem7x7_c2_res_ragged", 24, 2, 48, 90, 48, 7, 2, 3, 1, 5, 0),    # 576 rows of 45 pixels, 48 channels
     ("stem7x7_c1_oc40_silu", 34, 1, 64, 64, 40, 7, 2, 3, 1, 3, 0),     # 1088 rows of 32 pixels, SiLU
     ("stem_c1_direct_oc20_res", 1, 1, 33, 35, 20, 3, 1, 1, 1, 5, 3),  # partial 16-channel chunk, residual
+    # 3x3 stride-2 stems on the row-per-workgroup 16x16x4 MFMA kernel (rows <= 320 pixels,
+    # grids of at least 4 rows per CU: 1024 rows on 256 CUs)
+    ("stem3_mfma_640_b4", 4, 3, 640, 640, 16, 3, 2, 1, 1, 3, 3),      # YOLOv10n stem shape, 320-pixel rows
+    ("stem3_mfma_c1_oc5_res", 64, 1, 33, 47, 5, 3, 2, 1, 1, 5, 3),    # one channel, 5 of 16 rows, residual
+    ("stem3_mfma_c4_pad0", 56, 4, 40, 66, 16, 3, 2, 0, 1, 1, 3),      # four channels, no padding
+    ("stem3_mfma_c2_oc12_odd", 96, 2, 21, 29, 12, 3, 2, 1, 1, 0, 3),  # two channels, 11 x 15 outputs
+    ("stem3_fma_640_b1", 1, 3, 640, 640, 16, 3, 2, 1, 1, 3, 3),       # 320 rows: the FMA stem kernel
+    ("stem3_fma_ow321_fallback", 1, 3, 8, 642, 16, 3, 2, 1, 1, 3, 3), # 321-pixel rows: the FMA stem kernel
     ("direct_group1_general", 1, 6, 10, 12, 5, 3, 1, 1, 1, 1, 3),      # C > 4: general direct kernel
     ("conv3x3_s2", 2, 128, 28, 28, 128, 3, 2, 1, 1, 1, 0),
     ("ragged_silu_c3", 1, 3, 17, 19, 83, 3, 1, 1, 1, 3, 0),
