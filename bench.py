@@ -861,6 +861,58 @@ def trace_summary(path: Path, passes: int) -> str:
     return "\n".join(out)
 
 
+def roofline_trace_summary(trace: Path, pass_json: Path) -> str:
+    """Markdown comparison of a rocprofv3 --kernel-trace CSV of `bench.py --roofline-pass`
+    with the per-shape times that run printed (its JSON line in `pass_json`): per layer
+    shape, the mean kernel time per spinn_hip_conv call over every call the trace holds
+    (the warm-up call, the unmeasured first replay and both timed runs: 122 calls; a
+    split-K call's reduction launch included) beside the pass's own figure (the better
+    of its two timed runs), then the count-weighted mean per launch, which is what the
+    bench line's `launch_us` is. A shape's calls lie between its weight packing
+    (`conv_pack_*`) and the next shape's."""
+    import csv
+    line = json.loads(pass_json.read_text().strip().splitlines()[-1])
+    with open(trace) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    segs, cur, in_pack = [], None, False
+    for r in rows:
+        name = _kernel_label(r["Kernel_Name"])
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if name.startswith("conv_pack_"):
+            if not in_pack:
+                cur = {"main": None, "calls": 0, "us": 0.0}
+                segs.append(cur)
+            in_pack = True
+            continue
+        in_pack = False
+        if cur is None or not name.startswith(("conv_igemm", "conv_splitk_reduce", "stem7_mfma")):
+            continue
+        base = name.split("<")[0]
+        if cur["main"] is None:
+            cur["main"] = base
+        if base == cur["main"]:
+            cur["calls"] += 1
+        cur["us"] += us
+    shapes = line["shapes"]
+    if len(segs) != len(shapes):
+        raise SystemExit(f"{len(segs)} packed segments in the trace against {len(shapes)} shapes in the pass")
+    out = ["| layer (C,H,W -> OC, k/s, act) | x | kernel | calls traced | rocprof us / call | bench.py us / launch | diff |",
+           "|---|---|---|---|---|---|---|"]
+    wt = wb = n = 0.0
+    for sh, sg in zip(shapes, segs):
+        t = sg["us"] / max(sg["calls"], 1)
+        out.append(f"| {sh['layer']} | {sh['count']} | {sg['main']} | {sg['calls']} | {t:.2f} | {sh['us']:.2f} | "
+                   f"{100 * (t - sh['us']) / sh['us']:+.1f} % |")
+        wt += t * sh["count"]
+        wb += sh["us"] * sh["count"]
+        n += sh["count"]
+    out += ["", f"Count-weighted mean per launch over {int(n)} layers: rocprof {wt / n:.2f} us, bench.py "
+                f"{wb / n:.2f} us (`launch_us` {line['launch_us']}), {100 * (wt - wb) / wb:+.1f} %; "
+                f"{line['gflop_per_launch']:.3f} GFLOP per launch -> rocprof {line['gflop_per_launch'] / (wt / n) * 1e3:.1f} "
+                f"TFLOP/s, bench.py {line['achieved']} TFLOP/s."]
+    return "\n".join(out)
+
+
 def pmc_summary(d: Path) -> str:
     """Per-dispatch averages of the rocprofv3 --pmc counter CSVs under `d`
     (every *_counter_collection.csv), for the spinn kernels, plus derived ratios."""
@@ -1132,6 +1184,13 @@ def main() -> int:
                     help="only run the known-size fill/copy kernels that scale the HBM byte counters")
     ap.add_argument("--traffic-summary", metavar="DIR",
                     help="reduce rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE CSVs in DIR to the traffic file (no GPU)")
+    ap.add_argument("--roofline-pass", action="store_true",
+                    help="only the live implicit-GEMM launches behind `roofline` at batch B (what a kernel "
+                         "profiler wraps to check its average launch duration), printed as one JSON line")
+    ap.add_argument("--roofline-trace", metavar="CSV",
+                    help="compare a rocprofv3 kernel trace of --roofline-pass with that run's JSON line "
+                         "(--roofline-json; no GPU)")
+    ap.add_argument("--roofline-json", metavar="FILE", help="the --roofline-pass output, for --roofline-trace")
     ap.add_argument("--trace-summary", metavar="CSV",
                     help="print markdown tables of a rocprofv3 kernel-trace CSV (no GPU)")
     ap.add_argument("--passes", type=int, default=1, help="passes in the traced run, for --trace-summary")
@@ -1165,6 +1224,9 @@ def main() -> int:
         return 0
     if a.trace_summary:
         print(trace_summary(Path(a.trace_summary), a.passes))
+        return 0
+    if a.roofline_trace:
+        print(roofline_trace_summary(Path(a.roofline_trace), Path(a.roofline_json)))
         return 0
     if a.pmc_summary:
         print(pmc_summary(Path(a.pmc_summary)))
@@ -1213,6 +1275,20 @@ def main() -> int:
     L = N.lib()
     N.check(L.spinn_hip_init(0), "spinn_hip_init")
 
+    if a.roofline_pass:
+        rows = [r for r in conv_table(gB) if algo_of(N, r, policy) == N.ALGO_IMPLICIT_GEMM]
+        live = conv_layers_live(N, rows, lambda r: algo_of(N, r, policy))
+        ms = sum(e["ms"] * e["count"] for e in live)
+        fl = sum(e["flops"] * e["count"] for e in live)
+        n = sum(e["count"] for e in live)
+        tf = fl / (ms * 1e-3) / 1e12
+        lab = lambda r: f"{r['c']},{r['h']},{r['w']} -> {r['oc']}, {r['kh']}x{r['kw']}/s{r['sh']}, {r['act']}"  # noqa: E731
+        print(json.dumps({"roofline_pass": True, "batch": a.batch, "layers": n, "launch_us": round(ms / n * 1e3, 2),
+                          "gflop_per_launch": fl / n / 1e9, "achieved": round(tf, 3),
+                          "frac": round(tf * 1e12 / PEAK_FP32_MFMA, 4),
+                          "shapes": [{"layer": lab(e["row"]), "count": e["count"], "us": round(e["ms"] * 1e3, 3),
+                                      "split": e["split"]} for e in live]}))
+        return 0
     if a.profile_pass and a.profile_model == "yolov10n":
         gy, xy = models.yolov10n(batch=a.batch, seed=0, postprocess=True)
         py = gy.write(tmp / f"y10_b{a.batch}.ennf")

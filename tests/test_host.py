@@ -283,6 +283,45 @@ def test_bench_traffic_summary_scaling(tmp_path, monkeypatch):
     assert s["traffic_bytes_per_launch"] == 200 * 1024 * 2 + 20 * 1024
 
 
+def test_bench_roofline_trace_summary(tmp_path):
+    """The roofline-pass trace reduction: a shape's calls start after its weight packing,
+    a split-K call's reduction launch counts into that call, other kernels are ignored,
+    and the per-launch mean is weighted by each shape's layer count."""
+    import json
+    import sys
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    rows, t = [], 0
+
+    def k(name, us):
+        nonlocal t
+        rows.append((name, t, t + int(us * 1000)))
+        t += int(us * 1000) + 500
+
+    k("void spinn::fill_random_kernel(float*, unsigned long)", 3.0)  # before any shape: ignored
+    k("void spinn::conv_pack_wt_kernel(float const*, float*)", 2.0)
+    k("void spinn::conv_pack_kcopy_kernel(float const*, float*)", 1.0)
+    for _ in range(4):  # shape 1: split-K, 10 + 2 us per call
+        k("void spinn::conv_igemm_kernel<64, 64, 16, spinn::Im2colTapLoader<64, 16>, true, 0>(spinn::ConvKArgs)", 10.0)
+        k("void spinn::conv_splitk_reduce_kernel(float const*, int)", 2.0)
+    k("void spinn::conv_pack_wt_kernel(float const*, float*)", 2.0)
+    for _ in range(4):  # shape 2: one kernel of 30 us per call
+        k("void spinn::conv_igemm_sk_kernel<64, 64, 16, spinn::Pointwise1x1Loader<64, 16>, 1, 1>(spinn::ConvKArgs, "
+          "spinn::SkSched)", 30.0)
+    k("void spinn::xcc_id_kernel(unsigned int*)", 4.0)  # ignored
+    lines = ["Kernel_Name,Start_Timestamp,End_Timestamp"] + [f'"{n}",{a},{b}' for n, a, b in rows]
+    (tmp_path / "trace.csv").write_text("\n".join(lines) + "\n")
+    (tmp_path / "pass.json").write_text(json.dumps({
+        "launch_us": 26.0, "gflop_per_launch": 2.6, "achieved": 100.0,
+        "shapes": [{"layer": "a", "count": 1, "us": 12.0}, {"layer": "b", "count": 3, "us": 30.0}]}) + "\n")
+    md = bench.roofline_trace_summary(tmp_path / "trace.csv", tmp_path / "pass.json")
+    assert "| a | 1 | conv_igemm_kernel | 4 | 12.00 | 12.00 | +0.0 % |" in md
+    assert "| b | 3 | conv_igemm_sk_kernel | 4 | 30.00 | 30.00 | +0.0 % |" in md
+    # (12 * 1 + 30 * 3) / 4 = 25.5 us; 2.6 GFLOP / 25.5 us = 102.0 TFLOP/s
+    assert "rocprof 25.50 us, bench.py 25.50 us" in md and "rocprof 102.0 TFLOP/s" in md
+
+
 def _hdr_fields(data):
     """(entry table offset, graph meta offset, tensor meta offset) of an ENNF image."""
     f = E._HDR.unpack_from(data, 0)
