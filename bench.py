@@ -30,8 +30,8 @@ every call, then replays the node loop from a HIP graph). Prints ONE JSON line:
                     reference's own runtime as shipped when built; ResNet-101
                     batch 1, a bounded sample
 
-Per-layer GFLOP/s and % of peak go to gpurun_out/bench_layers.json (per node,
-from events) and gpurun_out/bench_layers.md (per distinct layer shape, from
+Per-layer GFLOP/s and % of peak go to the --layers-out JSON file (per node,
+from events) and the Markdown file beside it (per distinct layer shape, from
 back-to-back launches, with Winograd's executed FLOPs).
 """
 from __future__ import annotations
@@ -1204,8 +1204,9 @@ def main() -> int:
                     help="time 1x1 convs at batch 32 over K to split fixed cost from the K loop's rate")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported "
-              "(the path shards by batch with no collective; see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py: measures one GPU; --gpus {a.gpus} is not supported (the conv path would "
+              "shard by batch, each GPU running the whole model on its images with no collective)",
+              file=sys.stderr)
         return 2
     if a.clock_summary:
         print(clock_summary(Path(a.clock_summary)), end="")

@@ -1,7 +1,7 @@
 /*
  * oracle.h - ORACLE (test infrastructure only): CPU restatement of the
  * reference's conv / GEMM path and a CPU runner for ENNF models. Used by the
- * tests as the parity checker and by bench.py as the timed CPU baseline;
+ * tests as the parity reference and by bench.py as the timed CPU baseline;
  * never linked into the product library.
  */
 #ifndef SPINN_ORACLE_H

@@ -3,7 +3,7 @@
 built, to the reference's own CPU runtime (_ref/libspinn_ref.so).
 
 Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use
-this module, and only as the checker / the timed CPU baseline.
+this module, and only as the parity reference / the timed CPU baseline.
 """
 from __future__ import annotations
 

@@ -2,7 +2,7 @@
  * spinn_cpu.c - ORACLE (test infrastructure only; never linked into the product).
  *
  * A CPU restatement of the reference's conv / GEMM hot path, used by the tests
- * as the parity checker and by bench.py as the timed CPU baseline. Each
+ * as the parity reference and by bench.py as the timed CPU baseline. Each
  * function names the reference code it follows; the arithmetic order is the
  * reference's (per output: one fused multiply-add chain over K in im2col row
  * order, K blocked by 256, N by 128, 6x16 register tiles), so results agree
