@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int row8 = 4 * hsel + rr;
     const int ohw = g.OH * g.OW;
     for (int g4 = 0; g4 < 4; ++g4) {
-        if (g4) __syncthreads(); // the previous round's reads are done
+        if (g4) __syncthreads(); // the previous pass's reads are done
 #pragma unroll
         for (int j = 0; j < kWfUnits; ++j)
 #pragma unroll
