@@ -141,7 +141,7 @@ int spinn_hip_maxpool2d(const SpinnHipPoolDesc *d, const float *x, float *y, voi
 int spinn_hip_reduce_mean(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y,
                           void *stream);
 
-/* Device-to-device copy for Reshape / Flatten / Identity
+/* Device-to-device copy (regions must not overlap) for Reshape / Flatten / Identity
  * (SPINN/run_time/ops/shape/reshape.c:6-14, SPINN/run_time/ops/tensor/flatten.c:3-8). */
 int spinn_hip_copy(void *dst, const void *src, size_t bytes, void *stream);
 

@@ -241,3 +241,32 @@ def test_bad_arguments(hip, torch_gpu):
     assert L.spinn_hip_block_copy(blocks, 17, 1, None) == hip.SPINN_HIP_EINVAL
     assert L.spinn_hip_resize_nearest(1, 0, 4, 4, 4, p, p, None) == hip.SPINN_HIP_EINVAL
     torch_gpu.cuda.synchronize()
+
+
+@pytest.mark.parametrize("nbytes,src_off,dst_off", [
+    (16, 0, 0),
+    (59_000_000, 0, 0),           # a detector-head Reshape at batch 16
+    (4 * 4096 * 4097, 0, 0),
+    (4 * 1000 + 8, 0, 0),         # not a multiple of 16 bytes
+    (4 * 1000, 4, 8),             # misaligned ends
+    (4 * 1000, 16, 32),           # aligned offsets inside the buffers
+])
+def test_device_copy(hip, torch_gpu, nbytes, src_off, dst_off):
+    """spinn_hip_copy (Reshape / Flatten / Identity, the resident runs' input restore)
+    copies exactly `nbytes` bytes at any size and alignment and leaves the bytes
+    around the destination run untouched."""
+    print(f"[tensor-op] copy bytes={nbytes} src_off={src_off} dst_off={dst_off}", flush=True)
+    L = hip.lib()
+    n = (nbytes + src_off + 64) // 4 + 16
+    rng = np.random.default_rng(nbytes % 1000 + src_off)
+    src_h = rng.integers(0, 2**31, n, dtype=np.int64).astype(np.int32)
+    src = torch_gpu.from_numpy(src_h).cuda()
+    dst = torch_gpu.full(((nbytes + dst_off + 64) // 4 + 16,), -7, dtype=torch_gpu.int32, device="cuda")
+    hip.check(L.spinn_hip_copy(C.c_void_p(dst.data_ptr() + dst_off), C.c_void_p(src.data_ptr() + src_off),
+                               C.c_size_t(nbytes), None), "spinn_hip_copy")
+    torch_gpu.cuda.synchronize()
+    got = dst.cpu().numpy().view(np.uint8)
+    want = np.full(got.shape, 0, np.uint8)
+    want[:] = np.frombuffer(np.full(got.size // 4, -7, np.int32).tobytes(), np.uint8)
+    want[dst_off:dst_off + nbytes] = src_h.view(np.uint8)[src_off:src_off + nbytes]
+    np.testing.assert_array_equal(got, want)
