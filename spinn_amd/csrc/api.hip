@@ -33,31 +33,45 @@ static int env_winograd() {
 }
 
 static int env_winograd_tile() {
-    // SPINN_WINOGRAD_TILE=2|4 picks the Winograd tile under AUTO; unset = F(4,3).
+    // SPINN_WINOGRAD_TILE=2|4 fixes the Winograd tile under AUTO; unset = per-shape choice.
     static int v = [] {
         const char *e = std::getenv("SPINN_WINOGRAD_TILE");
-        return (e && e[0] == '2') ? 2 : 4;
+        if (!e || !*e) return 0;
+        return e[0] == '2' ? 2 : 4;
     }();
     return v;
 }
 
-static bool winograd_pays(const SpinnHipConvDesc *d, int m) {
-    // Winograd moves V and M through memory in three launches. F(2,3) cuts GEMM flops
-    // 2.25x with V / M 4x the input / output; measured on MI355X it wins from 128
-    // channels in and out once there are >= 256 2x2 output tiles (1.6x at 128@28x28
-    // batch 32). F(4,3) cuts flops 4x with V / M 2.25x the input / output and wins from
-    // 128 channels with >= 128 4x4 tiles (512@7x7 batch 32: 45 against 50 us for F(2,3)),
-    // and at 64 channels with >= 256 tiles (64@56x56 batch 32: 72 against 92 us for the
-    // implicit GEMM; at batch 1, 196 tiles, it loses).
-    if (m == 4) {
-        // the one-launch form (winograd_fused.hip) where it applies: few channels, many tiles
-        if (wino4_fused_selected(d)) return true;
-        const int64_t tiles = (int64_t)d->n * ((d->oh + 3) / 4) * ((d->ow + 3) / 4);
-        const bool wide = d->c >= 128 && d->oc >= 128;
-        return d->c >= 64 && d->oc >= 64 && tiles >= (wide ? 128 : 256);
+// AUTO's Winograd tile for an eligible 3x3 stride-1 conv: 4 (F(4,3)), 2 (F(2,3)) or
+// 0 (stay on the implicit GEMM). Winograd cuts the GEMM flops 4x (F(4,3)) or 2.25x
+// (F(2,3)) but moves V and M through memory in three launches, and its packed
+// weights are 4x (F(4,3)) or 1.8x (F(2,3)) the raw ones. At small batch a layer's
+// time is mostly its weight read, and a model's weights together compete for the
+// 256 MB Infinity Cache: 22 ResNet-101 layers at 256@14x14 hold 207 MB as F(4,3)
+// against 52 MB raw, which slows the 1x1 layers beside them too. Thresholds from
+// whole-model graph replays and per-node times on MI355X (ResNet-101 at batch 1-32,
+// YOLOv10n at 1, 4 and 16), with per-layer timings (weights cycled through copies
+// larger than the cache) between them:
+//  * 128+ channels in and out: at K >= 512 F(2,3) from 16 4x4 tiles (512@7x7
+//    batch 8: 22.0 against 32.5 us for the implicit GEMM, the model step 17 us
+//    faster) and F(4,3) from 48; at K = 256 F(4,3) from 64 tiles (256@14x14 batch 4:
+//    21.1 against 23.9 us per node in the model; at 32 tiles, batch 2, 18.0 against
+//    16.9); at K = 128 F(4,3) from 128 tiles.
+//  * 64+ channels: F(4,3) from 256 tiles when 128+ channels come in (128->64@40x40
+//    batch 4: 20.8 against 23.3 us), from 512 at 64 channels in (64@56x56 batch 2,
+//    392 tiles: 15.0 against 12.3 us on the implicit GEMM; batch 4, 784 tiles: 20.2
+//    against 21.7).
+//  * fewer channels: the one-launch F(4,3) where it applies (many tiles), else the
+//    implicit GEMM.
+static int winograd_tile_for(const SpinnHipConvDesc *d) {
+    if (wino4_fused_selected(d)) return 4;
+    const int64_t t4 = (int64_t)d->n * ((d->oh + 3) / 4) * ((d->ow + 3) / 4);
+    if (d->c >= 128 && d->oc >= 128) {
+        if (d->c >= 512) return t4 < 16 ? 0 : (t4 < 48 ? 2 : 4);
+        return t4 >= (d->c >= 256 ? 64 : 128) ? 4 : 0;
     }
-    const int64_t tiles = (int64_t)d->n * ((d->oh + 1) / 2) * ((d->ow + 1) / 2);
-    return d->c >= 128 && d->oc >= 128 && tiles >= 256;
+    if (d->c >= 64 && d->oc >= 64) return t4 >= (d->c >= 128 ? 256 : 512) ? 4 : 0;
+    return 0;
 }
 
 static int select_algo(const SpinnHipConvDesc *d) {
@@ -68,9 +82,11 @@ static int select_algo(const SpinnHipConvDesc *d) {
     if (stem_conv_pays(d)) return SPINN_CONV_ALGO_DIRECT;
     if (winograd_eligible(d)) {
         const int w = env_winograd();
-        const int m = env_winograd_tile();
-        if (w == 1 || (w < 0 && winograd_pays(d, m)))
-            return m == 4 ? SPINN_CONV_ALGO_WINOGRAD_F43 : SPINN_CONV_ALGO_WINOGRAD;
+        const int fixed = env_winograd_tile();
+        int m = w == 0 ? 0 : winograd_tile_for(d);
+        if (w == 1 && m == 0) m = 4;
+        if (m && fixed) m = fixed;
+        if (m) return m == 4 ? SPINN_CONV_ALGO_WINOGRAD_F43 : SPINN_CONV_ALGO_WINOGRAD;
     }
     return SPINN_CONV_ALGO_IMPLICIT_GEMM;
 }

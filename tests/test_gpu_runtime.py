@@ -68,10 +68,11 @@ def test_resnet101_b1(hip, tmp_path):
     assert_parity(y, ref, what="resnet101 b1", scale_by_ref=True)
 
 
-def test_resnet101_b4_winograd_f43(hip, tmp_path):
-    """Batch 4: AUTO runs the 3x3 stride-1 convs of stages 1 and 2 (64@56x56, 128@28x28) as
-    Winograd F(4x4,3x3); the 101-layer result stays within the bound of the oracle's
-    direct (im2col) convolution."""
+def test_resnet101_b4_winograd_f43_and_f23(hip, tmp_path):
+    """Batch 4: AUTO runs the 3x3 stride-1 convs of stages 1-3 (64@56x56, 128@28x28,
+    256@14x14) as Winograd F(4x4,3x3) and stage 4's (512@7x7, 16 4x4 tiles) as
+    F(2x2,3x3); the 101-layer result stays within the bound of the oracle's direct
+    (im2col) convolution."""
     g, x = models.resnet101(batch=4, seed=2)
     algos = []
     L = N.lib()
@@ -83,7 +84,7 @@ def test_resnet101_b4_winograd_f43(hip, tmp_path):
         d = N.ConvDesc(n, c, h, w, oc, oh, ow, kh, kw, p["strides"][0], p["strides"][1], p["pads"][0], p["pads"][1],
                        p["group"] or 1, p["act"], 0, 0)
         algos.append(L.spinn_hip_conv_select_algo(C.byref(d)))
-    assert algos.count(N.ALGO_WINOGRAD_F43) == 6
+    assert algos.count(N.ALGO_WINOGRAD_F43) == 28 and algos.count(N.ALGO_WINOGRAD) == 2
     y, y2, ref = _run_both(tmp_path, g, x, "r101b4")
     print(f"[r101 b4] |ref|max={np.abs(ref).max():.3e}", flush=True)
     assert_parity(y, ref, what="resnet101 b4 with F(4x4,3x3)", scale_by_ref=True)

@@ -209,11 +209,21 @@ def test_conv_algo_selection(native):
 
     assert algo(32, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43
     assert algo(32, 128, 28, 28, 128, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43
-    assert algo(1, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM  # 49 output tiles: too few
+    assert algo(1, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM  # 16 4x4 tiles: too few
+    assert algo(2, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM  # 32
+    assert algo(4, 256, 14, 14, 256, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43   # 64
     assert algo(32, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43    # 64 channels, 6272 4x4 tiles
     assert algo(1, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM    # 64 channels, 196 4x4 tiles
+    assert algo(2, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM    # 392: below 512
+    assert algo(4, 64, 56, 56, 64, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43     # 784
     assert algo(32, 512, 7, 7, 512, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43    # 128 4x4 tiles
+    assert algo(1, 512, 7, 7, 512, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM    # 4
+    assert algo(4, 512, 7, 7, 512, 3, 1, 1, 1) == native.ALGO_WINOGRAD         # 16 tiles at K = 512: F(2,3)
+    assert algo(8, 512, 7, 7, 512, 3, 1, 1, 1) == native.ALGO_WINOGRAD         # 32
+    assert algo(12, 512, 7, 7, 512, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43    # 48
     assert algo(1, 128, 28, 28, 128, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM  # 49 4x4 tiles
+    assert algo(4, 256, 20, 20, 64, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM   # 64 out: 100 tiles
+    assert algo(16, 256, 20, 20, 64, 3, 1, 1, 1) == native.ALGO_WINOGRAD_F43   # 400 tiles
     assert algo(8, 32, 80, 80, 32, 3, 1, 1, 1) == native.ALGO_IMPLICIT_GEMM    # 32 channels
     assert algo(1, 256, 14, 14, 256, 3, 2, 1, 1) == native.ALGO_IMPLICIT_GEMM
     assert algo(1, 128, 20, 20, 128, 3, 2, 1, 128) == native.ALGO_DIRECT
