@@ -511,7 +511,7 @@ static int igemm_wavek(const SpinnHipConvDesc *d) {
     const bool pointwise = d->kh == 1 && d->kw == 1 && d->sh == 1 && d->sw == 1 && d->ph == 0 && d->pw == 0 &&
                            d->oh == d->h && d->ow == d->w;
     return wavek_tile(d->oc / d->group, d->n * d->oh * d->ow, (d->c / d->group) * d->kh * d->kw, d->group,
-                      pointwise);
+                      pointwise ? kWkConvPointwise : kWkConvGather);
 }
 
 static bool igemm_stem(const SpinnHipConvDesc *d) { return stem_mfma_eligible(d) && !tiles_forced(); }

@@ -253,7 +253,7 @@ bool gemm_is_gemv(const SpinnHipGemmDesc *d) {
 } // namespace
 
 static int gemm_wavek(const SpinnHipGemmDesc *d) {
-    return wavek_tile(d->m, d->n, d->k, d->batch > 0 ? d->batch : 1, false);
+    return wavek_tile(d->m, d->n, d->k, d->batch > 0 ? d->batch : 1, kWkGemm);
 }
 
 size_t gemm_workspace_bytes(const SpinnHipGemmDesc *d) {

@@ -104,8 +104,9 @@ void probe_xcd_local(int device);
 bool xcd_local_parts();
 // Output tile edge of the wave-K kernel (K split over a workgroup's waves) for
 // an (M x N x K) problem repeated `reps` times: 32 or 16, or 0 when it runs on the
-// 64/128-wide tiles of choose_tiles. `pointwise`: a 1x1 stride-1 unpadded conv.
-int wavek_tile(int M, int N, int K, int reps, bool pointwise);
+// 64/128-wide tiles of choose_tiles. `kind`: what the operands are.
+enum WkKind { kWkGemm, kWkConvGather, kWkConvPointwise }; // pointwise: 1x1 stride-1 unpadded conv
+int wavek_tile(int M, int N, int K, int reps, WkKind kind);
 // true while spinn_hip_tune_force_tiles holds a tile shape or a K split
 bool tiles_forced();
 

@@ -32,20 +32,33 @@ static int env_wavek() {
     return v;
 }
 
-int wavek_tile(int M, int N, int K, int reps, bool pointwise) {
+int wavek_tile(int M, int N, int K, int reps, WkKind kind) {
     if (g_force_bm) return (g_force_bm == g_force_bn && (g_force_bm == 32 || g_force_bm == 16)) ? g_force_bm : 0;
     const int e = env_wavek();
     if (e >= 0) return e == 1 ? 32 : 0;
     const int cus = device_cu_count();
     const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * reps;
     if (tiles64 >= cus) return 0;
-    // Measured on MI355X (ResNet-101 and YOLOv10n at batch 1, the Gemm sweep).
+    // Measured on MI355X (ResNet-101 and YOLOv10n at batch 1, the Gemm sweep; the
+    // batch-1 conv layers with their weights cycled through copies larger than the
+    // Infinity Cache, as inside a model).
     // 16 x 16 tiles: 1x1 convs whose 32 x 32 grid covers at most half the CUs with
     // K of 256..1024 (the 1024 -> 256 layers at 14x14: 8.1 -> 5.8 us, split-K's
-    // reduction launch gone). Their B loads are one float per k and lane, so a
-    // 3x3 gather or a longer K stays on 32-wide or split-K tiles.
+    // reduction launch gone), and 1x1 convs with K of 64..128 over at most ~1.6
+    // 32 x 32 tiles per CU (YOLOv10n 128@20x20: 3.9 -> 2.8 us, 128 -> 512@28x28 of
+    // ResNet-101: 5.4 -> 4.6 us; with more tiles, 64 -> 256@56x56, the 64-wide tiles
+    // keep 4.7 against 5.8 us). Gathered (3x3) convs with K of 576..1152 over at most
+    // ~0.8 16 x 16 tiles per CU: 128@20x20 10.2 -> 6.9 us against split K, 64@20x20
+    // 7.9 -> 6.0 us against 32 x 32 tiles; over more tiles (64@40x40, 400) the 32 x 32
+    // tiles keep 7.5 against 8.8 us, and a longer gather (256 -> 64@20x20, K = 2304)
+    // keeps split K (10.4 against 12.0).
     const int64_t tiles32 = (int64_t)((M + 31) / 32) * ((N + 31) / 32) * reps;
-    if (pointwise && tiles32 <= cus / 2 && K >= 256 && K <= 1024) return 16;
+    const int64_t tiles16 = (int64_t)((M + 15) / 16) * ((N + 15) / 16) * reps;
+    if (kind == kWkConvPointwise) {
+        if (tiles32 <= cus / 2 && K >= 256 && K <= 1024) return 16;
+        if (16 * tiles32 <= 25 * (int64_t)cus && K >= 64 && K <= 128) return 16;
+    }
+    if (kind == kWkConvGather && 32 * tiles16 <= 25 * (int64_t)cus && K >= 576 && K <= 1152) return 16;
     // 32 x 32 tiles where 64 x 64 tiles underfill the chip and K is 128..576
     // (one to a few 32-deep chunks per wave); with longer K its one-float-per-lane
     // operand loads cost more than the 64 x 64 tiles' split-K reduction launch,

@@ -231,6 +231,18 @@ def test_conv_algo_selection(native):
     assert algo(32, 3, 224, 224, 64, 7, 2, 3, 1) == native.ALGO_IMPLICIT_GEMM   # ResNet stem: matrix cores
     assert algo(1, 6, 8, 8, 4, 3, 1, 1, 4) == native.SPINN_HIP_EINVAL  # C % group != 0
 
+    def workspace(*a):
+        n, c, h, w, oc, k, s, p, g = a
+        oh = (h + 2 * p - k) // s + 1
+        d = native.ConvDesc(n, c, h, w, oc, oh, oh, k, k, s, s, p, p, g, 0, native.ALGO_IMPLICIT_GEMM, 0)
+        return L.spinn_hip_conv_workspace_size(C.byref(d))
+
+    # batch-1 grids under 256 CUs: the wave-K kernel needs no workspace, split K does
+    assert workspace(1, 128, 20, 20, 128, 3, 1, 1, 1) == 0       # K 1152 over 200 16x16 tiles: wave-K
+    assert workspace(1, 256, 20, 20, 64, 3, 1, 1, 1) > 0         # K 2304: split K
+    assert workspace(1, 256, 14, 14, 256, 3, 1, 1, 1) > 0        # 208 16x16 tiles: split K
+    assert workspace(1, 128, 20, 20, 256, 1, 1, 0, 1) == 0       # 1x1, K 128: wave-K
+
 
 def _declared_functions():
     names = set()
