@@ -175,6 +175,44 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(const float *__r
     }
 }
 
+// inner == 1, rows of at most 64 * NPL floats: one wave per row, held in
+// registers. The reference's three passes (SPINN/run_time/ops/activation/softmax.c:
+// max; exp(x - max) and their sum; scale by 1 / sum) on one read of the row and
+// one exp per element; lane j holds elements j, j + 64, ... (YOLOv10n's batch-16
+// attention, 12800 rows of 400: 8.8 us, 4.6 TB/s, against 18.1 us for the running
+// (max, sum) form above, which takes two exps per element and reads the row twice).
+template <int NPL>
+__global__ __launch_bounds__(kThreads) void softmax_rows_reg_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                                    int64_t rows, int dim) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wave = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6;
+    const int64_t nwaves = ((int64_t)gridDim.x * kThreads) >> 6;
+    for (int64_t r = wave; r < rows; r += nwaves) {
+        const float *xp = x + r * dim;
+        float *yp = y + r * dim;
+        float v[NPL];
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) v[i] = lane + 64 * i < dim ? xp[lane + 64 * i] : -INFINITY;
+        float m = v[0];
+#pragma unroll
+        for (int i = 1; i < NPL; ++i) m = fmaxf(m, v[i]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            v[i] = lane + 64 * i < dim ? expf(v[i] - m) : 0.f;
+            s += v[i];
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+        const float inv = 1.0f / (s == 0.f ? 1e-10f : s); // SPINN/run_time/ops/activation/softmax.c:94
+#pragma unroll
+        for (int i = 0; i < NPL; ++i)
+            if (lane + 64 * i < dim) yp[lane + 64 * i] = v[i] * inv;
+    }
+}
+
 // inner > 1: one thread per (outer, inner) column, consecutive threads on inner.
 __global__ __launch_bounds__(kThreads) void softmax_cols_kernel(const float *__restrict__ x, float *__restrict__ y,
                                                                 int64_t outer, int64_t dim, int64_t inner) {
@@ -189,6 +227,42 @@ __global__ __launch_bounds__(kThreads) void softmax_cols_kernel(const float *__r
         const float sum = acc.s == 0.f ? 1e-10f : acc.s;
         const float inv = 1.0f / sum;
         for (int64_t j = 0; j < dim; ++j) yp[j * inner] = expf(xp[j * inner] - acc.m) * inv;
+    }
+}
+
+// inner > 1, at most ND elements per column: one thread per (outer, inner)
+// column, consecutive threads on inner, the column held in registers: the
+// reference's three passes on one read and one exp per element. (Four adjacent
+// columns per thread as float4 ran slower: 17.0 against 14.6 us for YOLOv10n's
+// batch-16 DFL softmax, a quarter of the waves in flight.)
+template <int ND>
+__global__ __launch_bounds__(kThreads) void softmax_cols_reg_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                                    int64_t outer, int dim, int64_t inner) {
+    const int64_t total = outer * inner;
+    for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < total; e += (int64_t)gridDim.x * kThreads) {
+        const int64_t o = e / inner;
+        const int64_t k = e - o * inner;
+        const float *xp = x + o * dim * inner + k;
+        float *yp = y + o * dim * inner + k;
+        float v[ND];
+#pragma unroll
+        for (int j = 0; j < ND; ++j)
+            if (j < dim) v[j] = xp[j * inner];
+        float m = v[0];
+#pragma unroll
+        for (int j = 1; j < ND; ++j)
+            if (j < dim) m = fmaxf(m, v[j]);
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < ND; ++j)
+            if (j < dim) {
+                v[j] = expf(v[j] - m);
+                s += v[j];
+            }
+        const float inv = 1.0f / (s == 0.f ? 1e-10f : s); // SPINN/run_time/ops/activation/softmax.c:94
+#pragma unroll
+        for (int j = 0; j < ND; ++j)
+            if (j < dim) yp[j * inner] = v[j] * inv;
     }
 }
 
@@ -356,6 +430,25 @@ __global__ __launch_bounds__(kThreads) void resize_nearest_kernel(const float *_
     }
 }
 
+// Exact 2x upsampling (oh = 2h, ow = 2w, w even): the reference's index rule
+// (h_in = h_out * h / oh, SPINN/run_time/ops/tensor/resize.c) is h_out / 2, so
+// input element (r, j) fills the 2x2 output block at (2r, 2j). Each thread reads
+// one float2 of an input row once and writes one float4 into each of the two
+// output rows; input rows are flattened over all planes (plane p's row i is flat
+// row p * h + i, whose output rows are flat rows 2 (p * h + i) and the next).
+// 32-bit indices: the launcher checks that the output's float4 count fits.
+__global__ __launch_bounds__(kThreads) void resize2x_kernel(const float2 *__restrict__ x, float4 *__restrict__ y,
+                                                            uint32_t pairs, uint32_t w2) {
+    for (uint32_t e = blockIdx.x * kThreads + threadIdx.x; e < pairs; e += gridDim.x * kThreads) {
+        const uint32_t r = e / w2;
+        const uint32_t c = e - r * w2;
+        const float2 v = x[e];
+        const float4 o = make_float4(v.x, v.x, v.y, v.y);
+        y[2 * r * w2 + c] = o;
+        y[2 * r * w2 + w2 + c] = o;
+    }
+}
+
 template <int OP>
 int launch_binary(const float *a, uint32_t na, const float *b, uint32_t nb, float *y, uint32_t n, hipStream_t st) {
     const bool vec = n % 4 == 0 && na % 4 == 0 && nb % 4 == 0 && aligned16(a) && aligned16(b) && aligned16(y);
@@ -417,8 +510,25 @@ int batchnorm(int64_t n, int64_t c, int64_t spatial, const float *x, const float
 
 int softmax(int64_t outer, int64_t dim, int64_t inner, const float *x, float *y, hipStream_t st) {
     if (outer * inner == 0 || dim == 0) return 0;
-    if (inner == 1)
-        hipLaunchKernelGGL(softmax_rows_kernel, dim3(grid_1d(outer * 64)), dim3(kThreads), 0, st, x, y, outer, dim);
+    const dim3 rgrid(grid_1d(outer * 64));
+    if (inner == 1 && dim <= 64)
+        hipLaunchKernelGGL(softmax_rows_reg_kernel<1>, rgrid, dim3(kThreads), 0, st, x, y, outer, (int)dim);
+    else if (inner == 1 && dim <= 128)
+        hipLaunchKernelGGL(softmax_rows_reg_kernel<2>, rgrid, dim3(kThreads), 0, st, x, y, outer, (int)dim);
+    else if (inner == 1 && dim <= 256)
+        hipLaunchKernelGGL(softmax_rows_reg_kernel<4>, rgrid, dim3(kThreads), 0, st, x, y, outer, (int)dim);
+    else if (inner == 1 && dim <= 512)
+        hipLaunchKernelGGL(softmax_rows_reg_kernel<8>, rgrid, dim3(kThreads), 0, st, x, y, outer, (int)dim);
+    else if (inner == 1 && dim <= 1024)
+        hipLaunchKernelGGL(softmax_rows_reg_kernel<16>, rgrid, dim3(kThreads), 0, st, x, y, outer, (int)dim);
+    else if (inner == 1)
+        hipLaunchKernelGGL(softmax_rows_kernel, rgrid, dim3(kThreads), 0, st, x, y, outer, dim);
+    else if (dim <= 16)
+        hipLaunchKernelGGL(softmax_cols_reg_kernel<16>, dim3(grid_1d(outer * inner)), dim3(kThreads), 0, st, x, y,
+                           outer, (int)dim, inner);
+    else if (dim <= 32)
+        hipLaunchKernelGGL(softmax_cols_reg_kernel<32>, dim3(grid_1d(outer * inner)), dim3(kThreads), 0, st, x, y,
+                           outer, (int)dim, inner);
     else
         hipLaunchKernelGGL(softmax_cols_kernel, dim3(grid_1d(outer * inner)), dim3(kThreads), 0, st, x, y, outer,
                            dim, inner);
@@ -524,6 +634,16 @@ int transpose(int ndim, const int64_t *dims, const int32_t *perm, const float *x
 int resize_nearest(int64_t nc, int h, int w, int oh, int ow, const float *x, float *y, hipStream_t st) {
     const int64_t total = nc * oh * ow;
     if (total == 0) return 0;
+    if (oh == 2 * h && ow == 2 * w && w % 2 == 0 && total / 4 <= (int64_t)UINT32_MAX && ((uintptr_t)x & 7u) == 0 &&
+        aligned16(y)) {
+        // 2x nearest (the detector's FPN upsampling): 16 x 128 x 40 x 40 -> 80 x 80 in 11.2 us (5.8 TB/s)
+        // against 20.2 us for the general kernel, whose per-element 64-bit divisions bound it
+        const int64_t pairs = nc * h * (w / 2);
+        hipLaunchKernelGGL(resize2x_kernel, dim3(grid_1d(pairs)), dim3(kThreads), 0, st,
+                           reinterpret_cast<const float2 *>(x), reinterpret_cast<float4 *>(y), (uint32_t)pairs,
+                           (uint32_t)(w / 2));
+        return check_launch();
+    }
     if (ow % 4 == 0 && aligned16(y))
         hipLaunchKernelGGL(resize_nearest_kernel<true>, dim3(grid_1d(total / 4)), dim3(kThreads), 0, st, x, y, nc, h,
                            w, oh, ow);

@@ -179,9 +179,9 @@ def run_transpose(N, torch, x, perm):
     return _done(torch, yd)
 
 
-def run_resize(N, torch, x, oh, ow):
+def run_resize(N, torch, x, oh, ow, offset=0):
     n, c, h, w = x.shape
-    xd = _in(torch, x)
+    xd = _in(torch, x, offset)
     yd = _out(torch, (n, c, oh, ow))
     N.check(N.lib().spinn_hip_resize_nearest(n * c, h, w, oh, ow, _p(xd), _p(yd), None), "spinn_hip_resize_nearest")
     return _done(torch, yd)

@@ -108,7 +108,17 @@ def test_unary_and_batchnorm(hip, torch_gpu, offset):
     ((7, 37), -1),                # dim < wave size
     ((16, 16, 4, 8400), 1),       # DFL: softmax over 16 bins, inner 33600
     ((2, 3, 5), 0),               # outer 1
-], ids=["attn", "long", "dim1", "short", "dfl", "outer1"])
+    ((9, 64), -1),                # one value per lane
+    ((9, 65), -1),                # two per lane, the second in lane 0 only
+    ((6, 200), -1),               # four per lane, partial
+    ((4, 1024), -1),              # sixteen per lane: the register form's longest row
+    ((3, 1025), -1),              # one past it: the running (max, sum) form
+    ((3, 32, 4, 10), 1),          # columns of 32
+    ((2, 33, 12), 1),             # columns of 33: the running form
+    ((4, 5, 7), 1),               # columns of 5, inner 7: one column per thread
+    ((2, 16, 6, 2), 1),           # columns of 16, inner 12
+], ids=["attn", "long", "dim1", "short", "dfl", "outer1", "dim64", "dim65", "dim200", "dim1024", "dim1025",
+        "cols32", "cols33", "cols5", "cols16"])
 def test_softmax(hip, torch_gpu, shape, axis):
     print(f"[tensor-op] softmax {shape} axis {axis}", flush=True)
     rng = np.random.default_rng(len(shape) * 100 + shape[-1])
@@ -157,11 +167,14 @@ def test_transpose(hip, torch_gpu, shape, perm):
 
 def test_resize_and_sppf_pool(hip, torch_gpu):
     rng = np.random.default_rng(41)
-    for shape, oh, ow in (((1, 256, 20, 20), 40, 40), ((16, 128, 40, 40), 80, 80), ((2, 3, 5, 3), 7, 8),
-                          ((1, 2, 6, 6), 3, 4)):
-        print(f"[tensor-op] resize {shape} -> {oh}x{ow}", flush=True)
+    # exact 2x (the two-per-thread form, then odd width and a misaligned input: the general form),
+    # other scales
+    for shape, oh, ow, off in (((1, 256, 20, 20), 40, 40, 0), ((16, 128, 40, 40), 80, 80, 0),
+                               ((3, 5, 7, 10), 14, 20, 0), ((2, 3, 4, 5), 8, 10, 0), ((2, 3, 4, 6), 8, 12, 1),
+                               ((2, 3, 5, 3), 7, 8, 0), ((1, 2, 6, 6), 3, 4, 0)):
+        print(f"[tensor-op] resize {shape} -> {oh}x{ow} offset {off}", flush=True)
         x = rng.uniform(-1, 1, shape).astype(np.float32)
-        np.testing.assert_array_equal(run_resize(hip, torch_gpu, x, oh, ow), O.resize_nearest(x, oh, ow))
+        np.testing.assert_array_equal(run_resize(hip, torch_gpu, x, oh, ow, off), O.resize_nearest(x, oh, ow))
     x = rng.uniform(-1, 1, (16, 128, 20, 20)).astype(np.float32)
     print("[tensor-op] maxpool 5x5 s1 p2", flush=True)
     np.testing.assert_array_equal(run_maxpool(hip, torch_gpu, x, 20, 20, 5, 5, 1, 1, 2, 2),
