@@ -52,6 +52,12 @@ CASES = [
     ("stem3_mfma_c2_oc12_odd", 96, 2, 21, 29, 12, 3, 2, 1, 1, 0, 3),  # two channels, 11 x 15 outputs
     ("stem3_fma_640_b1", 1, 3, 640, 640, 16, 3, 2, 1, 1, 3, 3),       # 320 rows: the FMA stem kernel
     ("stem3_fma_ow321_fallback", 1, 3, 8, 642, 16, 3, 2, 1, 1, 3, 3), # 321-pixel rows: the FMA stem kernel
+    # AUTO's small-grid choices: 16 x 16 wave-K tiles for a 3x3 gather with K 1152 over 200 tiles and for
+    # 1x1 convs with K 64 / 128; F(2x2,3x3) for 512 channels over 16 4x4 tiles
+    ("auto_wavek16_3x3_k1152", 1, 128, 20, 20, 128, 3, 1, 1, 1, 3, 0),
+    ("auto_wavek16_1x1_k64", 1, 64, 40, 40, 64, 1, 1, 0, 1, 3, 0),
+    ("auto_wavek16_1x1_k128_add", 1, 128, 20, 20, 128, 1, 1, 0, 1, 4, 0),
+    ("auto_f23_c512_b4", 4, 512, 7, 7, 512, 3, 1, 1, 1, 1, 0),
     ("direct_group1_general", 1, 6, 10, 12, 5, 3, 1, 1, 1, 1, 3),      # C > 4: general direct kernel
     ("conv3x3_s2", 2, 128, 28, 28, 128, 3, 2, 1, 1, 1, 0),
     ("ragged_silu_c3", 1, 3, 17, 19, 83, 3, 1, 1, 1, 3, 0),
