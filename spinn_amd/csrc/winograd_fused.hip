@@ -156,23 +156,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
 
-    float d[6][3];
+    // Patches are loaded two K slices ahead (register buffers pa / pb in turn): slice s
+    // computes from V slice s % 2 while slice s + 1's patches, issued during slice s - 1,
+    // are transformed and slice s + 2's are loaded. With fewer workgroups than CUs each
+    // workgroup's slices form one chain, and a one-slice distance left every slice
+    // waiting out a memory round trip.
+    float pa[6][3], pb[6][3];
     float uv[kUPer];
-    load_half(0, d);
+    load_half(0, pa);
     load_u(0, uv);
-    columns(d);
+    if (S > 1) load_half(1, pb);
+    columns(pa);
     __syncthreads();
     rows(vs0);
     store_u(uv);
     __syncthreads();
-    for (int s = 0; s < S; ++s) {
+    // dn: slice s + 1's patches (loaded); df: consumed, receives slice s + 2's
+    auto slice = [&](int s, const float (&dn)[6][3], float (&df)[6][3]) {
         const float *cur = (s & 1) ? vs1 : vs0;
         float *nxt = (s & 1) ? vs0 : vs1;
         const bool more = s + 1 < S;
-        if (more) { // in flight during this slice's MFMAs
-            load_half(s + 1, d);
-            load_u(s + 1, uv);
-        }
+        if (more) load_u(s + 1, uv); // in flight during this slice's MFMAs
+        if (s + 2 < S) load_half(s + 2, df);
 #pragma unroll
         for (int q = 0; q < kWfCs / 2; ++q) {
             const int brow = (2 * q + h) * kWfT + l32;
@@ -186,14 +191,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int j = 0; j < kWfUnits; ++j)
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[j], bv[j], acc[j], 0, 0, 0);
         }
-        if (more) columns(d);
+        if (more) columns(dn);
         __syncthreads(); // exchange area complete; every wave is past this slice's MFMAs
         if (more) {
             rows(nxt);
             store_u(uv);
         }
         __syncthreads(); // next V and U slices complete, exchange area free
+    };
+    int s = 0;
+    for (; s + 1 < S; s += 2) {
+        slice(s, pb, pa);
+        slice(s + 1, pa, pb);
     }
+    if (s < S) slice(s, pb, pa);
 
     // ---- output transform: 4 rounds of 8 of the 32 output channels ----
     // Staged layout [position][r % 4][lane half][32 tiles] over both V slices: the two
