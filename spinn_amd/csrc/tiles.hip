@@ -57,12 +57,20 @@ int wavek_tile(int M, int N, int K, int reps, WkKind kind) {
     if (kind == kWkConvPointwise) {
         if (tiles32 <= cus / 2 && K >= 256 && K <= 1024) return 16;
         if (16 * tiles32 <= 25 * (int64_t)cus && K >= 64 && K <= 128) return 16;
+        // 32 x 32 tiles for 1x1 convs with K of 577..1152 over at most ~0.43 64 x 64
+        // tiles per CU, where the 64 x 64 grid would split K 8 ways (ResNet-101's
+        // 1024 -> 256@14x14 at batch 4: 13.3 -> 10.0 us, batch 8: 20.1 -> 15.6 us)
+        if (K > 576 && K <= 1152 && 7 * tiles64 <= 3 * (int64_t)cus) return 32;
     }
     if (kind == kWkConvGather && 32 * tiles16 <= 25 * (int64_t)cus && K >= 576 && K <= 1152) return 16;
     // 32 x 32 tiles where 64 x 64 tiles underfill the chip and K is 128..576
     // (one to a few 32-deep chunks per wave); with longer K its one-float-per-lane
     // operand loads cost more than the 64 x 64 tiles' split-K reduction launch,
-    // and below 128 it saves nothing.
+    // and below 128 it saves nothing. A conv grid of more than half a 64 x 64 tile
+    // per CU keeps the 64 x 64 tiles, unsplit (choose_tiles): ResNet-101 at batch 4,
+    // 256 -> 1024@14x14 (208 tiles) 10.6 -> 8.4 us, 512 -> 1024@28x28 stride 2
+    // 22.0 -> 15.8 us; YOLOv10n at batch 4, 192 -> 128@40x40 9.8 -> 7.0 us.
+    if (kind != kWkGemm && 2 * tiles64 > cus) return 0;
     return (K >= 128 && K <= 576) ? 32 : 0;
 }
 
@@ -102,10 +110,13 @@ TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
     }
     const int64_t tiles = (int64_t)((M + tc.bm - 1) / tc.bm) * ((N + tc.bn - 1) / tc.bn) * reps;
     if (allow_split &&
-        ((K >= 512 && tiles < cus) || (K >= 1536 && tiles < 2 * cus) || (K >= 256 && 2 * tiles < cus))) {
+        ((K >= 512 && 2 * tiles <= cus) || (K >= 1536 && tiles < 2 * cus) || (K >= 256 && 2 * tiles < cus))) {
         // Split K only when each split still runs >= 128 deep: the partial
-        // sums cost a write and a read of the output per split. A grid of
-        // 1-2 tiles per CU splits only a long K (>= 1536: the 3x3 convs of
+        // sums cost a write and a read of the output per split. A K of 512
+        // or more splits over at most half a tile per CU (a grid of half to
+        // one tile per CU runs faster unsplit: ResNet-101's 1024 -> 512@14x14
+        // at batch 8, 200 tiles, 27.7 -> 21.9 us with its weights cold, as in
+        // a model). A grid of 1-2 tiles per CU splits only a long K (>= 1536: the 3x3 convs of
         // ResNet-101 at batch 32 gain, its 1024-deep 1x1 convs lose); a
         // 256-deep K splits only when the grid covers less than half the
         // CUs (batch-1 1x1 convs). At most 16 splits: measured on the batch-1
