@@ -38,6 +38,12 @@ int wavek_tile(int M, int N, int K, int reps, WkKind kind) {
     if (e >= 0) return e == 1 ? 32 : 0;
     const int cus = device_cu_count();
     const int64_t tiles64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64) * reps;
+    // 1x1 convs with K = 64 into one 64-row tile over 1 to 2 tiles per CU: each
+    // 64 x 64 tile is four K slices of load, prologue and store, and 16 x 16
+    // wave-K tiles stream them instead (64@56x56 at batch 8: 13.7 -> 9.7 us,
+    // YOLOv10n's 64@80x80 at batch 4: 13.1 -> 9.1 us); over more tiles (batch 32,
+    // 1568) the 64 x 64 tiles keep 16.7 against 28.5 us.
+    if (kind == kWkConvPointwise && M <= 64 && K > 48 && K <= 64 && tiles64 < 2 * (int64_t)cus) return 16;
     if (tiles64 >= cus) return 0;
     // Measured on MI355X (ResNet-101 and YOLOv10n at batch 1, the Gemm sweep; the
     // batch-1 conv layers with their weights cycled through copies larger than the
