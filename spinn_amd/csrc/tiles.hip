@@ -44,6 +44,11 @@ int wavek_tile(int M, int N, int K, int reps, WkKind kind) {
     // YOLOv10n's 64@80x80 at batch 4: 13.1 -> 9.1 us); over more tiles (batch 32,
     // 1568) the 64 x 64 tiles keep 16.7 against 28.5 us.
     if (kind == kWkConvPointwise && M <= 64 && K > 48 && K <= 64 && tiles64 < 2 * (int64_t)cus) return 16;
+    // and 1x1 convs with K of 96..192 over one to two tiles per CU: 32 x 32 tiles
+    // (128 -> 512@28x28 at batch 4: 15.1 -> 13.2 us, YOLOv10n's 128 -> 256@20x20 at
+    // batch 16: 15.5 -> 13.3 us; with K = 256 no gain, and below one tile per CU the
+    // unsplit 64 x 64 tiles below win)
+    if (kind == kWkConvPointwise && K >= 96 && K <= 192 && tiles64 >= cus && tiles64 < 2 * (int64_t)cus) return 32;
     if (tiles64 >= cus) return 0;
     // Measured on MI355X (ResNet-101 and YOLOv10n at batch 1, the Gemm sweep; the
     // batch-1 conv layers with their weights cycled through copies larger than the
