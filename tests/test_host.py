@@ -242,6 +242,9 @@ def test_conv_algo_selection(native):
     assert workspace(1, 256, 20, 20, 64, 3, 1, 1, 1) > 0         # K 2304: split K
     assert workspace(1, 256, 14, 14, 256, 3, 1, 1, 1) > 0        # 208 16x16 tiles: split K
     assert workspace(1, 128, 20, 20, 256, 1, 1, 0, 1) == 0       # 1x1, K 128: wave-K
+    assert workspace(4, 1024, 14, 14, 256, 1, 1, 0, 1) == 0      # K 1024 over 52 tiles: wave-K, no split
+    assert workspace(8, 1024, 14, 14, 512, 1, 1, 0, 1) == 0      # 200 tiles: 64 x 64 unsplit
+    assert workspace(8, 2048, 7, 7, 512, 1, 1, 0, 1) > 0         # K 2048 over 56 tiles: split K
 
 
 def _declared_functions():
