@@ -91,6 +91,36 @@ def test_resnet101_b4_winograd_f43_and_f23(hip, tmp_path):
     assert np.array_equal(y, y2)
 
 
+def test_resnet101_b8_small_grid_tiles(hip, tmp_path):
+    """Batch 8: the grids under two tiles per CU take the small-grid tile rules - 16 x 16
+    wave-K tiles for the K = 64 1x1 layer at 56x56, 32 x 32 for the 1024-deep 1x1 layers at
+    14x14, unsplit 64 x 64 tiles for 200-tile grids, F(2x2,3x3) for 512@7x7 - and the graph
+    replays the eager result bit for bit; the 101-layer output stays within the bound of
+    the oracle's direct convolution."""
+    g, x = models.resnet101(batch=8, seed=5)
+    algos = []
+    L = N.lib()
+    for nd in (n for n in g.nodes if n.op == E.OP_CONV):
+        p = E.unpack_conv_params(nd.params)
+        n, c, h, w = g.dims(nd.inputs[0])
+        oc, _, kh, kw = g.dims(nd.inputs[1])
+        _, _, oh, ow = g.dims(nd.outputs[0])
+        d = N.ConvDesc(n, c, h, w, oc, oh, ow, kh, kw, p["strides"][0], p["strides"][1], p["pads"][0], p["pads"][1],
+                       p["group"] or 1, p["act"], 0, 0)
+        algos.append(L.spinn_hip_conv_select_algo(C.byref(d)))
+    assert algos.count(N.ALGO_WINOGRAD) == 2
+    path = g.write(tmp_path / "r101b8.ennf")
+    with Session(path) as s:
+        y = s.run(x)
+    with Session(path, graph=True) as s:
+        replays = [s.run(x) for _ in range(2)]
+    ref = O.Model(path).run(x, g.dims(g.outputs[0]))
+    print(f"[r101 b8] |ref|max={np.abs(ref).max():.3e}", flush=True)
+    assert_parity(y, ref, what="resnet101 b8 (AUTO) vs oracle", scale_by_ref=True)
+    for r in replays:
+        assert np.array_equal(r, y)
+
+
 def test_resnet101_b1_graph_replay(hip, tmp_path):
     g, x = models.resnet101(batch=1, seed=0)
     path = g.write(tmp_path / "r101g.ennf")
