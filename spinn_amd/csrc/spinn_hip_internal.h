@@ -45,10 +45,21 @@ __device__ __forceinline__ float apply_act_c(float v) {
 
 // Sum of the split-K partials ws[s * plane + e] for s = 0..nsplit-1, added in
 // split order starting from 0 (the order the partials' K ranges take). The
-// loads of a group of 8 splits are issued before the first add: a plain loop
-// would wait out one memory round trip per split.
+// loads of a group of 8 splits (all of them, up to 16) are issued before the
+// first add: a plain loop would wait out one memory round trip per split.
 __device__ __forceinline__ float splitk_sum(const float *__restrict__ ws, int nsplit, int64_t plane, int64_t e) {
     float v = 0.f;
+    if (nsplit > 8 && nsplit <= 16) {
+        // 9..16 splits (the tile rule's largest): every split's load in flight at
+        // once, one memory round trip instead of two; the same split-order sum
+        float p[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) p[u] = ws[(int64_t)min(u, nsplit - 1) * plane + e];
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+            if (u < nsplit) v += p[u];
+        return v;
+    }
     for (int s0 = 0; s0 < nsplit; s0 += 8) {
         float p[8];
 #pragma unroll
