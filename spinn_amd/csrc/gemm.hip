@@ -130,46 +130,76 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *__
 
 // Y = alpha * A B^T (+ beta C) for at most MR rows, A [M][K] and B [N][K] both
 // row-major with K contiguous (the Gemm transB=1 layout of fully-connected
-// layers): one wave per output column streams its row of B once, in float4s
+// layers): KS waves per output column stream its row of B once, in float4s
 // when K % 4 == 0 and both bases are 16-byte aligned, against the M rows of A
-// (L2-resident), then sums each row's lane partials with a shuffle tree. The
+// (L2-resident), then sum each row's lane partials with a shuffle tree. The
 // whole launch reads B once from HBM; the MFMA tiles would stage it through
-// LDS for a single row of A.
-template <int MR, bool VEC>
-__global__ __launch_bounds__(256) void gemv_rows_kernel(const float *__restrict__ A, const float *__restrict__ B,
+// LDS for a single row of A. A workgroup serves 4 columns; with KS > 1 each
+// wave of a column takes a contiguous 1/KS of K and the first of them adds the
+// others' sums (through LDS, in part order), so more loads are in flight per
+// column on the same number of workgroups (gemv_k_parts picks KS).
+template <int MR, bool VEC, int KS>
+__global__ __launch_bounds__(1024) void gemv_rows_kernel(const float *__restrict__ A, const float *__restrict__ B,
                                                         const float *__restrict__ Cm, int c_mode, float alpha,
                                                         float beta, float *__restrict__ Y, int M, int N, int K) {
+    static_assert(KS == 1 || KS == 2 || KS == 4, "K parts per column: 1, 2 or 4");
     const int lane = threadIdx.x & 63;
-    const int n = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (n >= N) return; // whole wave
-    const float *bp = B + (int64_t)n * K;
+    const int w = threadIdx.x >> 6;
+    const int n = blockIdx.x * 4 + w / KS;
+    const int kp = w % KS;
+    const bool live = n < N;
+    if constexpr (KS == 1) {
+        if (!live) return; // whole wave; no barrier follows
+    }
+    const float *bp = B + (int64_t)(live ? n : 0) * K;
     float acc[MR];
 #pragma unroll
     for (int m = 0; m < MR; ++m) acc[m] = 0.f;
-    if constexpr (VEC) {
+    if (live) {
+        if constexpr (VEC) {
+            const int k4 = K >> 2;
+            const int beg = (int)((int64_t)kp * k4 / KS), end = (int)((int64_t)(kp + 1) * k4 / KS);
 #pragma unroll 4
-        for (int k = lane * 4; k < K; k += 256) {
-            const f32x4 b = *reinterpret_cast<const f32x4 *>(bp + k);
+            for (int j = beg + lane; j < end; j += 64) {
+                const f32x4 b = *reinterpret_cast<const f32x4 *>(bp + 4 * j);
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                if (m < M) {
-                    const f32x4 av = *reinterpret_cast<const f32x4 *>(A + (int64_t)m * K + k);
-                    acc[m] += av[0] * b[0] + av[1] * b[1] + av[2] * b[2] + av[3] * b[3];
+                for (int m = 0; m < MR; ++m) {
+                    if (m < M) {
+                        const f32x4 av = *reinterpret_cast<const f32x4 *>(A + (int64_t)m * K + 4 * j);
+                        acc[m] += av[0] * b[0] + av[1] * b[1] + av[2] * b[2] + av[3] * b[3];
+                    }
                 }
             }
-        }
-    } else {
-        for (int k = lane; k < K; k += 64) {
-            const float b = bp[k];
+        } else {
+            const int beg = (int)((int64_t)kp * K / KS), end = (int)((int64_t)(kp + 1) * K / KS);
+            for (int k = beg + lane; k < end; k += 64) {
+                const float b = bp[k];
 #pragma unroll
-            for (int m = 0; m < MR; ++m)
-                if (m < M) acc[m] += A[(int64_t)m * K + k] * b;
+                for (int m = 0; m < MR; ++m)
+                    if (m < M) acc[m] += A[(int64_t)m * K + k] * b;
+            }
         }
     }
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+    if constexpr (KS > 1) {
+        __shared__ float red[4 * KS][MR];
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; ++m) red[w][m] = acc[m];
+        }
+        __syncthreads();
+        if (kp != 0 || !live) return;
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            float s = red[w][m];
+#pragma unroll
+            for (int p = 1; p < KS; ++p) s += red[w + p][m];
+            acc[m] = s;
+        }
+    }
     if (lane == 0) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
@@ -250,6 +280,16 @@ bool gemm_is_gemv(const SpinnHipGemmDesc *d) {
     return (d->batch <= 1) && d->m <= 4 && !d->trans_a && d->trans_b;
 }
 
+// Waves per output column in gemv_rows_kernel (graph-replayed on MI355X, weights
+// MALL-resident / after a 512 MiB flush): 1000 x 2048 with one row of A 3.52 /
+// 9.4 us on one wave per column, 3.38 / 8.2 on two, 3.77 / 7.5 on four; with
+// four rows 6.3 / 18.8 on one, 5.0 / 10.6 on four. K = 600 (2.90 against 3.11
+// us on two waves) and 4096 columns (12.9 against 13.3 us) keep one wave.
+int gemv_k_parts(int M, int N, int K) {
+    if (N >= 2048 || K < 1024) return 1;
+    return M == 1 ? 2 : 4;
+}
+
 } // namespace
 
 static int gemm_wavek(const SpinnHipGemmDesc *d) {
@@ -291,13 +331,23 @@ int gemm_run(const SpinnHipGemmDesc *d, const float *A, const float *B, const fl
     const bool vb = aligned16(B) && (a.ldb % 4 == 0) && (batch == 1 || d->stride_b % 4 == 0);
     if (gemm_is_gemv(d)) {
         // fully-connected shape: B streamed once by waves, no tiles, no workspace
+        const int ks = gemv_k_parts(d->m, d->n, d->k);
         const dim3 grid((unsigned)((d->n + 3) / 4));
-        if (va && vb)
-            hipLaunchKernelGGL((gemv_rows_kernel<4, true>), grid, dim3(256), 0, st, A, B, C, a.c_mode, d->alpha,
-                               d->beta, Y, d->m, d->n, d->k);
-        else
-            hipLaunchKernelGGL((gemv_rows_kernel<4, false>), grid, dim3(256), 0, st, A, B, C, a.c_mode, d->alpha,
-                               d->beta, Y, d->m, d->n, d->k);
+        const bool vec = va && vb;
+#define SPINN_GEMV(VEC, KS)                                                                                      \
+    hipLaunchKernelGGL((gemv_rows_kernel<4, VEC, KS>), grid, dim3(256 * KS), 0, st, A, B, C, a.c_mode, d->alpha,   \
+                       d->beta, Y, d->m, d->n, d->k)
+        if (ks == 4) {
+            if (vec) SPINN_GEMV(true, 4);
+            else SPINN_GEMV(false, 4);
+        } else if (ks == 2) {
+            if (vec) SPINN_GEMV(true, 2);
+            else SPINN_GEMV(false, 2);
+        } else {
+            if (vec) SPINN_GEMV(true, 1);
+            else SPINN_GEMV(false, 1);
+        }
+#undef SPINN_GEMV
         return check_launch();
     }
     if (const int ts = gemm_wavek(d)) return wavek_gemm(d, ts, A, B, C, Y, st);

@@ -39,12 +39,14 @@ def test_gemm_transposes_ragged(hip, torch_gpu, ta, tb, cmode, m):
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
-@pytest.mark.parametrize("k", [2048, 2047, 5], ids=["k2048", "k2047_scalar", "k5"])
+@pytest.mark.parametrize("k", [2048, 2047, 600, 5], ids=["k2048", "k2047_scalar", "k600", "k5"])
 @pytest.mark.parametrize("cmode", [0, 1, 2])
 def test_gemm_few_rows_fc(hip, torch_gpu, m, k, cmode):
-    """M <= 4 with transB=1 (fully-connected layers) runs one wave per output column over a
-    row of B; float4 loads when K % 4 == 0, scalar otherwise; alpha, beta and both C forms."""
-    n = 1000
+    """M <= 4 with transB=1 (fully-connected layers) runs waves over the rows of B: one per
+    output column below K = 1024, else two (M = 1) or four (M > 1), each summing its share of
+    K; float4 loads when K % 4 == 0, scalar otherwise; alpha, beta and both C forms; 999
+    columns leave the last workgroup part-filled."""
+    n = 1000 if k == 2048 else 999
     rng = np.random.default_rng(m * 10 + k + cmode)
     a = rng.uniform(-1, 1, (m, k)).astype(np.float32)
     b = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float32)
