@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void reduce_max_short_kernel(const float *__re
 //   1. radix select of the k-th largest order key, 8 bits per pass, LDS histogram;
 //   2. compaction of the k winners: every key above the threshold, and the
 //      lowest-index elements equal to it (block-wide prefix count in index order);
-//   3. bitonic sort of the winners by (key desc, index asc) in LDS.
+//   3. bitonic sort of the winners by (key desc, index asc), in registers and LDS.
 // ---------------------------------------------------------------------------
 constexpr int kTopkThreads = 1024;
 
@@ -94,6 +94,8 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 }
 
 constexpr int kTopkWaves = kTopkThreads / 64;
+constexpr int kTopkWaveSlots = 128; // sampled-threshold candidates one wave may hold
+static_assert(kTopkThreads == SPINN_HIP_TOPK_MAX_K, "the sort holds one candidate per thread");
 constexpr int kTopkBins = 257; // per-wave histograms, padded so equal bins of two waves sit in different banks
 
 // Radix-select state shared by the workgroup.
@@ -163,52 +165,59 @@ __device__ __forceinline__ void topk_pick_digit(TopkSel &sh, int shift, uint32_t
     __syncthreads();
 }
 
-// Bitonic sort of cand[0, k) descending over the next power of two >= k (pads
-// sort last), then the row's values and indices in that order. A compare-exchange
-// stage with stride < 128 keeps every pair inside one 128-element block, which
-// one wave owns (64 pairs, one per lane): those stages need only the wave's own
-// ordering of its LDS accesses. Block-wide barriers surround only the stages of
-// stride >= 128 (5 of the 45 stages for k = 300).
-__device__ __forceinline__ void bitonic_pair(uint64_t *cand, int t, int stride, int size) {
-    const int i = ((t & ~(stride - 1)) << 1) | (t & (stride - 1)); // pair t: i has the stride bit clear
-    const int j = i + stride;
-    const bool desc = (i & size) == 0;
-    const uint64_t a = cand[i], b = cand[j];
-    if (desc ? (a < b) : (a > b)) {
-        cand[i] = b;
-        cand[j] = a;
+// Bitonic network over P2 elements, descending, thread t holding element t in
+// registers: a compare-exchange stage of stride < 64 pairs lanes of one wave
+// (a shuffle), one of stride >= 64 goes through LDS (10 of the 55 stages for
+// 1024), alternating between the two 1024-entry buffers xa and xb so that each
+// needs one barrier (a buffer is rewritten only after the barrier of the next
+// exchange, which every thread reaches after its read). Fully unrolled: no loop
+// or branch between stages. Callers may still read xa / xb until the first
+// exchange's leading barrier.
+template <int P2>
+__device__ __forceinline__ uint64_t bitonic_regs(uint64_t x, uint64_t *xa, uint64_t *xb, int tid) {
+    int ex = 0; // LDS exchanges so far
+#pragma unroll
+    for (int size = 2; size <= P2; size <<= 1) {
+        const bool desc = (tid & size) == 0;
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            uint64_t y;
+            if (stride >= 64) {
+                uint64_t *buf = (ex & 1) ? xb : xa;
+                if (ex == 0) __syncthreads(); // the callers' reads of xa / xb are done
+                buf[tid] = x;
+                __syncthreads();
+                y = buf[tid ^ stride];
+                ++ex;
+            } else {
+                y = __shfl_xor(x, stride, 64);
+            }
+            const bool hi = ((tid & stride) == 0) == desc; // keep the larger one
+            x = hi ? (x > y ? x : y) : (x < y ? x : y);
+        }
     }
+    return x;
 }
 
-__device__ __forceinline__ void topk_sort_store(uint64_t *cand, int k, int tid, const float *xr, float *values,
-                                                int64_t *indices) {
-    int p2 = 1;
-    while (p2 < k) p2 <<= 1;
-    for (int i = k + tid; i < p2; i += kTopkThreads) cand[i] = 0ull;
-    __syncthreads();
-    const int lane = tid & 63, wave = tid >> 6;
-    const bool in_wave = wave * 128 < p2 && 2 * lane < p2; // this lane's pair of its wave's block exists
-    for (int size = 2; size <= p2; size <<= 1) {
-        int stride = size >> 1;
-        if (stride >= 128) {
-            for (; stride >= 128; stride >>= 1) {
-                __syncthreads();
-                if (2 * tid < p2) bitonic_pair(cand, tid, stride, size);
-            }
-            __syncthreads();
-        }
-        for (; stride > 0; stride >>= 1) {
-            if (in_wave) bitonic_pair(cand, wave * 64 + lane, stride, size);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        }
-    }
-    __syncthreads();
-    for (int j = tid; j < k; j += kTopkThreads) {
-        const uint32_t i = 0xffffffffu - (uint32_t)cand[j];
-        values[(int64_t)blockIdx.x * k + j] = xr[i];
-        indices[(int64_t)blockIdx.x * k + j] = (int64_t)i;
+// Sort count (<= 1024) elements descending, pads (0) last, then write the first
+// k in that order as the row's values and indices. `x` is this thread's element
+// (0 past count); xa and xb are the exchange buffers. The value is rebuilt from the
+// order key except for zeros (whose sign the key drops) and NaNs, which are read
+// back from the row.
+__device__ __forceinline__ void topk_sort_store(uint64_t *xa, uint64_t *xb, uint64_t x, int count, int k, int tid,
+                                                const float *xr, float *values, int64_t *indices) {
+    if (count <= 64) x = bitonic_regs<64>(x, xa, xb, tid); // uniform branches
+    else if (count <= 128) x = bitonic_regs<128>(x, xa, xb, tid);
+    else if (count <= 256) x = bitonic_regs<256>(x, xa, xb, tid);
+    else if (count <= 512) x = bitonic_regs<512>(x, xa, xb, tid);
+    else x = bitonic_regs<1024>(x, xa, xb, tid);
+    if (tid < k) {
+        const uint32_t key = (uint32_t)(x >> 32);
+        const uint32_t i = 0xffffffffu - (uint32_t)x;
+        const uint32_t u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
+        const float v = (key == 0x80000000u || key == 0u) ? xr[i] : __uint_as_float(u);
+        values[(int64_t)blockIdx.x * k + tid] = v;
+        indices[(int64_t)blockIdx.x * k + tid] = (int64_t)i;
     }
 }
 
@@ -217,6 +226,20 @@ __device__ __forceinline__ void topk_sort_store(uint64_t *cand, int k, int tid, 
 // registers. The threshold-equal elements are ranked in index order from
 // per-(chunk, wave) counts with three barriers, instead of one block-wide count
 // per chunk. Same keys, threshold and sort as topk_rows_kernel: identical output.
+//
+// Rows of at least 4096 elements with k <= 512 first try a sampled threshold:
+// the q-th largest of 1024 keys spread over the row's full chunks (thread t
+// samples element (t mod chunks) * 1024 + t), with q = e + 3 sqrt(e) + 2 for
+// e = k * 1024 / n the sample's expected count above the k-th largest key, is
+// bounded from below by the same radix select over one key per thread, three
+// digits deep (T: that key with its low 8 bits cleared). When between k and
+// 1024 keys of the row are >= T, they hold the row's top k (every key above
+// the k-th largest one is >= T, and at least k keys are), so they alone are
+// sorted: one pass of compares over the row writes each wave's candidates to
+// its own 128 slots in index order, instead of four histogram passes and the
+// threshold ranking. Otherwise (ties around T, or a sample that misjudged the
+// row, or more than 128 candidates in one wave) the full selection below runs.
+// Either way the output is the unique top k by (key desc, index asc).
 template <int R>
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_reg_kernel(const float *__restrict__ x, int n, int k,
                                                                      float *__restrict__ values,
@@ -225,6 +248,8 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_reg_kernel(const float
     __shared__ uint32_t ceq[R][kTopkWaves]; // threshold-equal elements per (chunk, wave)
     __shared__ uint32_t cbase[R];           // ... in the chunks before this one
     __shared__ uint64_t cand[SPINN_HIP_TOPK_MAX_K];
+    __shared__ uint64_t wcand[kTopkWaves * kTopkWaveSlots]; // sampled-threshold candidates, per wave
+    __shared__ uint32_t wcount[kTopkWaves];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -234,6 +259,58 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_reg_kernel(const float
     for (int u = 0; u < R; ++u) {
         const int i = u * kTopkThreads + tid;
         key[u] = i < n ? order_key(xr[i]) : 0u;
+    }
+    if (n >= 4 * kTopkThreads && k <= 512) { // uniform
+        const int chunks = n / kTopkThreads;
+        const uint32_t skey = order_key(xr[(tid % chunks) * kTopkThreads + tid]);
+        const float e = (float)k * (float)kTopkThreads / (float)n;
+        const uint32_t q = min((uint32_t)kTopkThreads, (uint32_t)ceilf(e + 3.f * sqrtf(e)) + 2u);
+        if (tid == 0) {
+            sh.prefix = 0u;
+            sh.mask = 0u;
+            sh.need = q;
+            sh.gt = 0u;
+        }
+        for (int shift = 24; shift >= 8; shift -= 8) {
+            for (int b = tid; b < kTopkWaves * kTopkBins; b += kTopkThreads) sh.whist[b] = 0u;
+            __syncthreads();
+            const uint32_t prefix = sh.prefix, mask = sh.mask;
+            topk_count((skey & mask) == prefix, (skey >> shift) & 255u, lane, sh.whist + wave * kTopkBins);
+            __syncthreads();
+            topk_pick_digit(sh, shift, prefix, mask, tid, lane, wave);
+        }
+        const uint32_t T = sh.prefix; // the q-th largest sample key with its low 8 bits cleared
+        // this wave's keys >= T into its own slots, in index order
+        uint64_t *const wc = wcand + wave * kTopkWaveSlots;
+        uint32_t c = 0u;
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+            const int i = u * kTopkThreads + tid;
+            const bool take = i < n && key[u] >= T;
+            const uint64_t tb = __ballot(take);
+            const uint32_t pos = c + (uint32_t)__popcll(tb & ((1ull << lane) - 1ull));
+            if (take && pos < (uint32_t)kTopkWaveSlots)
+                wc[pos] = ((uint64_t)key[u] << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+            c += (uint32_t)__popcll(tb);
+        }
+        if (lane == 0) wcount[wave] = c;
+        __syncthreads();
+        // element tid of the waves' slots concatenated in wave order
+        uint32_t total = 0u;
+        int src = -1;
+        bool fits = true;
+#pragma unroll
+        for (int w = 0; w < kTopkWaves; ++w) {
+            const uint32_t cw = wcount[w];
+            if ((uint32_t)tid >= total && (uint32_t)tid < total + cw) src = w * kTopkWaveSlots + (tid - (int)total);
+            total += cw;
+            fits = fits && cw <= (uint32_t)kTopkWaveSlots;
+        }
+        if (fits && total >= (uint32_t)k && total <= (uint32_t)SPINN_HIP_TOPK_MAX_K) { // uniform
+            topk_sort_store(cand, wcand, src >= 0 ? wcand[src] : 0ull, (int)total, k, tid, xr, values, indices);
+            return;
+        }
+        __syncthreads(); // every thread has read wcount before the full selection reuses the state
     }
     if (tid == 0) {
         sh.prefix = 0u;
@@ -289,7 +366,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_reg_kernel(const float
         }
     }
     __syncthreads();
-    topk_sort_store(cand, k, tid, xr, values, indices);
+    topk_sort_store(cand, wcand, tid < k ? cand[tid] : 0ull, k, k, tid, xr, values, indices);
 }
 
 __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__restrict__ x, int64_t n, int k,
@@ -297,6 +374,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
                                                                  int64_t *__restrict__ indices) {
     __shared__ TopkSel sh;
     __shared__ uint64_t cand[SPINN_HIP_TOPK_MAX_K];
+    __shared__ uint64_t xb[SPINN_HIP_TOPK_MAX_K]; // the sort's second exchange buffer
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -380,7 +458,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_rows_kernel(const float *__
     __syncthreads();
 
     // 3. bitonic sort, descending, and the output
-    topk_sort_store(cand, k, tid, xr, values, indices);
+    topk_sort_store(cand, xb, tid < k ? cand[tid] : 0ull, k, k, tid, xr, values, indices);
 }
 
 // ---------------------------------------------------------------------------

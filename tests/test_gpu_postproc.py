@@ -108,6 +108,47 @@ def test_topk_detector_sizes(hip, torch_gpu, rows, n, k, grid):
     np.testing.assert_array_equal(got_v.view(np.uint32), ref_v.view(np.uint32))
 
 
+def _sampled_positions(n):
+    """The elements the register TopK kernels sample for their threshold: thread t of 1024
+    reads element (t mod chunks) * 1024 + t, chunks = n // 1024."""
+    t = np.arange(1024)
+    return (t % (n // 1024)) * 1024 + t
+
+
+@pytest.mark.parametrize("rows,n,k,layout", [
+    (16, 8400, 300, "uniform"), (2, 24000, 300, "uniform"), (1, 24000, 300, "sigmoid"),
+    (1, 24000, 300, "descending"), (1, 24000, 300, "ascending"), (1, 24000, 300, "top_at_samples"),
+    (1, 4096, 512, "uniform"), (2, 32768, 1, "uniform"), (1, 5000, 300, "sigmoid"),
+    (1, 8192, 300, "top_off_samples")])
+def test_topk_sampled_threshold(hip, torch_gpu, rows, n, k, layout):
+    """Continuous values, where the register kernels take the sampled threshold (one count
+    pass, then only the keys >= the sample's q-th largest are sorted), and layouts that defeat
+    the sample: the row's largest values exactly at the sampled elements (too few keys pass,
+    so the full selection runs) or everywhere else; sorted rows; k = 1 and k = 512."""
+    print(f"[topk] sampled rows={rows} n={n} k={k} {layout}", flush=True)
+    rng = np.random.default_rng(n + k + len(layout))
+    if layout == "sigmoid":
+        x = 1.0 / (1.0 + np.exp(-rng.normal(-6.0, 2.0, (rows, n))))
+    elif layout in ("descending", "ascending"):
+        x = np.sort(rng.uniform(0, 1, (rows, n)), axis=1)
+        if layout == "descending":
+            x = x[:, ::-1]
+    else:
+        x = rng.uniform(-1, 1, (rows, n))
+        s = _sampled_positions(n)
+        if layout == "top_at_samples":
+            x[:, s] += 10.0
+        elif layout == "top_off_samples":
+            x += 10.0
+            x[:, s] -= 10.0
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ref_v, ref_i = O.topk(x, k)
+    got_v, got_i = device_postproc(hip, torch_gpu, "topk", [x, np.array([k], np.int64)], b"",
+                                   [(rows, k), (rows, k)], [np.float32, np.int64])
+    np.testing.assert_array_equal(got_i, ref_i)
+    np.testing.assert_array_equal(got_v.view(np.uint32), ref_v.view(np.uint32))
+
+
 def test_reduce_gather_tile_detector_sizes(hip, torch_gpu):
     rng = np.random.default_rng(3)
     scores = np.round(rng.uniform(0, 1, (16, 8400, 80)), 3).astype(np.float32)
