@@ -186,6 +186,56 @@ static int dispatch_node(SpinnContext *ctx, uint32_t i) {
                              node->num_outputs);
 }
 
+/* Reshape, Flatten, Identity and Unsqueeze copy their input unless the two
+ * tensors share device bytes (op_copy_alias). The planner (the reference's,
+ * whose offsets are kept) gives such an output a region of its own; when no
+ * node writes into the input's bytes from this node until the output's last
+ * reader, the output reads those bytes in place instead: its device address
+ * becomes the input's and the node launches nothing. Graph outputs keep their
+ * own region. A node's outputs count as written even when the node is itself
+ * an aliased view (conservative: it may only forgo an alias). */
+static int view_op(uint16_t op) {
+    return op == ENNF_OP_Reshape || op == ENNF_OP_Flatten || op == ENNF_OP_Identity || op == ENNF_OP_Unsqueeze;
+}
+
+static int bytes_overlap(const uint8_t *a, uint32_t an, const uint8_t *b, uint32_t bn) {
+    return a < b + bn && b < a + an;
+}
+
+static void alias_views(SpinnContext *ctx) {
+    const uint32_t nt = ctx->num_tensors, nn = ctx->num_nodes;
+    int64_t *last = (int64_t *)malloc((size_t)(nt ? nt : 1) * sizeof(int64_t));
+    if (!last) return; /* every view keeps its copy */
+    for (uint32_t t = 0; t < nt; t++) last[t] = -1;
+    for (uint32_t i = 0; i < nn; i++)
+        for (int j = 0; j < ctx->nodes[i].num_inputs; j++)
+            if (ctx->nodes[i].input_ids[j] < nt) last[ctx->nodes[i].input_ids[j]] = i;
+    for (uint32_t o = 0; o < ctx->header.num_outputs && o < 16; o++)
+        if (ctx->output_ids[o] < nt) last[ctx->output_ids[o]] = INT64_MAX;
+    for (uint32_t k = 0; k < nn; k++) {
+        const SpinnNode *nd = &ctx->nodes[k];
+        if (!view_op(nd->op_type) || nd->num_inputs < 1 || nd->num_outputs != 1) continue;
+        if (nd->input_ids[0] >= nt || nd->output_ids[0] >= nt) continue;
+        SpinnTensor *I = &ctx->tensors[nd->input_ids[0]];
+        SpinnTensor *O = &ctx->tensors[nd->output_ids[0]];
+        if (I->is_weight || O->is_weight || !I->data || !O->data || I->size == 0 || I->size != O->size) continue;
+        const int64_t end = last[nd->output_ids[0]];
+        if (end == INT64_MAX) continue;
+        int ok = 1;
+        for (int64_t j = (int64_t)k + 1; j <= end && ok; j++) {
+            const SpinnNode *w = &ctx->nodes[j];
+            for (int q = 0; q < w->num_outputs && ok; q++) {
+                if (w->output_ids[q] >= nt) continue;
+                const SpinnTensor *T = &ctx->tensors[w->output_ids[q]];
+                if (T->data && T->size && bytes_overlap((const uint8_t *)T->data, T->size, (const uint8_t *)I->data, I->size))
+                    ok = 0;
+            }
+        }
+        if (ok) O->data = I->data;
+    }
+    free(last);
+}
+
 /* Bytes of a weight's payload in the file, from its dense entry (0 = none). */
 static uint32_t weight_payload_bytes(SpinnContext *ctx, uint16_t tensor_id) {
     uint32_t entry_pos = ctx->header.reserved[0] + (uint32_t)tensor_id * (uint32_t)sizeof(ENNF_WeightEntry);
@@ -228,6 +278,7 @@ int spinn_plan(SpinnContext *ctx, uint32_t max_arena_bytes) {
         if (!t->is_weight && t->size > 0 && (uint64_t)t->offset + t->size <= (uint64_t)peak)
             t->data = ctx->arena.base + t->offset;
     }
+    alias_views(ctx);
 
     /* weights: one device pool, 256-byte aligned entries */
     size_t pool = 0;

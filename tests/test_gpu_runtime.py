@@ -206,6 +206,41 @@ def test_yolov10n_b16_graph_replay(hip, tmp_path):
     assert_parity(y_eager, ref, what="yolov10n b16", scale_by_ref=True)
 
 
+VIEW_OPS = (E.OP_RESHAPE, E.OP_FLATTEN, E.OP_IDENTITY, E.OP_UNSQUEEZE)
+
+
+def _views(s):
+    """(view nodes, those whose output shares its input's device address)."""
+    c = s.c
+    views = [c.nodes[k] for k in range(c.num_nodes) if c.nodes[k].op_type in VIEW_OPS]
+    shared = [nd for nd in views if c.tensors[nd.input_ids[0]].data == c.tensors[nd.output_ids[0]].data]
+    return len(views), len(shared)
+
+
+@pytest.mark.parametrize("tail", [False, True], ids=["head", "tail"])
+def test_view_nodes_read_in_place(hip, tmp_path, tail):
+    """Reshape / Flatten / Identity / Unsqueeze copy their input unless the tensors share
+    bytes. At plan time an output whose input bytes no node overwrites before the output's
+    last reader takes the input's device address, so the node launches nothing. YOLOv10n at
+    batch 1 has such nodes in its head and TopK tail; eager and graph-replayed runs agree bit
+    for bit, and the head's output matches the oracle."""
+    g, x = models.yolov10n(batch=1, seed=21, hw=320, postprocess=tail)
+    path = g.write(tmp_path / f"y10_views_{tail}.ennf")
+    print(f"[views] yolov10n b1 320 tail={tail}", flush=True)
+    with Session(path) as s:
+        n_views, n_shared = _views(s)
+        y = s.run(x)
+    with Session(path, graph=True) as sg:
+        yg = [sg.run(x) for _ in range(2)]
+    print(f"[views] {n_shared} of {n_views} view nodes read in place", flush=True)
+    assert n_shared >= 1
+    for o in yg:
+        assert np.array_equal(o, y)
+    if not tail:
+        ref = O.Model(path).run(x, g.dims(g.outputs[0]))
+        assert_parity(y, ref, what="yolov10n b1@320 with in-place views", scale_by_ref=True)
+
+
 def test_graph_mode_failed_node_is_not_replayed(hip, tmp_path):
     """A node that fails host-side validation during graph capture leaves no graph
     behind: every later graph-mode run captures again and reports the failure
