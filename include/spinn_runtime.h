@@ -94,6 +94,10 @@ typedef struct {
     int conv_policy;         /* SPINN_CONV_POLICY_* fixed at plan time */
     void *input_stage;       /* device copy of input 0 that spinn_run_resident restores from */
     int input_staged;        /* 1 once spinn_stage_input has filled input_stage */
+    uint8_t *node_folded;    /* per node, set by spinn_plan: 1 when a consumer reads the node's input in its
+                                place (a Transpose read transposed by its MatMul), so the node launches nothing */
+    int32_t *node_tsrc;      /* per node, two entries set by spinn_plan: the tensor a MatMul reads transposed
+                                as its operand A / B instead of that operand, or -1 */
 } SpinnContext;
 
 /* Which algorithm eligible 3x3 stride-1 convolutions use (spinn_set_conv_policy). */

@@ -271,14 +271,19 @@ int op_matmul(SpinnTensor **in, int n_in, void *params, uint16_t params_size, Sp
     SpinnTensor *A = in[0], *B = in[1], *Y = out[0];
     int an = A->ndim, bn = B->ndim;
     if (an < 2 || bn < 2) return -1;
+    /* An operand handed over as its transpose (the runtime folded a Transpose of
+     * the last two axes into this node) is read with the Gemm's transpose flag. */
+    const int ta = g_spinn_exec.matmul_transposed & 1, tb = (g_spinn_exec.matmul_transposed >> 1) & 1;
     SpinnHipGemmDesc d;
     memset(&d, 0, sizeof(d));
     d.alpha = 1.f;
     d.beta = 0.f;
-    d.m = (int)A->dims[an - 2];
-    d.k = (int)A->dims[an - 1];
-    d.n = (int)B->dims[bn - 1];
-    if ((int)B->dims[bn - 2] != d.k) return -1;
+    d.trans_a = ta;
+    d.trans_b = tb;
+    d.m = (int)A->dims[an - (ta ? 1 : 2)];
+    d.k = (int)A->dims[an - (ta ? 2 : 1)];
+    d.n = (int)B->dims[bn - (tb ? 2 : 1)];
+    if ((int)B->dims[bn - (tb ? 1 : 2)] != d.k) return -1;
     int batch = 1, batch_b = 1;
     for (int i = 0; i < an - 2; i++) batch *= (int)A->dims[i];
     for (int i = 0; i < bn - 2; i++) batch_b *= (int)B->dims[i];

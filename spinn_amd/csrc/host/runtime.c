@@ -172,9 +172,17 @@ static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 static int dispatch_node(SpinnContext *ctx, uint32_t i) {
     SpinnNode *node = &ctx->nodes[i];
+    if (ctx->node_folded && ctx->node_folded[i]) return 0; /* its consumer reads its input in place */
     SpinnTensor *ins[SPINN_MAX_IO], *outs[SPINN_MAX_IO];
     for (int j = 0; j < node->num_inputs; j++) ins[j] = &ctx->tensors[node->input_ids[j]];
     for (int j = 0; j < node->num_outputs; j++) outs[j] = &ctx->tensors[node->output_ids[j]];
+    int transposed = 0;
+    if (ctx->node_tsrc)
+        for (int s = 0; s < 2 && s < node->num_inputs; s++)
+            if (ctx->node_tsrc[2 * i + s] >= 0) {
+                ins[s] = &ctx->tensors[ctx->node_tsrc[2 * i + s]];
+                transposed |= 1 << s;
+            }
     /* A non-empty operand without device memory (a weight whose file entry has
      * no payload, a tensor the planner never placed) would reach a kernel as a
      * null pointer: the node fails instead. */
@@ -182,8 +190,11 @@ static int dispatch_node(SpinnContext *ctx, uint32_t i) {
         if (ins[j]->size > 0 && !ins[j]->data) return -1;
     for (int j = 0; j < node->num_outputs; j++)
         if (outs[j]->size > 0 && !outs[j]->data) return -1;
-    return spinn_dispatch_op(node->op_type, ins, node->num_inputs, node->params, node->params_size, outs,
-                             node->num_outputs);
+    g_spinn_exec.matmul_transposed = transposed;
+    int rc = spinn_dispatch_op(node->op_type, ins, node->num_inputs, node->params, node->params_size, outs,
+                               node->num_outputs);
+    g_spinn_exec.matmul_transposed = 0;
+    return rc;
 }
 
 /* Reshape, Flatten, Identity and Unsqueeze copy their input unless the two
@@ -236,6 +247,91 @@ static void alias_views(SpinnContext *ctx) {
     free(last);
 }
 
+/* A Transpose that swaps the last two axes (leading axes in place) and whose
+ * only reader is a MatMul operand: the MatMul reads the Transpose's input
+ * with the Gemm's transpose flag instead (the tile loaders stage either
+ * orientation), provided no node writes into that input's bytes from the
+ * Transpose through the MatMul (the MatMul's own output included); the
+ * Transpose then launches nothing. Its output tensor is never written. */
+static int swaps_last_two(const SpinnNode *nd, int ndim) {
+    if (ndim < 2 || ndim > ENNF_MAX_DIMS) return 0;
+    int perm[ENNF_MAX_DIMS];
+    for (int d = 0; d < ndim; d++) perm[d] = ndim - 1 - d; /* ONNX default: reverse */
+    if (nd->params && nd->params_size >= sizeof(ENNF_TransposeParams)) {
+        const ENNF_TransposeParams *p = (const ENNF_TransposeParams *)nd->params;
+        for (int d = 0; d < ndim; d++) perm[d] = p->perm[d];
+    }
+    for (int d = 0; d < ndim - 2; d++)
+        if (perm[d] != d) return 0;
+    return perm[ndim - 2] == ndim - 1 && perm[ndim - 1] == ndim - 2;
+}
+
+static int written_between(const SpinnContext *ctx, uint32_t from, uint32_t to, const SpinnTensor *T) {
+    for (uint32_t j = from; j <= to; j++) {
+        const SpinnNode *w = &ctx->nodes[j];
+        if (ctx->node_folded[j]) continue; /* launches nothing */
+        for (int q = 0; q < w->num_outputs; q++) {
+            if (w->output_ids[q] >= ctx->num_tensors) continue;
+            const SpinnTensor *O = &ctx->tensors[w->output_ids[q]];
+            if (O->data && O->size && bytes_overlap((const uint8_t *)O->data, O->size, (const uint8_t *)T->data, T->size))
+                return 1;
+        }
+    }
+    return 0;
+}
+
+static void fold_transposes(SpinnContext *ctx) {
+    const uint32_t nt = ctx->num_tensors, nn = ctx->num_nodes;
+    free(ctx->node_folded);
+    free(ctx->node_tsrc);
+    ctx->node_folded = (uint8_t *)calloc(nn ? nn : 1, 1);
+    ctx->node_tsrc = (int32_t *)malloc((size_t)(nn ? nn : 1) * 2 * sizeof(int32_t));
+    int32_t *producer = (int32_t *)malloc((size_t)(nt ? nt : 1) * sizeof(int32_t));
+    uint32_t *readers = (uint32_t *)calloc(nt ? nt : 1, sizeof(uint32_t));
+    if (!ctx->node_folded || !ctx->node_tsrc || !producer || !readers) {
+        free(ctx->node_folded);
+        free(ctx->node_tsrc);
+        ctx->node_folded = NULL;
+        ctx->node_tsrc = NULL;
+        free(producer);
+        free(readers);
+        return; /* every Transpose runs */
+    }
+    for (uint32_t i = 0; i < 2 * nn; i++) ctx->node_tsrc[i] = -1;
+    for (uint32_t t = 0; t < nt; t++) producer[t] = -1;
+    for (uint32_t i = 0; i < nn; i++) {
+        const SpinnNode *nd = &ctx->nodes[i];
+        for (int q = 0; q < nd->num_outputs; q++)
+            if (nd->output_ids[q] < nt) producer[nd->output_ids[q]] = (int32_t)i;
+        for (int q = 0; q < nd->num_inputs; q++)
+            if (nd->input_ids[q] < nt) readers[nd->input_ids[q]]++;
+    }
+    for (uint32_t o = 0; o < ctx->header.num_outputs && o < 16; o++)
+        if (ctx->output_ids[o] < nt) readers[ctx->output_ids[o]] += 2; /* a graph output is read by the caller */
+    for (uint32_t j = 0; j < nn; j++) {
+        const SpinnNode *mm = &ctx->nodes[j];
+        if (mm->op_type != ENNF_OP_MatMul || mm->num_inputs < 2) continue;
+        for (int s = 0; s < 2; s++) {
+            const uint16_t x = mm->input_ids[s];
+            if (x >= nt || readers[x] != 1 || producer[x] < 0) continue;
+            const uint32_t k = (uint32_t)producer[x];
+            const SpinnNode *tn = &ctx->nodes[k];
+            if (tn->op_type != ENNF_OP_Transpose || tn->num_inputs < 1 || tn->num_outputs != 1) continue;
+            if (tn->input_ids[0] >= nt) continue;
+            const SpinnTensor *T = &ctx->tensors[tn->input_ids[0]];
+            const SpinnTensor *X = &ctx->tensors[x];
+            if (!T->data || T->dtype != ENNF_TYPE_FLOAT32 || X->dtype != ENNF_TYPE_FLOAT32 || T->ndim != X->ndim ||
+                T->size != X->size || !swaps_last_two(tn, T->ndim))
+                continue;
+            if (written_between(ctx, k + 1, j, T)) continue;
+            ctx->node_folded[k] = 1;
+            ctx->node_tsrc[2 * j + s] = (int32_t)tn->input_ids[0];
+        }
+    }
+    free(producer);
+    free(readers);
+}
+
 /* Bytes of a weight's payload in the file, from its dense entry (0 = none). */
 static uint32_t weight_payload_bytes(SpinnContext *ctx, uint16_t tensor_id) {
     uint32_t entry_pos = ctx->header.reserved[0] + (uint32_t)tensor_id * (uint32_t)sizeof(ENNF_WeightEntry);
@@ -279,6 +375,7 @@ int spinn_plan(SpinnContext *ctx, uint32_t max_arena_bytes) {
             t->data = ctx->arena.base + t->offset;
     }
     alias_views(ctx);
+    fold_transposes(ctx);
 
     /* weights: one device pool, 256-byte aligned entries */
     size_t pool = 0;
@@ -587,6 +684,8 @@ static void ctx_release(SpinnContext *ctx) {
         for (uint32_t i = 0; i < ctx->num_nodes; i++) free(ctx->nodes[i].params);
         free(ctx->nodes);
     }
+    free(ctx->node_folded);
+    free(ctx->node_tsrc);
     free(ctx->tensors);
     if (ctx->ennf_fp) fclose(ctx->ennf_fp);
     free(ctx);

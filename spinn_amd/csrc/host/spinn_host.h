@@ -24,6 +24,7 @@ typedef struct {
     size_t prepare_ws_need;
     int prepare_error;
     int conv_policy; /* SPINN_CONV_POLICY_* of the context being planned / run */
+    int matmul_transposed; /* bit 0 / 1: the MatMul being dispatched gets operand A / B as its transpose */
 } SpinnExec;
 
 extern SpinnExec g_spinn_exec;

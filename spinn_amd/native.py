@@ -119,6 +119,7 @@ class SpinnContext(C.Structure):
         ("graph_exec", C.c_void_p), ("use_graph", C.c_int), ("prof_state", C.c_void_p),
         ("conv_policy", C.c_int),
         ("input_stage", C.c_void_p), ("input_staged", C.c_int),
+        ("node_folded", C.POINTER(C.c_uint8)), ("node_tsrc", C.POINTER(C.c_int32)),
     ]
 
 

@@ -217,28 +217,42 @@ def _views(s):
     return len(views), len(shared)
 
 
-@pytest.mark.parametrize("tail", [False, True], ids=["head", "tail"])
-def test_view_nodes_read_in_place(hip, tmp_path, tail):
+def _folded_transposes(s):
+    """(Transpose nodes, those a MatMul reads transposed in their place)."""
+    c = s.c
+    tr = [k for k in range(c.num_nodes) if c.nodes[k].op_type == E.OP_TRANSPOSE]
+    mm = [k for k in range(c.num_nodes) if c.nodes[k].op_type == E.OP_MATMUL]
+    folded = [k for k in tr if c.node_folded[k]]
+    reads = sum(1 for j in mm for q in range(2) if c.node_tsrc[2 * j + q] >= 0)
+    assert reads == len(folded)
+    return len(tr), len(folded)
+
+
+@pytest.mark.parametrize("batch,tail", [(1, False), (1, True), (2, False)], ids=["b1_head", "b1_tail", "b2_head"])
+def test_view_nodes_read_in_place(hip, tmp_path, batch, tail):
     """Reshape / Flatten / Identity / Unsqueeze copy their input unless the tensors share
     bytes. At plan time an output whose input bytes no node overwrites before the output's
-    last reader takes the input's device address, so the node launches nothing. YOLOv10n at
-    batch 1 has such nodes in its head and TopK tail; eager and graph-replayed runs agree bit
-    for bit, and the head's output matches the oracle."""
-    g, x = models.yolov10n(batch=1, seed=21, hw=320, postprocess=tail)
-    path = g.write(tmp_path / f"y10_views_{tail}.ennf")
-    print(f"[views] yolov10n b1 320 tail={tail}", flush=True)
+    last reader takes the input's device address, so the node launches nothing; a Transpose
+    of the last two axes read only by a MatMul is folded into it (the Gemm reads the
+    Transpose's input with its transpose flag). YOLOv10n has both in its attention and head;
+    eager and graph-replayed runs agree bit for bit, and the head's output matches the oracle."""
+    g, x = models.yolov10n(batch=batch, seed=21, hw=320, postprocess=tail)
+    path = g.write(tmp_path / f"y10_views_{batch}_{tail}.ennf")
+    print(f"[views] yolov10n b{batch} 320 tail={tail}", flush=True)
     with Session(path) as s:
         n_views, n_shared = _views(s)
+        n_tr, n_folded = _folded_transposes(s)
         y = s.run(x)
     with Session(path, graph=True) as sg:
         yg = [sg.run(x) for _ in range(2)]
-    print(f"[views] {n_shared} of {n_views} view nodes read in place", flush=True)
-    assert n_shared >= 1
+    print(f"[views] {n_shared} of {n_views} view nodes read in place, {n_folded} of {n_tr} Transposes folded",
+          flush=True)
+    assert n_shared >= 1 and n_folded >= 1
     for o in yg:
         assert np.array_equal(o, y)
     if not tail:
         ref = O.Model(path).run(x, g.dims(g.outputs[0]))
-        assert_parity(y, ref, what="yolov10n b1@320 with in-place views", scale_by_ref=True)
+        assert_parity(y, ref, what=f"yolov10n b{batch}@320 with in-place views", scale_by_ref=True)
 
 
 def test_graph_mode_failed_node_is_not_replayed(hip, tmp_path):
