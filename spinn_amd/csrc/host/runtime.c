@@ -374,8 +374,18 @@ int spinn_plan(SpinnContext *ctx, uint32_t max_arena_bytes) {
         if (!t->is_weight && t->size > 0 && (uint64_t)t->offset + t->size <= (uint64_t)peak)
             t->data = ctx->arena.base + t->offset;
     }
-    alias_views(ctx);
-    fold_transposes(ctx);
+    /* SPINN_PLAN_FOLD=0 keeps every view copy and Transpose (each node's output
+     * then holds its own bytes, for inspecting intermediate tensors) */
+    const char *fold_env = getenv("SPINN_PLAN_FOLD");
+    if (fold_env && fold_env[0] == '0') {
+        free(ctx->node_folded);
+        free(ctx->node_tsrc);
+        ctx->node_folded = NULL;
+        ctx->node_tsrc = NULL;
+    } else {
+        alias_views(ctx);
+        fold_transposes(ctx);
+    }
 
     /* weights: one device pool, 256-byte aligned entries */
     size_t pool = 0;

@@ -222,6 +222,9 @@ def _folded_transposes(s):
     c = s.c
     tr = [k for k in range(c.num_nodes) if c.nodes[k].op_type == E.OP_TRANSPOSE]
     mm = [k for k in range(c.num_nodes) if c.nodes[k].op_type == E.OP_MATMUL]
+    if not c.node_folded:  # folding switched off: no tables
+        assert not c.node_tsrc
+        return len(tr), 0
     folded = [k for k in tr if c.node_folded[k]]
     reads = sum(1 for j in mm for q in range(2) if c.node_tsrc[2 * j + q] >= 0)
     assert reads == len(folded)
@@ -253,6 +256,22 @@ def test_view_nodes_read_in_place(hip, tmp_path, batch, tail):
     if not tail:
         ref = O.Model(path).run(x, g.dims(g.outputs[0]))
         assert_parity(y, ref, what=f"yolov10n b{batch}@320 with in-place views", scale_by_ref=True)
+
+
+def test_plan_fold_off_keeps_every_copy(hip, tmp_path, monkeypatch):
+    """SPINN_PLAN_FOLD=0 at plan time keeps every view copy and Transpose (each tensor in its
+    own bytes, as the planner placed it); the output matches the folded plan's within the
+    bar (the Gemm reads the folded operands in the other orientation)."""
+    g, x = models.yolov10n(batch=1, seed=22, hw=320)
+    path = g.write(tmp_path / "y10_nofold.ennf")
+    with Session(path) as s:
+        assert _views(s)[1] >= 1 and _folded_transposes(s)[1] >= 1
+        y_fold = s.run(x)
+    monkeypatch.setenv("SPINN_PLAN_FOLD", "0")
+    with Session(path) as s:
+        assert _views(s)[1] == 0 and _folded_transposes(s)[1] == 0
+        y = s.run(x)
+    assert_parity(y, y_fold, what="yolov10n b1@320 unfolded vs folded", scale_by_ref=True)
 
 
 def test_graph_mode_failed_node_is_not_replayed(hip, tmp_path):
