@@ -98,6 +98,9 @@ typedef struct {
                                 place (a Transpose read transposed by its MatMul), so the node launches nothing */
     int32_t *node_tsrc;      /* per node, two entries set by spinn_plan: the tensor a MatMul reads transposed
                                 as its operand A / B instead of that operand, or -1 */
+    int32_t *node_tdst;      /* per node, set by spinn_plan: the tensor a MatMul writes instead of its output
+                                (the output of a folded Mul by a constant scalar), or -1 */
+    float *node_alpha;       /* per node: the scale a MatMul applies to its product (that scalar), else 1 */
 } SpinnContext;
 
 /* Which algorithm eligible 3x3 stride-1 convolutions use (spinn_set_conv_policy). */

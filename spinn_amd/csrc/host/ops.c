@@ -15,7 +15,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-SpinnExec g_spinn_exec = {0};
+SpinnExec g_spinn_exec = {.matmul_alpha = 1.f};
 
 static void *g_fallback_ws = NULL;
 static size_t g_fallback_ws_bytes = 0;
@@ -276,7 +276,7 @@ int op_matmul(SpinnTensor **in, int n_in, void *params, uint16_t params_size, Sp
     const int ta = g_spinn_exec.matmul_transposed & 1, tb = (g_spinn_exec.matmul_transposed >> 1) & 1;
     SpinnHipGemmDesc d;
     memset(&d, 0, sizeof(d));
-    d.alpha = 1.f;
+    d.alpha = g_spinn_exec.matmul_alpha;
     d.beta = 0.f;
     d.trans_a = ta;
     d.trans_b = tb;

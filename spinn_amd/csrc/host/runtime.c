@@ -183,6 +183,11 @@ static int dispatch_node(SpinnContext *ctx, uint32_t i) {
                 ins[s] = &ctx->tensors[ctx->node_tsrc[2 * i + s]];
                 transposed |= 1 << s;
             }
+    float alpha = 1.f;
+    if (ctx->node_tdst && ctx->node_tdst[i] >= 0 && node->num_outputs >= 1) {
+        outs[0] = &ctx->tensors[ctx->node_tdst[i]];
+        alpha = ctx->node_alpha[i];
+    }
     /* A non-empty operand without device memory (a weight whose file entry has
      * no payload, a tensor the planner never placed) would reach a kernel as a
      * null pointer: the node fails instead. */
@@ -190,10 +195,12 @@ static int dispatch_node(SpinnContext *ctx, uint32_t i) {
         if (ins[j]->size > 0 && !ins[j]->data) return -1;
     for (int j = 0; j < node->num_outputs; j++)
         if (outs[j]->size > 0 && !outs[j]->data) return -1;
+    g_spinn_exec.matmul_alpha = alpha;
     g_spinn_exec.matmul_transposed = transposed;
     int rc = spinn_dispatch_op(node->op_type, ins, node->num_inputs, node->params, node->params_size, outs,
                                node->num_outputs);
     g_spinn_exec.matmul_transposed = 0;
+    g_spinn_exec.matmul_alpha = 1.f;
     return rc;
 }
 
@@ -332,6 +339,100 @@ static void fold_transposes(SpinnContext *ctx) {
     free(readers);
 }
 
+/* A Mul of a MatMul's product by a one-element float constant, where the Mul
+ * is the product's only reader: the MatMul writes the Mul's output itself with
+ * the constant as the Gemm's alpha (alpha * acc is the Mul's own float product,
+ * so the bits are the same) and the Mul launches nothing. The MatMul then
+ * writes the Mul's output bytes earlier than the plan did: no node from the
+ * MatMul until the Mul may read or write them (a tensor the planner placed
+ * there and still reads). */
+static int touched_between(const SpinnContext *ctx, uint32_t from, uint32_t to, int reads_from, const SpinnTensor *Z) {
+    for (uint32_t m = from; m <= to; m++) {
+        if (ctx->node_folded[m]) continue;
+        const SpinnNode *nd = &ctx->nodes[m];
+        if ((int64_t)m >= (int64_t)reads_from) {
+            for (int q = 0; q < nd->num_inputs; q++) {
+                int32_t id = nd->input_ids[q];
+                if (q < 2 && ctx->node_tsrc[2 * m + q] >= 0) id = ctx->node_tsrc[2 * m + q];
+                if ((uint32_t)id >= ctx->num_tensors) continue;
+                const SpinnTensor *T = &ctx->tensors[id];
+                if (T->data && T->size && bytes_overlap((const uint8_t *)T->data, T->size, (const uint8_t *)Z->data, Z->size))
+                    return 1;
+            }
+        }
+        if (m == from) continue; /* the MatMul's own output is what moves */
+        for (int q = 0; q < nd->num_outputs; q++) {
+            if (nd->output_ids[q] >= ctx->num_tensors) continue;
+            const SpinnTensor *T = &ctx->tensors[nd->output_ids[q]];
+            if (T->data && T->size && bytes_overlap((const uint8_t *)T->data, T->size, (const uint8_t *)Z->data, Z->size))
+                return 1;
+        }
+    }
+    return 0;
+}
+
+static void fold_scales(SpinnContext *ctx) {
+    const uint32_t nt = ctx->num_tensors, nn = ctx->num_nodes;
+    free(ctx->node_tdst);
+    free(ctx->node_alpha);
+    ctx->node_tdst = NULL;
+    ctx->node_alpha = NULL;
+    if (!ctx->node_folded || !ctx->node_tsrc) return;
+    ctx->node_tdst = (int32_t *)malloc((size_t)(nn ? nn : 1) * sizeof(int32_t));
+    ctx->node_alpha = (float *)malloc((size_t)(nn ? nn : 1) * sizeof(float));
+    int32_t *producer = (int32_t *)malloc((size_t)(nt ? nt : 1) * sizeof(int32_t));
+    uint32_t *readers = (uint32_t *)calloc(nt ? nt : 1, sizeof(uint32_t));
+    if (!ctx->node_tdst || !ctx->node_alpha || !producer || !readers) {
+        free(ctx->node_tdst);
+        free(ctx->node_alpha);
+        ctx->node_tdst = NULL;
+        ctx->node_alpha = NULL;
+        free(producer);
+        free(readers);
+        return; /* every Mul runs */
+    }
+    for (uint32_t i = 0; i < nn; i++) {
+        ctx->node_tdst[i] = -1;
+        ctx->node_alpha[i] = 1.f;
+    }
+    for (uint32_t t = 0; t < nt; t++) producer[t] = -1;
+    for (uint32_t i = 0; i < nn; i++) {
+        const SpinnNode *nd = &ctx->nodes[i];
+        for (int q = 0; q < nd->num_outputs; q++)
+            if (nd->output_ids[q] < nt) producer[nd->output_ids[q]] = (int32_t)i;
+        for (int q = 0; q < nd->num_inputs; q++)
+            if (nd->input_ids[q] < nt) readers[nd->input_ids[q]]++;
+    }
+    for (uint32_t o = 0; o < ctx->header.num_outputs && o < 16; o++)
+        if (ctx->output_ids[o] < nt) readers[ctx->output_ids[o]] += 2;
+    for (uint32_t k = 0; k < nn; k++) {
+        const SpinnNode *mul = &ctx->nodes[k];
+        if (mul->op_type != ENNF_OP_Mul || mul->num_inputs != 2 || mul->num_outputs != 1) continue;
+        if (mul->input_ids[0] >= nt || mul->input_ids[1] >= nt || mul->output_ids[0] >= nt) continue;
+        for (int s = 0; s < 2; s++) {
+            const uint16_t y = mul->input_ids[s], c = mul->input_ids[1 - s];
+            const SpinnTensor *Y = &ctx->tensors[y], *S = &ctx->tensors[c], *Z = &ctx->tensors[mul->output_ids[0]];
+            if (producer[y] < 0 || readers[y] != 1) continue;
+            const uint32_t j = (uint32_t)producer[y];
+            const SpinnNode *mm = &ctx->nodes[j];
+            if (mm->op_type != ENNF_OP_MatMul || mm->num_outputs != 1 || ctx->node_tdst[j] >= 0) continue;
+            if (!S->is_weight || S->dtype != ENNF_TYPE_FLOAT32 || S->elem_count != 1) continue;
+            if (Y->dtype != ENNF_TYPE_FLOAT32 || Z->dtype != ENNF_TYPE_FLOAT32 || Z->elem_count != Y->elem_count ||
+                !Z->data || !Y->data)
+                continue;
+            const float *sv = (const float *)spinn_get_weight(ctx, c);
+            if (!sv) continue;
+            if (touched_between(ctx, j, k - 1, (int)j, Z)) continue;
+            ctx->node_tdst[j] = (int32_t)mul->output_ids[0];
+            ctx->node_alpha[j] = sv[0];
+            ctx->node_folded[k] = 1;
+            break;
+        }
+    }
+    free(producer);
+    free(readers);
+}
+
 /* Bytes of a weight's payload in the file, from its dense entry (0 = none). */
 static uint32_t weight_payload_bytes(SpinnContext *ctx, uint16_t tensor_id) {
     uint32_t entry_pos = ctx->header.reserved[0] + (uint32_t)tensor_id * (uint32_t)sizeof(ENNF_WeightEntry);
@@ -380,11 +481,16 @@ int spinn_plan(SpinnContext *ctx, uint32_t max_arena_bytes) {
     if (fold_env && fold_env[0] == '0') {
         free(ctx->node_folded);
         free(ctx->node_tsrc);
+        free(ctx->node_tdst);
+        free(ctx->node_alpha);
         ctx->node_folded = NULL;
         ctx->node_tsrc = NULL;
+        ctx->node_tdst = NULL;
+        ctx->node_alpha = NULL;
     } else {
         alias_views(ctx);
         fold_transposes(ctx);
+        fold_scales(ctx);
     }
 
     /* weights: one device pool, 256-byte aligned entries */
@@ -696,6 +802,8 @@ static void ctx_release(SpinnContext *ctx) {
     }
     free(ctx->node_folded);
     free(ctx->node_tsrc);
+    free(ctx->node_tdst);
+    free(ctx->node_alpha);
     free(ctx->tensors);
     if (ctx->ennf_fp) fclose(ctx->ennf_fp);
     free(ctx);

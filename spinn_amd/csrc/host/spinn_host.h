@@ -25,6 +25,7 @@ typedef struct {
     int prepare_error;
     int conv_policy; /* SPINN_CONV_POLICY_* of the context being planned / run */
     int matmul_transposed; /* bit 0 / 1: the MatMul being dispatched gets operand A / B as its transpose */
+    float matmul_alpha;    /* scale of the MatMul being dispatched (1 unless a Mul was folded into it) */
 } SpinnExec;
 
 extern SpinnExec g_spinn_exec;

@@ -120,6 +120,7 @@ class SpinnContext(C.Structure):
         ("conv_policy", C.c_int),
         ("input_stage", C.c_void_p), ("input_staged", C.c_int),
         ("node_folded", C.POINTER(C.c_uint8)), ("node_tsrc", C.POINTER(C.c_int32)),
+        ("node_tdst", C.POINTER(C.c_int32)), ("node_alpha", C.POINTER(C.c_float)),
     ]
 
 

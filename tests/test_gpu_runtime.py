@@ -231,6 +231,22 @@ def _folded_transposes(s):
     return len(tr), len(folded)
 
 
+def _folded_scales(s):
+    """MatMuls that write a folded Mul's output with its scalar as alpha."""
+    c = s.c
+    if not c.node_tdst:
+        return 0
+    n = 0
+    for j in range(c.num_nodes):
+        if c.node_tdst[j] >= 0:
+            assert c.nodes[j].op_type == E.OP_MATMUL
+            muls = [k for k in range(c.num_nodes) if c.nodes[k].op_type == E.OP_MUL
+                    and c.nodes[k].output_ids[0] == c.node_tdst[j]]
+            assert len(muls) == 1 and c.node_folded[muls[0]]
+            n += 1
+    return n
+
+
 @pytest.mark.parametrize("batch,tail", [(1, False), (1, True), (2, False)], ids=["b1_head", "b1_tail", "b2_head"])
 def test_view_nodes_read_in_place(hip, tmp_path, batch, tail):
     """Reshape / Flatten / Identity / Unsqueeze copy their input unless the tensors share
@@ -245,11 +261,12 @@ def test_view_nodes_read_in_place(hip, tmp_path, batch, tail):
     with Session(path) as s:
         n_views, n_shared = _views(s)
         n_tr, n_folded = _folded_transposes(s)
+        n_scales = _folded_scales(s)
         y = s.run(x)
     with Session(path, graph=True) as sg:
         yg = [sg.run(x) for _ in range(2)]
-    print(f"[views] {n_shared} of {n_views} view nodes read in place, {n_folded} of {n_tr} Transposes folded",
-          flush=True)
+    print(f"[views] {n_shared} of {n_views} view nodes read in place, {n_folded} of {n_tr} Transposes folded, "
+          f"{n_scales} scalar Muls folded", flush=True)
     assert n_shared >= 1 and n_folded >= 1
     for o in yg:
         assert np.array_equal(o, y)
@@ -269,7 +286,7 @@ def test_plan_fold_off_keeps_every_copy(hip, tmp_path, monkeypatch):
         y_fold = s.run(x)
     monkeypatch.setenv("SPINN_PLAN_FOLD", "0")
     with Session(path) as s:
-        assert _views(s)[1] == 0 and _folded_transposes(s)[1] == 0
+        assert _views(s)[1] == 0 and _folded_transposes(s)[1] == 0 and _folded_scales(s) == 0
         y = s.run(x)
     assert_parity(y, y_fold, what="yolov10n b1@320 unfolded vs folded", scale_by_ref=True)
 
