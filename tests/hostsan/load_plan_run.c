@@ -4,7 +4,9 @@
  * For each file: spinn_load; if it loads, spinn_plan, then spinn_run eagerly
  * and in graph mode (the stub's graph capture fails, exercising that error
  * path), then spinn_free. Prints one line per file: the load / plan / run
- * return codes. Any sanitizer report aborts the process with a non-zero exit.
+ * return codes and what the plan folded (view outputs sharing their input's
+ * bytes, Transposes read by their MatMul, scalar Muls taken as MatMul alpha).
+ * Any sanitizer report aborts the process with a non-zero exit.
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -20,6 +22,20 @@ int main(int argc, char **argv) {
         }
         int plan = spinn_plan(ctx, 0);
         int run = 99, run_graph = 99;
+        int views = 0, transposes = 0, scales = 0;
+        if (plan == 0) {
+            for (uint32_t k = 0; k < ctx->num_nodes; k++) {
+                const SpinnNode *nd = &ctx->nodes[k];
+                const uint16_t op = nd->op_type;
+                if ((op == ENNF_OP_Reshape || op == ENNF_OP_Flatten || op == ENNF_OP_Identity ||
+                     op == ENNF_OP_Unsqueeze) &&
+                    nd->num_inputs >= 1 && nd->num_outputs >= 1 &&
+                    ctx->tensors[nd->input_ids[0]].data == ctx->tensors[nd->output_ids[0]].data)
+                    views++;
+                if (ctx->node_folded && ctx->node_folded[k] && op == ENNF_OP_Transpose) transposes++;
+                if (ctx->node_tdst && ctx->node_tdst[k] >= 0) scales++;
+            }
+        }
         if (plan == 0) {
             /* spinn_run copies tensor input_ids[0] in and output_ids[0] out
              * (both validated ids, 0 when the file lists none) */
@@ -32,7 +48,8 @@ int main(int argc, char **argv) {
             free(in);
             free(out);
         }
-        printf("%s load=ok plan=%d run=%d run_graph=%d\n", argv[i], plan, run, run_graph);
+        printf("%s load=ok plan=%d run=%d run_graph=%d views=%d transposes=%d scales=%d\n", argv[i], plan, run,
+               run_graph, views, transposes, scales);
         spinn_free(ctx);
     }
     return 0;

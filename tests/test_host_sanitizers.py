@@ -74,6 +74,22 @@ def test_valid_models_run_clean(san_bin, tmp_path):
         assert "load=ok plan=0 run=0" in line, line
 
 
+def test_plan_folds_on_host(san_bin, tmp_path, monkeypatch):
+    """The plan step's folds, decided on host addresses (the stand-in's arena): YOLOv10n's
+    attention has a Transpose read only by a MatMul and a scalar Mul of a MatMul's product,
+    both folded; SPINN_PLAN_FOLD=0 folds nothing; either way load, plan and run are clean."""
+    g, _ = models.yolov10n(batch=1, seed=4, hw=64)
+    path = g.write(tmp_path / "yolo_fold.ennf")
+    line = _run(san_bin, [path])[0]
+    fields = dict(f.split("=") for f in line.split()[1:])
+    assert fields["plan"] == "0" and fields["run"] == "0", line
+    assert int(fields["transposes"]) >= 1 and int(fields["scales"]) == 1, line
+    monkeypatch.setenv("SPINN_PLAN_FOLD", "0")
+    line = _run(san_bin, [path])[0]
+    fields = dict(f.split("=") for f in line.split()[1:])
+    assert fields["run"] == "0" and fields["views"] == "0" and fields["transposes"] == "0" and fields["scales"] == "0"
+
+
 def test_corrupted_files_are_rejected_or_clean(san_bin, tmp_path):
     rng = random.Random(1234)
     srcs = _models(tmp_path)
