@@ -15,6 +15,9 @@
 // global memory; here the im2col is an address constant. Each wave owns 32 of
 // the row's pixels and both 32-channel blocks; bias, residual and the post-op
 // are applied on the way out (SPINN/run_time/ops/mm/gemm_kernel.c:316-338).
+// With SPLIT (grids of fewer rows than CUs: batch 1 and 2 at 224x224) two
+// workgroups share a row, blockIdx.y choosing the 32-channel block: twice the
+// workgroups, each with half the MFMA chain (same steps per output, same bits).
 #include "mfma_core.h"
 #include "spinn_hip_internal.h"
 
@@ -32,10 +35,12 @@ __host__ __device__ constexpr int stem_koff(int k) {
     return ((k / (kStemK * kStemK)) * kStemK + (k % (kStemK * kStemK)) / kStemK) * kStemPW + k % kStemK;
 }
 
-template <int C, bool RES>
+template <int C, bool RES, bool SPLIT>
 __global__ __launch_bounds__(256) void stem7_mfma_kernel(const float *__restrict__ x, const float *__restrict__ wpk,
                                                          const float *__restrict__ bias, const float *__restrict__ res,
                                                          float *__restrict__ y, SpinnHipConvDesc d, int ldw) {
+    constexpr int NMB = SPLIT ? 1 : 2;           // 32-channel blocks this workgroup computes
+    const int mb0 = SPLIT ? (int)blockIdx.y : 0; // the first of them
     constexpr int K = C * kStemK * kStemK;
     constexpr int STEPS = (K + 1) / 2; // lane group h supplies k = 2s + h
     __shared__ float patch[C * kStemK * kStemPW]; // [c][kh][col]
@@ -73,8 +78,9 @@ __global__ __launch_bounds__(256) void stem7_mfma_kernel(const float *__restrict
     // workgroup: L1 / L2 hits): lane (m = l32 + 32 mb, h) reads row k = 2s + h;
     // rows past K and columns past ldw read 0 through the descriptor's extent.
     const __amdgpu_buffer_rsrc_t rw = make_rsrc(wpk, (uint32_t)(K * ldw * 4));
-    const uint32_t a_lane0 = l32 < ldw ? (uint32_t)(h * ldw + l32) * 4u : kOOB;
-    const uint32_t a_lane1 = l32 + 32 < ldw ? (uint32_t)(h * ldw + l32 + 32) * 4u : kOOB;
+    const int ma = l32 + 32 * mb0;
+    const uint32_t a_lane0 = ma < ldw ? (uint32_t)(h * ldw + ma) * 4u : kOOB;
+    const uint32_t a_lane1 = ma + 32 < ldw ? (uint32_t)(h * ldw + ma + 32) * 4u : kOOB;
     const uint32_t a_step = (uint32_t)(2 * ldw) * 4u;
     if (tid < kStemOC) bsh[tid] = (bias && tid < d.oc) ? bias[tid] : 0.f;
     __syncthreads();
@@ -90,9 +96,11 @@ __global__ __launch_bounds__(256) void stem7_mfma_kernel(const float *__restrict
         const int off1 = 2 * s + 1 < K ? stem_koff(2 * s + 1) : off0;
         const float b = pb[h ? off1 : off0];
         const float a0 = buf_f32(rw, a_lane0 + (uint32_t)s * a_step);
-        const float a1 = buf_f32(rw, a_lane1 + (uint32_t)s * a_step);
         acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b, acc1, 0, 0, 0);
+        if constexpr (!SPLIT) {
+            const float a1 = buf_f32(rw, a_lane1 + (uint32_t)s * a_step);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b, acc1, 0, 0, 0);
+        }
     }
     if (n >= d.ow) return;
     // The bias comes from LDS and every residual load is issued before the first
@@ -102,40 +110,41 @@ __global__ __launch_bounds__(256) void stem7_mfma_kernel(const float *__restrict
     const int64_t base = (int64_t)img * d.oc * ohw + (int64_t)oh * d.ow + n;
     if constexpr (!RES) {
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int m = (mb0 + mb) * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                 if (m < d.oc) y[base + (int64_t)m * ohw] = apply_act((mb ? acc1[r] : acc0[r]) + bsh[m], d.act);
             }
         return;
     }
-    float v[2][16];
+    float v[NMB][16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int mr = 8 * (r >> 2) + 4 * h + (r & 3);
-        v[0][r] = acc0[r] + bsh[mr];
-        v[1][r] = acc1[r] + bsh[32 + mr];
-    }
+    for (int mb = 0; mb < NMB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = (mb0 + mb) * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            v[mb][r] = (mb ? acc1[r] : acc0[r]) + bsh[m];
+        }
     {
-        float rv[2][16];
+        float rv[NMB][16];
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int m = (mb0 + mb) * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
                 rv[mb][r] = m < d.oc ? res[base + (int64_t)m * ohw] : 0.f;
             }
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) v[mb][r] += rv[mb][r];
     }
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int mb = 0; mb < NMB; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int m = mb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const int m = (mb0 + mb) * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
             if (m < d.oc) y[base + (int64_t)m * ohw] = apply_act(v[mb][r], d.act);
         }
 }
@@ -245,27 +254,40 @@ bool stem_mfma_eligible(const SpinnHipConvDesc *d) {
            (int64_t)d->n * d->c * d->h * d->w * 4 <= (int64_t)kMaxOperandBytes;
 }
 
+template <int C, bool RES>
+static void launch_stem7(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+                         const float *res, float *y, int ldw, bool split, hipStream_t st) {
+    const unsigned rows = (unsigned)(d->n * d->oh);
+    if (split)
+        hipLaunchKernelGGL((stem7_mfma_kernel<C, RES, true>), dim3(rows, 2), dim3(256), 0, st, x, packed, bias, res, y,
+                           *d, ldw);
+    else
+        hipLaunchKernelGGL((stem7_mfma_kernel<C, RES, false>), dim3(rows), dim3(256), 0, st, x, packed, bias, res, y,
+                           *d, ldw);
+}
+
+template <bool RES>
+static void launch_stem7_c(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
+                           const float *res, float *y, int ldw, bool split, hipStream_t st) {
+    switch (d->c) {
+    case 1: launch_stem7<1, RES>(d, x, packed, bias, res, y, ldw, split, st); break;
+    case 2: launch_stem7<2, RES>(d, x, packed, bias, res, y, ldw, split, st); break;
+    case 3: launch_stem7<3, RES>(d, x, packed, bias, res, y, ldw, split, st); break;
+    default: launch_stem7<4, RES>(d, x, packed, bias, res, y, ldw, split, st); break;
+    }
+}
+
 // packed: the implicit GEMM's W^T [K][ldw] with K in (c, kh, kw) order (C < 16).
+// Grids of fewer rows than CUs split each row's two 32-channel blocks over two
+// workgroups (ResNet-101's stem at batch 1: 112 rows, 14.3 us on one workgroup
+// per row).
 int stem_mfma_conv(const SpinnHipConvDesc *d, const float *x, const float *packed, const float *bias,
                    const float *res, float *y, hipStream_t st) {
     if (!packed) return SPINN_HIP_EINVAL;
     const int ldw = (d->oc + 3) / 4 * 4;
-    const dim3 grid((unsigned)(d->n * d->oh));
-    if (res) {
-        switch (d->c) {
-        case 1: hipLaunchKernelGGL((stem7_mfma_kernel<1, true>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-        case 2: hipLaunchKernelGGL((stem7_mfma_kernel<2, true>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-        case 3: hipLaunchKernelGGL((stem7_mfma_kernel<3, true>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-        default: hipLaunchKernelGGL((stem7_mfma_kernel<4, true>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-        }
-    } else {
-        switch (d->c) {
-        case 1: hipLaunchKernelGGL((stem7_mfma_kernel<1, false>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-        case 2: hipLaunchKernelGGL((stem7_mfma_kernel<2, false>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-        case 3: hipLaunchKernelGGL((stem7_mfma_kernel<3, false>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-        default: hipLaunchKernelGGL((stem7_mfma_kernel<4, false>), grid, dim3(256), 0, st, x, packed, bias, res, y, *d, ldw); break;
-        }
-    }
+    const bool split = d->oc > 32 && (int64_t)d->n * d->oh < (int64_t)device_cu_count();
+    if (res) launch_stem7_c<true>(d, x, packed, bias, res, y, ldw, split, st);
+    else launch_stem7_c<false>(d, x, packed, bias, res, y, ldw, split, st);
     return check_launch();
 }
 

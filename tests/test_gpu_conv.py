@@ -36,8 +36,10 @@ CASES = [
     ("stem7x7_direct", 1, 3, 40, 40, 64, 7, 2, 3, 1, 1, 3),
     # 7x7 stride-2 stems on the row-per-workgroup MFMA kernel (LDS-staged window)
     ("stem7x7_224_res", 2, 3, 224, 224, 64, 7, 2, 3, 1, 5, 0),         # ResNet stem shape, residual + ReLU
+    ("stem7x7_224_b1_split", 1, 3, 224, 224, 64, 7, 2, 3, 1, 1, 0),    # 112 rows: two workgroups per row
     ("stem7x7_c1_oc40_ragged", 3, 1, 37, 45, 40, 7, 2, 3, 1, 3, 0),   # one channel, 40 of 64 rows, 23-pixel rows
     ("stem7x7_c4_ow128", 1, 4, 30, 256, 64, 7, 2, 3, 1, 1, 0),         # four channels, 128-pixel rows
+    ("stem7x7_oc24_few_rows", 1, 3, 56, 56, 24, 7, 2, 3, 1, 1, 0),     # 28 rows, one channel block: no row split
     ("stem7x7_ow129_fallback", 1, 3, 9, 258, 64, 7, 2, 3, 1, 1, 0),    # 129-pixel rows: generic implicit GEMM
     # stem epilogue: bias from LDS, residual loads batched (no-residual and residual variants)
     ("stem7x7_224_b8", 8, 3, 224, 224, 64, 7, 2, 3, 1, 1, 0),          # 896 rows
