@@ -132,9 +132,11 @@ TileChoice choose_tiles(int M, int N, int K, int reps, bool allow_split) {
         // 256-deep K splits only when the grid covers less than half the
         // CUs (batch-1 1x1 convs). At most 16 splits: measured on the batch-1
         // ResNet-101 convs, 16 beat 8 (the 14x14 3x3 layers then cover all
-        // CUs), while 64-deep splits or 8 workgroups per CU were slower.
+        // CUs), while 64-deep splits or 8 workgroups per CU were slower; up to
+        // 32 where 16 would still leave CUs idle (the 7x7 3x3 layers at batch 1:
+        // 8 tiles, K = 4608, 144-deep splits on 256 workgroups).
         int split = (int)std::min<int64_t>((4 * cus + tiles - 1) / tiles, K / 128);
-        split = std::max(1, std::min(split, 16));
+        split = std::max(1, std::min(split, tiles * 16 < cus ? 32 : 16));
         if (split > 1) {
             int chunk = (K + split - 1) / split;
             chunk = (chunk + kBK - 1) / kBK * kBK;

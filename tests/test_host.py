@@ -245,6 +245,9 @@ def test_conv_algo_selection(native):
     assert workspace(4, 1024, 14, 14, 256, 1, 1, 0, 1) == 0      # K 1024 over 52 tiles: wave-K, no split
     assert workspace(8, 1024, 14, 14, 512, 1, 1, 0, 1) == 0      # 200 tiles: 64 x 64 unsplit
     assert workspace(8, 2048, 7, 7, 512, 1, 1, 0, 1) > 0         # K 2048 over 56 tiles: split K
+    # 16 splits of 16 tiles fill the CUs; 16 splits of 8 tiles would not: 32 splits of 144
+    assert workspace(1, 256, 14, 14, 256, 3, 1, 1, 1) == 16 * 256 * 196 * 4
+    assert workspace(1, 512, 7, 7, 512, 3, 1, 1, 1) == 32 * 512 * 49 * 4
 
 
 def _declared_functions():
