@@ -75,6 +75,45 @@ __global__ __launch_bounds__(256) void reduce_max_short_kernel(const float *__re
     }
 }
 
+// Short rows of a multiple of 16 floats (a detector's 80 class scores): four
+// lanes per row, each scanning a contiguous quarter in float4 steps with the
+// reference's rule, then the quarters combined in index order (a later
+// quarter's maximum replaces the running one only when strictly greater):
+// for NaN-free rows the first maximal element, as the single scan finds it,
+// with four times the threads (8400 rows at batch 1: 132 workgroups, not 33).
+__global__ __launch_bounds__(256) void reduce_max_short4_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                                int64_t rows, int block) {
+    const int64_t total = rows * 4;
+    const int len = block >> 2; // a multiple of 4
+    for (int64_t base = (int64_t)blockIdx.x * blockDim.x; base < total; base += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t t = base + threadIdx.x; // uniform trip count: every lane reaches the shuffles
+        const bool live = t < total;
+        const int64_t row = t >> 2;
+        const int q = (int)(t & 3);
+        float best = 0.f;
+        if (live) {
+            const float *xr = x + row * block + (int64_t)q * len;
+            best = xr[0];
+            for (int j = 0; j < len; j += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(xr + j);
+                if (v.x > best) best = v.x;
+                if (v.y > best) best = v.y;
+                if (v.z > best) best = v.z;
+                if (v.w > best) best = v.w;
+            }
+        }
+        const int lead = (int)(threadIdx.x & 63) & ~3;
+        const float b1 = __shfl(best, lead + 1, 64), b2 = __shfl(best, lead + 2, 64), b3 = __shfl(best, lead + 3, 64);
+        if (live && q == 0) {
+            float m = best;
+            if (b1 > m) m = b1;
+            if (b2 > m) m = b2;
+            if (b3 > m) m = b3;
+            y[row] = m;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // TopK (SPINN/run_time/ops/tensor/topk.c:20-89), one 1024-thread workgroup per row.
 // Order: value descending, ties by ascending index - what the reference's stable
@@ -547,6 +586,11 @@ int grid_for(int64_t n) { return (int)std::max<int64_t>(1, std::min<int64_t>((n 
 } // namespace
 
 int reduce_max_rows(int64_t rows, int64_t block, const float *x, float *y, hipStream_t st) {
+    if (block <= 256 && block % 16 == 0 && ((uintptr_t)x & 15u) == 0 && rows <= INT64_MAX / 4) {
+        const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>((rows * 4 + 255) / 256, 65536)));
+        hipLaunchKernelGGL(reduce_max_short4_kernel, grid, dim3(256), 0, st, x, y, rows, (int)block);
+        return check_launch();
+    }
     if (block <= 256) {
         const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>((rows + 255) / 256, 65536)));
         if (block % 4 == 0 && ((uintptr_t)x & 15u) == 0)

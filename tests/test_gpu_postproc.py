@@ -149,6 +149,20 @@ def test_topk_sampled_threshold(hip, torch_gpu, rows, n, k, layout):
     np.testing.assert_array_equal(got_v.view(np.uint32), ref_v.view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,block", [(8400, 80), (7, 80), (33, 16), (513, 48), (5, 256), (9, 20)],
+                         ids=["b1_scores", "few_rows", "b16", "b48", "b256", "b20_one_lane"])
+def test_reduce_max_short_rows(hip, torch_gpu, rows, block):
+    """Rows of up to 256 floats: four lanes per row (blocks of a multiple of 16) or one,
+    with ties everywhere (a 0.25 grid) and zeros of both signs, so the element kept must be
+    the first maximal one, bit for bit as the reference's scan."""
+    print(f"[reduce_max] rows={rows} block={block}", flush=True)
+    rng = np.random.default_rng(rows + block)
+    x = (np.round(rng.uniform(-1, 1, (rows, block)) * 4) / 4).astype(np.float32)
+    x[x == 0] = np.where(rng.random(int((x == 0).sum())) < 0.5, -0.0, 0.0).astype(np.float32)
+    got = device_postproc(hip, torch_gpu, "reduce_max", [x], b"", [(rows,)], [np.float32])[0]
+    np.testing.assert_array_equal(got.view(np.uint32), O.reduce_max(x, rows).reshape(rows).view(np.uint32))
+
+
 def test_reduce_gather_tile_detector_sizes(hip, torch_gpu):
     rng = np.random.default_rng(3)
     scores = np.round(rng.uniform(0, 1, (16, 8400, 80)), 3).astype(np.float32)
